@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Segment-LoRA shrink+expand benchmark on one MI355X.
+
+Workload (the headline configuration): Llama-3-8B q_proj 4096->4096, bf16,
+128 decode tokens, each its own segment; a 64-slot pool holding 32 rank-16
+adapters; slot per token uniform; x~N(0,1), A~N(0,1/4096), B~N(0,0.02),
+scaling 2.0, seed 1.  One step = one shrink+expand pass
+(``HipLoRABackend.apply_lora``) over the 128 tokens, inputs resident in HBM.
+
+Cold-cache protocol: the step rotates through ``--replicas`` independent
+copies of x / A pool / B pool / output (default 32 x ~18 MiB = 576 MiB, over
+twice the 256 MiB MALL), so weights come from HBM rather than the caches.
+
+Output: one JSON line.  ``value`` is the step's algorithmic HBM bytes divided
+by its time (GB/s); ``ms_per_step`` gives the latency.  ``roofline`` covers
+the dominant kernel, timed with HIP events on the launch stream; the
+``cpu_baseline`` is the oracle's per-segment PyTorch path on the host cores
+over a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "seg-LoRA shrink+expand µs & HBM GB/s, 8B shapes, 128 mixed-adapter decode"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--replicas", type=int, default=32)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-steps", type=int, default=500, help="steps of the per-kernel event timing")
+    return ap.parse_args()
+
+
+def cpu_cores() -> int:
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding of this path is design-only", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from multi_lora_amd import HipLoRABackend, synthetic
+    from multi_lora_amd.kernels.lora_ops import expand, shrink
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    host = synthetic.decode_q(device="cpu")
+    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+
+    reps = []
+    for _ in range(args.replicas):
+        reps.append((host.x.to(dev), host.a_stacks[0].to(dev), host.b_stacks[0].to(dev), host.base.to(dev)))
+    torch.cuda.synchronize()
+
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(meta)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(i):
+        x, a, b, out = reps[i % len(reps)]
+        be.apply_lora(x, a, b, out)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+
+    # Per-kernel durations: events bracketing each launch on the launch stream.
+    ks = args.kernel_steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3 * ks)]
+    mid = be.mid_buffer(host.tokens, host.a_stacks[0].shape[1], reps[0][0])
+    for i in range(ks):
+        x, a, b, out = reps[i % len(reps)]
+        ev[3 * i].record(stream)
+        shrink(x, [a], meta, mid, workspace=be.workspace)
+        ev[3 * i + 1].record(stream)
+        expand(mid, [b], meta, out, [0])
+        ev[3 * i + 2].record(stream)
+    torch.cuda.synchronize()
+    shrink_ms = sum(ev[3 * i].elapsed_time(ev[3 * i + 1]) for i in range(ks)) / ks
+    expand_ms = sum(ev[3 * i + 1].elapsed_time(ev[3 * i + 2]) for i in range(ks)) / ks
+
+    e = 2
+    used = sorted({s for s in host.seg_slots if host.slot_ranks[s] > 0})
+    r, in_dim, out_dim = 16, host.x.shape[1], host.b_stacks[0].shape[1]
+    shrink_bytes = host.x.numel() * e + len(used) * r * in_dim * e
+    expand_bytes = len(used) * out_dim * r * e + 2 * host.tokens * out_dim * e
+    total_bytes = synthetic.algorithmic_bytes(host)
+    assert total_bytes == shrink_bytes + expand_bytes
+    step_gbs = total_bytes / (ms_per_step * 1e-3) / 1e9
+
+    kernels = {
+        "shrink": {"us": shrink_ms * 1e3, "bytes": shrink_bytes, "GB/s": shrink_bytes / (shrink_ms * 1e-3) / 1e9},
+        "expand": {"us": expand_ms * 1e3, "bytes": expand_bytes, "GB/s": expand_bytes / (expand_ms * 1e-3) / 1e9},
+    }
+    dom_name = max(kernels, key=lambda k: kernels[k]["us"])
+    dom = kernels[dom_name]
+    traffic = None
+    tfile = ROOT / "profiles" / f"{dom_name}_decode_q_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(step_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "us_per_step": ms_per_step * 1e3,
+        "tokens_per_s": host.tokens / (ms_per_step * 1e-3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters",
+            "tokens": host.tokens,
+            "distinct_slots": len(used),
+            "algorithmic_bytes_per_step": total_bytes,
+            "replicas": args.replicas,
+            "path": "shrink + expand (two launches)",
+        },
+        "kernels": kernels,
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "hbm",
+            "achieved": round(dom["GB/s"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(host, total_bytes, args.cpu_seconds)
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(host, total_bytes: int, budget_s: float) -> dict:
+    """The oracle's per-segment PyTorch path on the host cores (bf16, same inputs)."""
+    import torch
+
+    from oracle.lora_ref import TorchLoRABackend
+
+    cores = cpu_cores()
+    torch.set_num_threads(cores)
+    be = TorchLoRABackend()
+    be.set_kernel_input_metadata(host.meta)
+    x, a, b = host.x, host.a_stacks[0], host.b_stacks[0]
+    out = host.base.clone()
+    for _ in range(3):
+        be.apply_lora(x, a, b, out)
+    times = []
+    start = time.perf_counter()
+    while time.perf_counter() - start < budget_s or len(times) < 20:
+        t = time.perf_counter_ns()
+        be.apply_lora(x, a, b, out)
+        times.append(time.perf_counter_ns() - t)
+        if len(times) >= 100000:
+            break
+    times.sort()
+    med_s = times[len(times) // 2] * 1e-9
+    return {
+        "value": round(total_bytes / med_s / 1e9, 4),
+        "unit": "GB/s",
+        "us_per_step": med_s * 1e6,
+        "cores": cores,
+        "kind": "port",
+        "cpu": cpu_model(),
+        "sample": f"median of {len(times)} full 128-token shrink+expand calls (bf16, host tensors)",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

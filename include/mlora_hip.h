@@ -1,0 +1,128 @@
+/*
+ * mlora_hip.h — C ABI of libmlora_hip.so, the MI355X (gfx950) segment-LoRA
+ * hot path: segment shrink, segment expand with residual accumulate (single
+ * and multi-slice), the slot-grouped decode apply, and fused RMSNorm.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are raw device pointers; strides are in ELEMENTS
+ *     and the innermost stride is always 1.  The library never allocates or
+ *     frees device memory: outputs and workspaces are owned by the caller.
+ *   - Every call is launch-only on `stream` (a hipStream_t passed as void*):
+ *     no host synchronisation, no allocation, so it can be captured into a
+ *     HIP graph.  Per-step values (segment bounds, slots, ranks, scalings) are
+ *     read from device memory; only `bs` and `max_len` size the grid.
+ *   - Return value: 0 = ok, < 0 = invalid argument (nothing launched),
+ *     > 0 = a hipError_t from the launch.  mlora_last_error() returns a
+ *     thread-local message for the last non-zero return on this thread.
+ *   - No C++ exception crosses this boundary.
+ */
+#ifndef MLORA_HIP_H_
+#define MLORA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types.  Data tensors (x, A, B, mid, out) share one dtype per call;
+ * scalings and RMSNorm weights carry their own. */
+enum mlora_dtype { MLORA_F32 = 0, MLORA_F16 = 1, MLORA_BF16 = 2 };
+
+/* Per-step segment table (device pointers, int32).  Mirrors
+ * KernelInputMetaData (multi_lora/batch_info.py:25-42):
+ *   seg_indptr[bs+1]      segment s owns rows [seg_indptr[s], seg_indptr[s+1])
+ *   weight_indices[bs]    pool slot of segment s
+ *   lora_ranks[num_slots] rank of each slot (0 = base model, no LoRA)
+ *   scalings[num_slots]   per-slot scaling, dtype `scal_dtype`
+ * A slot outside [0, num_slots) is treated as rank 0 (the segment is skipped),
+ * a rank above the tensor's r_max is clamped to r_max, and segment bounds are
+ * clamped to [0, num_rows) of the call, so an inconsistent table can produce
+ * wrong rows but never an access outside the caller's tensors. */
+typedef struct mlora_seg_meta {
+  const int32_t* seg_indptr;
+  const int32_t* weight_indices;
+  const int32_t* lora_ranks;
+  const void* scalings;
+  int32_t bs;
+  int32_t max_len;
+  int32_t num_slots;
+  int32_t scal_dtype;
+} mlora_seg_meta;
+
+/* One LoRA slice of a (possibly fused) projection.
+ *   a: A stack [num_slots, r_max, in_dim]   (a_slot_stride, a_row_stride)
+ *   b: B stack [num_slots, out_dim, r_max]  (b_slot_stride, b_row_stride)
+ *   out_col: first column of this slice in the output rows.
+ * The pool layout of multi_lora/pool.py:146-155 is exactly this. */
+typedef struct mlora_slice {
+  const void* a;
+  int64_t a_slot_stride;
+  int64_t a_row_stride;
+  const void* b;
+  int64_t b_slot_stride;
+  int64_t b_row_stride;
+  int32_t out_dim;
+  int32_t out_col;
+} mlora_slice;
+
+#define MLORA_MAX_SLICES 4
+
+/* ABI version of this header; bumped on any signature change. */
+int mlora_abi_version(void);
+
+/* Thread-local text of the last error returned on this thread ("" if none). */
+const char* mlora_last_error(void);
+
+/* Bytes of caller-owned workspace mlora_shrink needs for this launch shape
+ * (0 when none is needed, or when the shape is invalid — mlora_shrink then
+ * reports why).  The workspace starts with one int32 arrival counter per
+ * (segment, row tile); it must be zero-filled when first allocated, and every
+ * call leaves the counters zero again.  Calls that overlap in time (on
+ * different streams) need separate workspaces. */
+size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices,
+                                    int32_t bs, int32_t max_len, int32_t dtype);
+
+/* Segment shrink: mid[t, s*r_max + n] = sum_k x[t,k] * A_s[slot, n, k] for
+ * n < rank(slot) (fp32 accumulate, rounded once to `dtype`), zeros for
+ * rank <= n < r_max and for rank-0 segments.  Rows outside every segment
+ * are not written.
+ * Replaces sgemm_lora_a_fwd (multi_lora/kernels/sgemm_lora_a.py:186-274) and
+ * TritonLoRABackend.run_lora_a_sgemm (multi_lora/backend/triton_backend.py:34-45);
+ * n_slices > 1 is the fused-QKV / gate-up form (x read once).
+ * rank_mult implements the reference's stack_num (rank*stack_num rows of A
+ * are live, sgemm_lora_a.py:51); pass 1 otherwise. */
+int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                 const mlora_slice* slices, int32_t n_slices, int32_t r_max,
+                 int32_t rank_mult, void* mid, int64_t mid_row_stride,
+                 const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* Segment expand with residual accumulate, for every slice s:
+ *   out[t, out_col_s + n] = round(out[t, out_col_s + n]
+ *                                 + round(scaling[slot] * sum_{k<rank} mid[t, s*r_max + k] * B_s[slot, n, k]))
+ * fp32 accumulate; the scaled delta is rounded to `dtype` before the add,
+ * as the reference kernel does (multi_lora/kernels/sgemm_lora_b.py:84-89).
+ * Rank-0 segments leave `out` bit-identical.  `out` may be a strided view.
+ * Replaces sgemm_lora_b_fwd (multi_lora/kernels/sgemm_lora_b.py:156-237) and
+ * TritonLoRABackend.run_lora_b_sgemm (multi_lora/backend/triton_backend.py:47-61). */
+int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices,
+                 int32_t n_slices, int32_t r_max, void* out, int64_t out_row_stride,
+                 const mlora_seg_meta* meta, int32_t dtype, void* stream);
+
+/* Fused RMSNorm: y[row] = round(x[row] * rsqrt(mean(x[row]^2) + eps) * w) in
+ * fp32, one rounding.  Row `row` of x starts at
+ *   (row / inner) * x_stride_outer + (row % inner) * x_stride_inner,
+ * the two-level addressing of rmsnorm_fwd (multi_lora/kernels/rmsnorm.py:48-92);
+ * y is [rows, hidden] with row stride y_row_stride.  w has dtype w_dtype. */
+int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
+                  int64_t inner, const void* w, int32_t w_dtype, void* y,
+                  int64_t y_row_stride, int64_t rows, int32_t hidden, float eps,
+                  int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLORA_HIP_H_ */

@@ -1,0 +1,254 @@
+// extern "C" entry points of libmlora_hip.so (declared in include/mlora_hip.h).
+// Each entry point validates its arguments on the host, picks a launch
+// shape, and launches on the caller's stream.  Nothing here allocates,
+// frees or synchronises.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  std::snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return static_cast<int>(e);
+}
+
+constexpr int kBadArg = -1;
+constexpr int kUnsupported = -2;
+constexpr int kWorkspace = -3;
+
+int elem_bytes(int dtype) { return dtype == MLORA_F32 ? 4 : 2; }
+int vec_elems(int dtype) { return dtype == MLORA_F32 ? 4 : 8; }
+bool valid_dtype(int d) { return d == MLORA_F32 || d == MLORA_F16 || d == MLORA_BF16; }
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+int check_meta(const mlora_seg_meta* m) {
+  if (m == nullptr) return fail(kBadArg, "segment metadata is null");
+  if (m->bs < 0 || m->max_len < 0 || m->num_slots < 0)
+    return fail(kBadArg, "negative bs/max_len/num_slots (%d/%d/%d)", m->bs, m->max_len, m->num_slots);
+  if (!valid_dtype(m->scal_dtype)) return fail(kBadArg, "bad scalings dtype %d", m->scal_dtype);
+  if (m->bs > 0 && (m->seg_indptr == nullptr || m->weight_indices == nullptr || m->lora_ranks == nullptr))
+    return fail(kBadArg, "null segment table pointer");
+  return 0;
+}
+
+mlora::SegView seg_view(const mlora_seg_meta* m) {
+  mlora::SegView v;
+  v.indptr = m->seg_indptr;
+  v.widx = m->weight_indices;
+  v.ranks = m->lora_ranks;
+  v.scalings = m->scalings;
+  v.bs = m->bs;
+  v.num_slots = m->num_slots;
+  v.scal_dtype = m->scal_dtype;
+  return v;
+}
+
+mlora::SliceView slice_view(const mlora_slice& s) {
+  mlora::SliceView v;
+  v.a = s.a;
+  v.a_slot_stride = s.a_slot_stride;
+  v.a_row_stride = s.a_row_stride;
+  v.b = s.b;
+  v.b_slot_stride = s.b_slot_stride;
+  v.b_row_stride = s.b_row_stride;
+  v.out_dim = s.out_dim;
+  v.out_col = s.out_col;
+  return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlora_abi_version(void) { return 1; }
+
+const char* mlora_last_error(void) { return g_err; }
+
+size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t bs,
+                                    int32_t max_len, int32_t dtype) {
+  if (!valid_dtype(dtype)) return 0;
+  mlora::ShrinkPlan p;
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, bs, max_len, dtype, num_cus(), &p)) return 0;
+  return p.ws_bytes;
+}
+
+int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim, const mlora_slice* slices,
+                 int32_t n_slices, int32_t r_max, int32_t rank_mult, void* mid, int64_t mid_row_stride,
+                 const mlora_seg_meta* meta, int32_t dtype, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_err[0] = '\0';
+  if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
+  if (int rc = check_meta(meta)) return rc;
+  if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
+  if (slices == nullptr) return fail(kBadArg, "slices is null");
+  if (in_dim <= 0 || r_max <= 0 || rank_mult < 1 || num_rows < 0)
+    return fail(kBadArg, "in_dim %d, r_max %d, rank_mult %d, num_rows %d", in_dim, r_max, rank_mult, num_rows);
+  if (x_row_stride < in_dim) return fail(kBadArg, "x row stride %lld < in_dim %d", (long long)x_row_stride, in_dim);
+  if (mid_row_stride < static_cast<int64_t>(n_slices) * r_max)
+    return fail(kBadArg, "mid row stride %lld < n_slices*r_max %d", (long long)mid_row_stride, n_slices * r_max);
+  if (meta->bs == 0 || num_rows == 0) return 0;
+  if (x == nullptr || mid == nullptr) return fail(kBadArg, "x or mid is null");
+  for (int s = 0; s < n_slices; ++s) {
+    if (slices[s].a == nullptr) return fail(kBadArg, "slice %d: A is null", s);
+    if (slices[s].a_row_stride < in_dim || slices[s].a_slot_stride < static_cast<int64_t>(r_max) * slices[s].a_row_stride)
+      return fail(kBadArg, "slice %d: A strides (%lld, %lld) do not hold [r_max=%d, in=%d] rows", s,
+                  (long long)slices[s].a_slot_stride, (long long)slices[s].a_row_stride, r_max, in_dim);
+  }
+
+  mlora::ShrinkPlan plan;
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, meta->bs, meta->max_len, dtype, num_cus(), &plan))
+    return fail(kUnsupported, "shrink shape unsupported: r_max %d with %d slices (max 64 per slice with "
+                "several slices, 128 with one)", r_max, n_slices);
+  if (plan.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < plan.ws_bytes))
+    return fail(kWorkspace, "shrink workspace too small: need %zu bytes, got %zu", plan.ws_bytes, workspace_bytes);
+
+  const int vec = vec_elems(dtype);
+  const int eb = elem_bytes(dtype);
+  int align = 0;
+  if (al16(x) && x_row_stride % vec == 0 && in_dim % vec == 0) align |= mlora::kAlX;
+  bool ala = in_dim % vec == 0;
+  for (int s = 0; s < n_slices; ++s)
+    ala = ala && al16(slices[s].a) && slices[s].a_slot_stride % vec == 0 && slices[s].a_row_stride % vec == 0;
+  if (ala) align |= mlora::kAlA;
+  if (al16(mid) && mid_row_stride % vec == 0 && r_max % vec == 0) align |= mlora::kAlMid;
+  (void)eb;
+
+  mlora::ShrinkArgs args{};
+  args.x = x;
+  args.x_stride = x_row_stride;
+  args.rows = num_rows;
+  args.in_dim = in_dim;
+  for (int s = 0; s < n_slices; ++s) args.slices[s] = slice_view(slices[s]);
+  args.n_slices = n_slices;
+  args.r_max = r_max;
+  args.rank_mult = rank_mult;
+  args.mid = mid;
+  args.mid_stride = mid_row_stride;
+  args.meta = seg_view(meta);
+  args.align = align;
+  if (plan.ws_bytes > 0) {
+    const size_t tiles = static_cast<size_t>(meta->bs) * plan.m_tiles;
+    const size_t counter_bytes = (tiles * 4 + 255) / 256 * 256;
+    args.counters = static_cast<int*>(workspace);
+    args.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
+  }
+  hipError_t e = mlora::launch_shrink(plan, args, dtype, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "shrink launch");
+  return 0;
+}
+
+int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices, int32_t n_slices,
+                 int32_t r_max, void* out, int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype,
+                 void* stream) {
+  g_err[0] = '\0';
+  if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
+  if (int rc = check_meta(meta)) return rc;
+  if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
+  if (slices == nullptr) return fail(kBadArg, "slices is null");
+  if (r_max <= 0 || num_rows < 0) return fail(kBadArg, "r_max %d, num_rows %d", r_max, num_rows);
+  if (mid_row_stride < static_cast<int64_t>(n_slices) * r_max)
+    return fail(kBadArg, "mid row stride %lld < n_slices*r_max %d", (long long)mid_row_stride, n_slices * r_max);
+  if (meta->bs == 0 || num_rows == 0) return 0;
+  if (mid == nullptr || out == nullptr) return fail(kBadArg, "mid or out is null");
+
+  const int vec = vec_elems(dtype);
+  const int eb = elem_bytes(dtype);
+  mlora::ExpandArgs args{};
+  int tiles = 0;
+  bool alb = r_max % vec == 0;
+  bool alo = out_row_stride % vec == 0;
+  for (int s = 0; s < n_slices; ++s) {
+    const mlora_slice& sl = slices[s];
+    if (sl.b == nullptr) return fail(kBadArg, "slice %d: B is null", s);
+    if (sl.out_dim <= 0 || sl.out_col < 0) return fail(kBadArg, "slice %d: out_dim %d, out_col %d", s, sl.out_dim, sl.out_col);
+    if (sl.b_row_stride < r_max || sl.b_slot_stride < static_cast<int64_t>(sl.out_dim) * sl.b_row_stride)
+      return fail(kBadArg, "slice %d: B strides (%lld, %lld) do not hold [out=%d, r_max=%d] rows", s,
+                  (long long)sl.b_slot_stride, (long long)sl.b_row_stride, sl.out_dim, r_max);
+    args.slices[s] = slice_view(sl);
+    args.tile_base[s] = tiles;
+    tiles += mlora::cdiv(sl.out_dim, mlora::kExpandBN);
+    alb = alb && al16(sl.b) && sl.b_slot_stride % vec == 0 && sl.b_row_stride % vec == 0;
+    alo = alo && al16(static_cast<const char*>(out) + static_cast<int64_t>(sl.out_col) * eb) && sl.out_dim % vec == 0;
+  }
+  args.tile_base[n_slices] = tiles;
+  int align = 0;
+  if (alb) align |= mlora::kAlB;
+  if (alo) align |= mlora::kAlOut;
+  if (al16(mid) && mid_row_stride % vec == 0 && r_max % vec == 0) align |= mlora::kAlMid;
+
+  const int bm = (dtype == MLORA_F32 || meta->max_len <= 16) ? 16 : 64;
+  args.mid = mid;
+  args.mid_stride = mid_row_stride;
+  args.rows = num_rows;
+  args.n_slices = n_slices;
+  args.r_max = r_max;
+  args.out = out;
+  args.out_stride = out_row_stride;
+  args.meta = seg_view(meta);
+  args.m_tiles = mlora::cdiv(meta->max_len > 0 ? meta->max_len : 1, bm);
+  args.n_tiles = tiles;
+  args.align = align;
+  hipError_t e = mlora::launch_expand(bm, args, dtype, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "expand launch");
+  return 0;
+}
+
+int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner, int64_t inner, const void* w,
+                  int32_t w_dtype, void* y, int64_t y_row_stride, int64_t rows, int32_t hidden, float eps,
+                  int32_t dtype, void* stream) {
+  g_err[0] = '\0';
+  if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(kBadArg, "bad dtype %d / weight dtype %d", dtype, w_dtype);
+  if (hidden <= 0 || rows < 0 || inner < 1) return fail(kBadArg, "hidden %d, rows %lld, inner %lld", hidden, (long long)rows, (long long)inner);
+  if (y_row_stride < hidden) return fail(kBadArg, "y row stride %lld < hidden %d", (long long)y_row_stride, hidden);
+  if (rows == 0) return 0;
+  if (x == nullptr || w == nullptr || y == nullptr) return fail(kBadArg, "null x, w or y");
+  const int vec = vec_elems(dtype);
+  const int nch = mlora::cdiv(hidden, vec);
+  int tpr = 16;
+  while (tpr < 256 && tpr * 2 <= nch) tpr *= 2;
+  mlora::RmsArgs a{};
+  a.x = x;
+  a.x_stride_outer = x_stride_outer;
+  a.x_stride_inner = x_stride_inner;
+  a.inner = inner;
+  a.w = w;
+  a.w_dtype = w_dtype;
+  a.y = y;
+  a.y_stride = y_row_stride;
+  a.rows = rows;
+  a.hidden = hidden;
+  a.eps = eps;
+  a.tpr = tpr;
+  a.aligned = al16(x) && al16(y) && hidden % vec == 0 && x_stride_outer % vec == 0 &&
+              x_stride_inner % vec == 0 && y_row_stride % vec == 0;
+  hipError_t e = mlora::launch_rmsnorm(a, dtype, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+// Device-side building blocks shared by the gfx950 segment-LoRA kernels:
+// element traits (bf16 / fp16 / fp32 storage, fp32 math), 128-bit fragment
+// loads, and one K-step of a 16x16 MFMA tile.
+//
+// MFMA fragment convention used by every kernel here (wave64):
+//   lane l owns row (l & 15) of a 16-row operand and the 16-byte chunk
+//   k = k0 + (l >> 4) * VEC .. + VEC of that row, so one K-step covers
+//   KSTEP = 4 * VEC reduction elements.  Both operands of an MFMA are loaded
+//   with this same mapping, which makes the product independent of the order
+//   in which the hardware walks k inside a step.
+//   The 16x16 fp32 result lives as lane l -> column (l & 15),
+//   rows 4 * (l >> 4) + q for q = 0..3.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mlora_hip.h"
+
+namespace mlora {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- traits
+struct BF16 {
+  using raw_t = uint16_t;
+  static constexpr int VEC = 8;  // elements per 16-byte chunk
+  static constexpr int KSTEP = 32;
+  __device__ static __forceinline__ float to_f32(raw_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+  }
+  __device__ static __forceinline__ raw_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  }
+  __device__ static __forceinline__ f32x4 mma(f32x4 acc, u32x4 a, u32x4 b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  using raw_t = uint16_t;
+  static constexpr int VEC = 8;
+  static constexpr int KSTEP = 32;
+  __device__ static __forceinline__ float to_f32(raw_t v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+  }
+  __device__ static __forceinline__ raw_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  __device__ static __forceinline__ f32x4 mma(f32x4 acc, u32x4 a, u32x4 b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+  }
+};
+
+struct F32 {
+  using raw_t = float;
+  static constexpr int VEC = 4;
+  static constexpr int KSTEP = 16;
+  __device__ static __forceinline__ float to_f32(raw_t v) { return v; }
+  __device__ static __forceinline__ raw_t from_f32(float f) { return f; }
+  __device__ static __forceinline__ f32x4 mma(f32x4 acc, u32x4 a, u32x4 b) {
+    // Four 16x16x4 steps; element e of every lane's chunk feeds step e.
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(b[e]),
+                                                  acc, 0, 0, 0);
+    return acc;
+  }
+};
+
+// Element e (0..VEC-1) of a 16-byte chunk, as fp32.
+template <class T>
+__device__ __forceinline__ float chunk_elem(const u32x4& v, int e) {
+  if constexpr (sizeof(typename T::raw_t) == 2) {
+    uint32_t w = v[e >> 1];
+    return T::to_f32(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
+  } else {
+    return __uint_as_float(v[e]);
+  }
+}
+
+// Keep the first `valid` elements of a chunk, zero the rest.
+template <class T>
+__device__ __forceinline__ u32x4 chunk_keep(u32x4 v, int valid) {
+  if (valid >= T::VEC) return v;
+  if constexpr (sizeof(typename T::raw_t) == 2) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int e0 = 2 * w;
+      uint32_t keep = (e0 < valid ? 0x0000ffffu : 0u) | (e0 + 1 < valid ? 0xffff0000u : 0u);
+      v[w] &= keep;
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v[w] = (w < valid) ? v[w] : 0u;
+  }
+  return v;
+}
+
+__device__ __forceinline__ u32x4 zero_chunk() { return u32x4{0u, 0u, 0u, 0u}; }
+
+// 16-byte aligned global load / store of one chunk.
+template <class R>
+__device__ __forceinline__ u32x4 ld_chunk(const R* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+template <class R>
+__device__ __forceinline__ void st_chunk(R* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// Pack VEC fp32 values into one chunk of T.
+template <class T>
+__device__ __forceinline__ u32x4 pack_chunk(const float* f) {
+  u32x4 v;
+  if constexpr (sizeof(typename T::raw_t) == 2) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      v[w] = static_cast<uint32_t>(T::from_f32(f[2 * w])) |
+             (static_cast<uint32_t>(T::from_f32(f[2 * w + 1])) << 16);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v[w] = __float_as_uint(f[w]);
+  }
+  return v;
+}
+
+__device__ __forceinline__ float load_scaling(const void* p, int idx, int dtype) {
+  if (dtype == MLORA_BF16) return BF16::to_f32(static_cast<const uint16_t*>(p)[idx]);
+  if (dtype == MLORA_F16) return F16::to_f32(static_cast<const uint16_t*>(p)[idx]);
+  return static_cast<const float*>(p)[idx];
+}
+
+// Kernel-side view of the per-step segment table.
+struct SegView {
+  const int32_t* indptr;
+  const int32_t* widx;
+  const int32_t* ranks;
+  const void* scalings;
+  int bs;
+  int num_slots;
+  int scal_dtype;
+};
+
+// Slot and live rank of segment `seg`; rank 0 for a slot outside the pool.
+__device__ __forceinline__ void seg_slot_rank(const SegView& m, int seg, int r_max, int rank_mult,
+                                              int* slot, int* rank) {
+  int s = m.widx[seg];
+  int r = 0;
+  if (s >= 0 && s < m.num_slots) r = m.ranks[s] * rank_mult;
+  if (r < 0) r = 0;
+  if (r > r_max) r = r_max;
+  *slot = s;
+  *rank = r;
+}
+
+struct SliceView {
+  const void* a;
+  int64_t a_slot_stride, a_row_stride;
+  const void* b;
+  int64_t b_slot_stride, b_row_stride;
+  int out_dim;
+  int out_col;
+};
+
+constexpr int kMaxSlices = MLORA_MAX_SLICES;
+
+}  // namespace mlora

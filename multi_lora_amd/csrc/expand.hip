@@ -1,0 +1,169 @@
+// Segment expand with residual accumulate on gfx950:
+//   out[t, out_col_s + n] += round(scaling[slot] * sum_{k<rank} mid[t, s*r_max+k] * B_s[slot, n, k])
+//
+// Behaviour follows the reference's segment GEMM for LoRA B
+// (multi_lora/kernels/sgemm_lora_b.py:10-90 tiled form, :93-153 decode form):
+// fp32 accumulation over k < rank, multiply by the slot's scaling, round the
+// delta to the storage type, add the existing output in fp32 and round again.
+// Rank-0 segments return before touching `out`.  Unlike the reference's tiled
+// form (whose store mask omits the column bound, sgemm_lora_b.py:362-364),
+// every access here is bounded by out_dim, so any output width is safe.
+//
+// Work decomposition (256 threads = 4 wave64s per workgroup):
+//   workgroup = (segment, tile of BM tokens, tile of 256 output columns of one slice)
+//   wave      = 64 output columns (4 MFMA n-blocks) x all BM tokens
+//   MFMA tile = D[n][t] += B[n][k] * mid[t][k]   (16 columns x 16 tokens)
+// The output tile is prefetched into registers before the MFMA loop so its
+// HBM latency overlaps the B/mid reads; the rounded deltas go through LDS so
+// the read-modify-write of `out` is done with row-contiguous 16-byte chunks.
+#include "kernels.h"
+#include "loads.h"
+
+namespace mlora {
+
+namespace {
+
+template <class T, int BM>
+__global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
+  using raw = typename T::raw_t;
+  constexpr int VEC = T::VEC;
+  constexpr int KSTEP = T::KSTEP;
+  constexpr int BN = kExpandBN;
+  constexpr int TB = BM / 16;
+  constexpr int LDS_STRIDE = BN + VEC;      // padded row, keeps 16-byte alignment
+  constexpr int CPR = BN / VEC;             // chunks per tile row
+  constexpr int RPT = BM * CPR / 256;       // chunks per thread in the RMW
+  __shared__ __attribute__((aligned(16))) raw delta[BM * LDS_STRIDE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int bid = blockIdx.x;
+  const int nt_g = bid % a.n_tiles;
+  const int tile = bid / a.n_tiles;
+  const int seg = tile / a.m_tiles;
+  const int mt = tile - seg * a.m_tiles;
+
+  const int start = max(a.meta.indptr[seg], 0);
+  const int end = min(a.meta.indptr[seg + 1], a.rows);
+  const int row0 = start + mt * BM;
+  if (row0 >= end) return;
+  int slot, rank;
+  seg_slot_rank(a.meta, seg, a.r_max, 1, &slot, &rank);
+  if (rank == 0) return;
+
+  int s = 0;
+  while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
+  const int n0 = (nt_g - a.tile_base[s]) * BN;
+  const int out_dim = a.slices[s].out_dim;
+  const float scale = load_scaling(a.meta.scalings, slot, a.meta.scal_dtype);
+  const bool alo = (a.align & kAlOut) != 0;
+  const bool alb = (a.align & kAlB) != 0;
+  const bool alm = (a.align & kAlMid) != 0;
+
+  raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
+
+  // Prefetch this thread's share of the output tile.
+  u32x4 ov[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / CPR;
+    const int n = n0 + (c - row * CPR) * VEC;
+    const int t = row0 + row;
+    ov[i] = (t < end) ? load_chunk<T>(out + static_cast<int64_t>(t) * a.out_stride + n, out_dim - n, alo)
+                      : zero_chunk();
+  }
+
+  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
+  const raw* mid = static_cast<const raw*>(a.mid) + s * a.r_max;
+  const int64_t brs = a.slices[s].b_row_stride;
+
+  f32x4 acc[4][TB];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < rank; k0 += KSTEP) {
+    const int kk = k0 + g * VEC;
+    const int valid = rank - kk;
+    u32x4 yv[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = row0 + tb * 16 + r16;
+      yv[tb] = (t < end) ? load_chunk<T>(mid + static_cast<int64_t>(t) * a.mid_stride + kk, valid, alm)
+                         : zero_chunk();
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = n0 + (wave * 4 + nb) * 16 + r16;
+      const u32x4 bv = (n < out_dim) ? load_chunk<T>(B + static_cast<int64_t>(n) * brs + kk, valid, alb)
+                                     : zero_chunk();
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = T::mma(acc[nb][tb], bv, yv[tb]);
+    }
+  }
+
+  // Scaled, rounded deltas -> LDS as [token][column].
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int nl = (wave * 4 + nb) * 16 + 4 * g;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int tl = tb * 16 + r16;
+      const f32x4 v = acc[nb][tb];
+      raw* p = delta + tl * LDS_STRIDE + nl;
+      if constexpr (sizeof(raw) == 2) {
+        uint2 w;
+        w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) |
+              (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
+        w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) |
+              (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
+        *reinterpret_cast<uint2*>(p) = w;
+      } else {
+        *reinterpret_cast<f32x4*>(p) = v * scale;
+      }
+    }
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / CPR;
+    const int cc = c - row * CPR;
+    const int n = n0 + cc * VEC;
+    const int t = row0 + row;
+    if (t < end && n < out_dim) {
+      const u32x4 d = *reinterpret_cast<const u32x4*>(delta + row * LDS_STRIDE + cc * VEC);
+      float f[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(ov[i], e) + chunk_elem<T>(d, e);
+      store_chunk<T>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n, alo);
+    }
+  }
+}
+
+template <class T, int BM>
+hipError_t launch_t(const ExpandArgs& args, hipStream_t stream) {
+  const int64_t blocks = static_cast<int64_t>(args.meta.bs) * args.m_tiles * args.n_tiles;
+  if (blocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL((expand_kernel<T, BM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_expand(int bm, ExpandArgs args, int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case MLORA_BF16: return bm == 16 ? launch_t<BF16, 16>(args, stream) : launch_t<BF16, 64>(args, stream);
+    case MLORA_F16: return bm == 16 ? launch_t<F16, 16>(args, stream) : launch_t<F16, 64>(args, stream);
+    default: return launch_t<F32, 16>(args, stream);
+  }
+}
+
+}  // namespace mlora

@@ -1,0 +1,259 @@
+"""Host entry points of the HIP segment-LoRA kernels.
+
+Same names, argument meaning and asserts as the reference's kernel entry
+points, so its kernel-level tests read the same:
+
+* ``sgemm_lora_a_fwd(x, weights, meta, output, stack_num=1)`` —
+  multi_lora/kernels/sgemm_lora_a.py:186-274;
+* ``sgemm_lora_b_fwd(x, weights, meta, base_output=None)`` —
+  multi_lora/kernels/sgemm_lora_b.py:156-237.
+
+Multi-slice forms (x read once for fused QKV / gate-up; one launch for all
+slices of the output) have no reference counterpart and are additive:
+``sgemm_lora_a_multi_fwd`` and ``sgemm_lora_b_multi_fwd``.
+
+Every call launches on the current HIP stream of the tensors' device and
+never synchronises.  There is no CPU path: CPU tensors raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from .. import _ffi
+from ..batch_info import KernelInputMetaData
+
+_WORKSPACES: Dict[Tuple[str, int], torch.Tensor] = {}
+
+
+class Workspace:
+    """Caller-owned scratch for the split-K shrink (zero-initialised, grown on demand).
+
+    The library leaves its counter words zero after every call, so one
+    workspace can serve any number of sequential launches on one stream.
+    Launches that overlap on different streams need separate workspaces.
+    """
+
+    def __init__(self) -> None:
+        self.buf: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int, device: torch.device) -> Tuple[int, int]:
+        if nbytes <= 0:
+            return 0, 0
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            size = max(nbytes, 1 << 20)
+            self.buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        return self.buf.data_ptr(), self.buf.numel()
+
+
+def _default_workspace(device: torch.device) -> Workspace:
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        ws = _WORKSPACES[key] = Workspace()
+    return ws
+
+
+def _require_gpu(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{what} must be on a ROCm GPU (got {t.device}); the HIP path has no CPU fallback")
+
+
+def _int32(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if t.dtype == torch.int32 and t.device == device and t.is_contiguous():
+        return t
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def seg_meta(meta: KernelInputMetaData, device: torch.device, num_slots: int) -> Tuple[_ffi.SegMeta, list]:
+    """Build the C segment table; returns it and the tensors it points into.
+
+    ``num_slots`` is the slot dimension of the stacks; slots at or past it
+    (or past ``lora_ranks``) are treated as rank 0 by the kernels.
+    """
+    if meta is None:
+        raise RuntimeError("kernel_input_metadata not set; call set_kernel_input_metadata first")
+    bs = int(meta.bs)
+    indptr = _int32(meta.seg_indptr, device)
+    widx = _int32(meta.weight_indices, device)
+    ranks = _int32(meta.lora_ranks, device)
+    scal = meta.scalings
+    if scal.dtype not in (torch.float32, torch.float16, torch.bfloat16) or scal.device != device:
+        scal = scal.to(device=device, dtype=torch.float32)
+    scal = scal.contiguous()
+    if indptr.numel() < bs + 1 or widx.numel() < bs:
+        raise ValueError(f"metadata holds {widx.numel()} segments / {indptr.numel()} offsets for bs={bs}")
+    if scal.numel() < ranks.numel():
+        raise ValueError(f"scalings ({scal.numel()}) shorter than lora_ranks ({ranks.numel()})")
+    m = _ffi.SegMeta(
+        indptr.data_ptr(),
+        widx.data_ptr(),
+        ranks.data_ptr(),
+        scal.data_ptr(),
+        bs,
+        int(meta.max_len),
+        min(ranks.numel(), int(num_slots)),
+        _ffi.dtype_code(scal.dtype),
+    )
+    return m, [indptr, widx, ranks, scal]
+
+
+def _slices(a_stacks: Sequence[Optional[torch.Tensor]], b_stacks: Sequence[Optional[torch.Tensor]],
+            out_cols: Sequence[int]) -> _ffi.SliceArray:
+    arr = _ffi.SliceArray()
+    for i, (a, b) in enumerate(zip(a_stacks, b_stacks)):
+        s = arr[i]
+        if a is not None:
+            s.a, s.a_slot_stride, s.a_row_stride = a.data_ptr(), a.stride(0), a.stride(1)
+        if b is not None:
+            s.b, s.b_slot_stride, s.b_row_stride = b.data_ptr(), b.stride(0), b.stride(1)
+            s.out_dim = b.shape[1]
+        s.out_col = int(out_cols[i])
+    return arr
+
+
+def _check_stack(w: torch.Tensor, what: str, dtype: torch.dtype, device: torch.device) -> None:
+    if w.dim() != 3:
+        raise ValueError(f"{what} must be 3-D [slots, rows, cols], got {tuple(w.shape)}")
+    if w.stride(2) != 1:
+        raise ValueError(f"{what} innermost dimension must be contiguous")
+    if w.dtype != dtype or w.device != device:
+        raise ValueError(f"{what} is {w.dtype} on {w.device}; expected {dtype} on {device}")
+
+
+def shrink(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], meta: KernelInputMetaData, output: torch.Tensor,
+           *, stack_num: int = 1, workspace: Optional[Workspace] = None) -> torch.Tensor:
+    """``output[t, s*r_max + n] = x[t] . A_s[slot(t), n]`` for every slice ``s``."""
+    _require_gpu(x, "x")
+    dev = x.device
+    n = len(a_stacks)
+    if not 1 <= n <= _ffi.MAX_SLICES:
+        raise ValueError(f"1..{_ffi.MAX_SLICES} A stacks expected, got {n}")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D [S, in] tensor with contiguous rows")
+    in_dim = x.shape[1]
+    r_max = a_stacks[0].shape[1]
+    for i, a in enumerate(a_stacks):
+        _check_stack(a, f"A[{i}]", x.dtype, dev)
+        if a.shape[1] != r_max or a.shape[2] != in_dim:
+            raise ValueError(f"A[{i}] {tuple(a.shape)} does not match r_max={r_max}, in={in_dim}")
+    if output.dim() != 2 or output.stride(1) != 1 or output.dtype != x.dtype or output.device != dev:
+        raise ValueError("output must be a 2-D row-contiguous tensor of x's dtype and device")
+    if output.shape[0] < x.shape[0] or output.shape[1] < n * r_max:
+        raise ValueError(f"output {tuple(output.shape)} smaller than [{x.shape[0]}, {n * r_max}]")
+    m, keep = seg_meta(meta, dev, min(a.shape[0] for a in a_stacks))
+    lib = _ffi.lib()
+    dt = _ffi.dtype_code(x.dtype)
+    ws = workspace or _default_workspace(dev)
+    need = lib.mlora_shrink_workspace_bytes(in_dim, r_max, n, m.bs, m.max_len, dt)
+    ws_ptr, ws_bytes = ws.get(need, dev)
+    sl = _slices(a_stacks, [None] * n, [0] * n)
+    rc = lib.mlora_shrink(
+        x.data_ptr(), x.stride(0), x.shape[0], in_dim, sl, n, r_max, int(stack_num), output.data_ptr(), output.stride(0),
+        ctypes.byref(m), dt, ws_ptr, ws_bytes, _ffi.stream_ptr(dev),
+    )
+    _ffi.check(rc, "mlora_shrink")
+    del keep
+    return output
+
+
+def expand(mid: torch.Tensor, b_stacks: Sequence[torch.Tensor], meta: KernelInputMetaData, out: torch.Tensor,
+           out_cols: Sequence[int]) -> torch.Tensor:
+    """``out[t, out_cols[s] + n] += scaling * mid[t, s*r_max:(s*r_max+rank)] . B_s[slot(t), n, :rank]``."""
+    _require_gpu(mid, "mid")
+    dev = mid.device
+    n = len(b_stacks)
+    if not 1 <= n <= _ffi.MAX_SLICES:
+        raise ValueError(f"1..{_ffi.MAX_SLICES} B stacks expected, got {n}")
+    if mid.dim() != 2 or mid.stride(1) != 1:
+        raise ValueError("mid must be a 2-D [S, n*r_max] tensor with contiguous rows")
+    r_max = b_stacks[0].shape[2]
+    for i, b in enumerate(b_stacks):
+        _check_stack(b, f"B[{i}]", mid.dtype, dev)
+        if b.shape[2] != r_max:
+            raise ValueError(f"B[{i}] {tuple(b.shape)} does not match r_max={r_max}")
+        if out_cols[i] < 0 or out_cols[i] + b.shape[1] > out.shape[1]:
+            raise ValueError(f"slice {i}: columns [{out_cols[i]}, {out_cols[i] + b.shape[1]}) outside output "
+                             f"of width {out.shape[1]}")
+    if mid.shape[1] < n * r_max:
+        raise ValueError(f"mid has {mid.shape[1]} columns, need {n * r_max}")
+    if out.dim() != 2 or out.stride(1) != 1 or out.dtype != mid.dtype or out.device != dev:
+        raise ValueError("output must be a 2-D row-contiguous tensor of mid's dtype and device")
+    if out.shape[0] < mid.shape[0]:
+        raise ValueError(f"output has {out.shape[0]} rows, mid has {mid.shape[0]}")
+    m, keep = seg_meta(meta, dev, min(b.shape[0] for b in b_stacks))
+    sl = _slices([None] * n, b_stacks, out_cols)
+    rc = _ffi.lib().mlora_expand(
+        mid.data_ptr(), mid.stride(0), mid.shape[0], sl, n, r_max, out.data_ptr(), out.stride(0), ctypes.byref(m),
+        _ffi.dtype_code(mid.dtype), _ffi.stream_ptr(dev),
+    )
+    _ffi.check(rc, "mlora_expand")
+    del keep
+    return out
+
+
+def sgemm_lora_a_fwd(x: torch.Tensor, weights: torch.Tensor, kernel_input_metadata: KernelInputMetaData,
+                     output: torch.Tensor, stack_num: int = 1) -> torch.Tensor:
+    """LoRA A segment GEMM: ``output[:S, :r_max]`` = per-segment ``x @ A[slot, :r].T``.
+
+    x: ``[S, in]``, weights: ``[K, r_max, in]``, output: a caller-owned
+    ``[>=S, >=r_max]`` buffer; returns the ``[S, r_max]`` view written.
+    """
+    assert x.is_contiguous()
+    assert weights.is_contiguous()
+    assert len(x.shape) == 2
+    assert len(weights.shape) == 3
+    assert x.shape[-1] == weights.shape[-1]
+    rows, r_max = x.shape[0], weights.shape[-2]
+    out = output[:rows, :r_max]
+    shrink(x, [weights], kernel_input_metadata, out, stack_num=stack_num)
+    return out
+
+
+def sgemm_lora_b_fwd(x: torch.Tensor, weights: torch.Tensor, kernel_input_metadata: KernelInputMetaData,
+                     base_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """LoRA B segment GEMM with fused residual: ``base_output += scaling * (mid @ B[slot, :, :r].T)``.
+
+    x (mid): ``[S, r_max]``, weights: ``[K, out, r_max]``.  With
+    ``base_output=None`` a zero output is allocated and returned.
+    """
+    assert x.is_contiguous()
+    assert weights.is_contiguous()
+    assert len(x.shape) == 2
+    assert len(weights.shape) == 3
+    assert x.shape[-1] == weights.shape[-1]
+    rows, out_dim = x.shape[0], weights.shape[-2]
+    if base_output is None:
+        base_output = torch.zeros((rows, out_dim), device=x.device, dtype=x.dtype)
+    if base_output.dim() != 2 or base_output.shape[1] != out_dim:
+        raise ValueError(f"base_output {tuple(base_output.shape)} is not [S, {out_dim}]")
+    expand(x, [weights], kernel_input_metadata, base_output, [0])
+    return base_output
+
+
+def sgemm_lora_a_multi_fwd(x: torch.Tensor, weights: List[torch.Tensor], kernel_input_metadata: KernelInputMetaData,
+                           output: torch.Tensor) -> torch.Tensor:
+    """Shrink for several slices at once; returns ``output[:S, :n*r_max]`` (slice s at columns s*r_max)."""
+    rows, r_max = x.shape[0], weights[0].shape[-2]
+    out = output[:rows, : len(weights) * r_max]
+    shrink(x.contiguous(), [w.contiguous() for w in weights], kernel_input_metadata, out)
+    return out
+
+
+def sgemm_lora_b_multi_fwd(x: torch.Tensor, weights: List[torch.Tensor], kernel_input_metadata: KernelInputMetaData,
+                           base_output: torch.Tensor, col_offsets: Optional[Sequence[int]] = None) -> torch.Tensor:
+    """Expand for several slices in one launch; slice s adds into columns starting at ``col_offsets[s]``.
+
+    ``col_offsets`` defaults to the running sum of the slices' output widths
+    (the q|k|v or gate|up concatenation).
+    """
+    if col_offsets is None:
+        col_offsets, c = [], 0
+        for w in weights:
+            col_offsets.append(c)
+            c += w.shape[1]
+    expand(x.contiguous(), [w.contiguous() for w in weights], kernel_input_metadata, base_output, list(col_offsets))
+    return base_output

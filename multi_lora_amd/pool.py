@@ -1,0 +1,292 @@
+"""Adapter slot pool: K device slots per LoRA module, filled on demand.
+
+Mirrors the reference's ``LoRAMemoryPool`` (multi_lora/pool.py:325-473) and
+its slot tensors (pool.py:97-155):
+
+* per module key, ``A[key]`` is ``[K, max_lora_rank, in]`` and ``B[key]`` is
+  ``[K, out, max_lora_rank]`` in the model dtype, zero-initialised; the
+  kernels read only the first ``rank`` rows of A / columns of B of a slot;
+* ``name_to_slot`` / ``slot_names`` / ``_slot_rank_scaling`` map adapters to
+  slots; ``None`` is the base model (rank 0, scaling 0, no weights);
+* a full pool evicts an adapter that is not in the current batch, chosen by
+  the eviction policy; the base slot goes last (pool.py:443-473).
+
+Upload.  The first time an adapter is loaded its weights are packed once
+into a flat host bank (pinned when the pool is on a GPU): all A blocks, then
+all B blocks, at offsets fixed per rank (the same packing the reference uses,
+pool.py:23-58).  A reload is then one contiguous H2D copy of the bank into a
+device staging row, on a side stream ordered after the compute stream, and a
+device-side scatter of each block into its slot.  The compute stream waits
+for the upload before the next forward.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Iterable, List, Optional, Tuple
+
+import torch
+
+from .batch_info import BatchLoRAInfo
+from .eviction import EvictionPolicy
+from .weights import AdapterWeights
+
+LoraName = Optional[str]
+
+# Adapters staged per device round trip; bounds the staging buffer.
+_BANK_CHUNK = 4
+
+
+class _RankPlan:
+    """Flat bank layout for one rank: every key's A block, then every B block."""
+
+    def __init__(self, rank: int, keys: List[str], dims: Dict[str, Tuple[int, int]]):
+        self.rank = rank
+        self.keys = keys
+        self.a_off: Dict[str, int] = {}
+        self.b_off: Dict[str, int] = {}
+        self.a_shape: Dict[str, Tuple[int, int]] = {}
+        self.b_shape: Dict[str, Tuple[int, int]] = {}
+        cursor = 0
+        for key in keys:
+            in_dim = dims[key][0]
+            self.a_off[key], self.a_shape[key] = cursor, (rank, in_dim)
+            cursor += rank * in_dim
+        for key in keys:
+            out_dim = dims[key][1]
+            self.b_off[key], self.b_shape[key] = cursor, (out_dim, rank)
+            cursor += out_dim * rank
+        self.total = cursor
+
+
+class _GpuBuffers:
+    """The slot tensors of every module key, plus the upload machinery."""
+
+    def __init__(self, max_loras_per_batch: int, max_lora_rank: int, device: torch.device, dtype: torch.dtype):
+        self.max_loras_per_batch = max_loras_per_batch
+        self.max_lora_rank = max_lora_rank
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.A: Dict[str, torch.Tensor] = {}
+        self.B: Dict[str, torch.Tensor] = {}
+        self._plans: Dict[int, _RankPlan] = {}
+        self._plan_keys: Optional[tuple] = None
+        self._banks: Dict[int, tuple] = {}
+        self._stage: Optional[torch.Tensor] = None
+        self._copy_stream = None
+        self._load_event = None
+        # Release the per-module host tensors once an adapter is packed into
+        # its bank, so host memory holds one copy of the weights.
+        self.release_modules = True
+
+    # -- allocation ---------------------------------------------------------
+    def ensure(self, weights: AdapterWeights) -> None:
+        """Allocate zeroed slot tensors for module keys seen for the first time."""
+        for key, (a, b) in weights.modules.items():
+            if key in self.A:
+                continue
+            in_dim, out_dim = int(a.shape[1]), int(b.shape[0])
+            k, r = self.max_loras_per_batch, self.max_lora_rank
+            self.A[key] = torch.zeros((k, r, in_dim), device=self.device, dtype=self.dtype)
+            self.B[key] = torch.zeros((k, out_dim, r), device=self.device, dtype=self.dtype)
+
+    def get(self, key: str) -> Tuple[torch.Tensor, torch.Tensor]:
+        if key not in self.A:
+            raise KeyError(f"module {key!r} not in pool")
+        return self.A[key], self.B[key]
+
+    # -- upload -------------------------------------------------------------
+    def write_many(self, pairs: List[Tuple[int, AdapterWeights]]) -> None:
+        """Load adapters into their slots: ``pairs = [(slot, weights), ...]``."""
+        if not pairs:
+            return
+        if self.device.type != "cuda":
+            self._load(pairs, non_blocking=False)
+            return
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(device=self.device)
+            self._load_event = torch.cuda.Event()
+        # Slots being overwritten may still be read by queued compute work.
+        self._copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self._copy_stream):
+            self._load(pairs, non_blocking=True)
+        self._load_event.record(self._copy_stream)
+
+    def wait_load(self) -> None:
+        """Make the compute stream wait for the last upload."""
+        if self._load_event is not None:
+            torch.cuda.current_stream(self.device).wait_event(self._load_event)
+
+    def _plan_for(self, rank: int) -> _RankPlan:
+        keys = tuple(self.A)
+        if keys != self._plan_keys:
+            self._plans.clear()
+            self._banks.clear()
+            self._plan_keys = keys
+        plan = self._plans.get(rank)
+        if plan is None:
+            dims = {k: (int(self.A[k].shape[2]), int(self.B[k].shape[1])) for k in keys}
+            plan = _RankPlan(rank, list(keys), dims)
+            self._plans[rank] = plan
+        return plan
+
+    def _bank_for(self, weights: AdapterWeights, plan: _RankPlan) -> torch.Tensor:
+        """The adapter's packed host bank; built on first use and cached."""
+        hit = self._banks.get(id(weights))
+        if hit is not None and hit[0] is weights and hit[1] == plan.rank:
+            return hit[2]
+        if weights.flattened:
+            raise RuntimeError(
+                f"adapter (rank {plan.rank}) was packed and released before the pool's module set "
+                f"changed to {len(plan.keys)} keys; its bank cannot be rebuilt"
+            )
+        bank = torch.zeros(plan.total, dtype=self.dtype, pin_memory=self.device.type == "cuda")
+        for key in plan.keys:
+            mod = weights.modules.get(key)
+            if mod is None:
+                continue  # missing module: its blocks stay zero
+            a, b = mod
+            ao, bo = plan.a_off[key], plan.b_off[key]
+            bank[ao : ao + a.numel()].copy_(a.reshape(-1))
+            bank[bo : bo + b.numel()].copy_(b.reshape(-1))
+        self._banks[id(weights)] = (weights, plan.rank, bank)
+        if self.release_modules:
+            weights.modules = {}
+            weights.flattened = True
+        return bank
+
+    def _stage_rows(self, total: int) -> torch.Tensor:
+        need = _BANK_CHUNK * total
+        if self._stage is None or self._stage.numel() < need:
+            self._stage = torch.empty(need, device=self.device, dtype=self.dtype)
+        return self._stage[:need].view(_BANK_CHUNK, total)
+
+    def _load(self, pairs: List[Tuple[int, AdapterWeights]], non_blocking: bool) -> None:
+        by_rank: Dict[int, List[Tuple[int, AdapterWeights]]] = {}
+        for slot, w in pairs:
+            by_rank.setdefault(int(w.rank), []).append((slot, w))
+        for rank, group in by_rank.items():
+            plan = self._plan_for(rank)
+            if self.device.type == "cuda":
+                stage = self._stage_rows(plan.total)
+                stage.record_stream(torch.cuda.current_stream(self.device))
+            for c0 in range(0, len(group), _BANK_CHUNK):
+                chunk = group[c0 : c0 + _BANK_CHUNK]
+                for i, (slot, w) in enumerate(chunk):
+                    bank = self._bank_for(w, plan)
+                    src = bank
+                    if self.device.type == "cuda":
+                        stage[i].copy_(bank, non_blocking=non_blocking)
+                        src = stage[i]
+                    self._scatter(src, slot, plan)
+
+    def _scatter(self, flat: torch.Tensor, slot: int, plan: _RankPlan) -> None:
+        """Copy one adapter's packed blocks into slot ``slot`` (first ``rank`` rows / columns)."""
+        r = plan.rank
+        for key in plan.keys:
+            ao, bo = plan.a_off[key], plan.b_off[key]
+            a_shape, b_shape = plan.a_shape[key], plan.b_shape[key]
+            self.A[key][slot, :r].copy_(flat[ao : ao + r * a_shape[1]].view(a_shape))
+            self.B[key][slot, :, :r].copy_(flat[bo : bo + b_shape[0] * r].view(b_shape))
+
+
+class LoRAMemoryPool:
+    """K device slots; each holds nothing, the base model, or one adapter."""
+
+    def __init__(
+        self,
+        max_loras_per_batch: int,
+        max_lora_rank: int,
+        device: torch.device,
+        dtype: torch.dtype = torch.float16,
+        eviction_policy: str = "lru",
+    ) -> None:
+        self.max_loras_per_batch = max_loras_per_batch
+        self.max_lora_rank = max_lora_rank
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.eviction_policy = EvictionPolicy(eviction_policy)
+        self.name_to_slot: Dict[LoraName, int] = {}
+        self.slot_names: Dict[int, LoraName] = {}
+        self._slot_rank_scaling: Dict[int, Tuple[int, float]] = {}
+        self.buffers = _GpuBuffers(max_loras_per_batch, max_lora_rank, self.device, dtype)
+
+    def get_slot_id(self, name: LoraName) -> int:
+        if name not in self.name_to_slot:
+            raise KeyError(f"lora {name!r} not resident in pool")
+        return self.name_to_slot[name]
+
+    def get_module_buffers(self, module_key: str) -> Tuple[torch.Tensor, torch.Tensor]:
+        return self.buffers.get(module_key)
+
+    def get_slot_weights(self, slot: int, module_key: str) -> Tuple[torch.Tensor, torch.Tensor]:
+        a, b = self.buffers.get(module_key)
+        return a[slot], b[slot]
+
+    def ensure_buffers(self, weights: AdapterWeights) -> None:
+        self.buffers.ensure(weights)
+
+    def prepare_lora_batch(
+        self, lora_names: Iterable[LoraName], *, weight_store: Dict[LoraName, AdapterWeights]
+    ) -> None:
+        """Make every adapter of the batch resident, evicting others as needed.
+
+        Adapters are visited in the iteration order of ``lora_names`` (pass an
+        ordered, de-duplicated list for a reproducible slot assignment).  All
+        uploads of the batch are issued together, then the compute stream is
+        ordered after them.
+        """
+        wanted = list(dict.fromkeys(lora_names))
+        keep = set(wanted)
+        for name in wanted:
+            self.eviction_policy.mark_used(name)
+        pairs: List[Tuple[int, AdapterWeights]] = []
+        for name in wanted:
+            if name in self.name_to_slot:
+                continue
+            slot = self._alloc_slot(keep)
+            self.name_to_slot[name] = slot
+            self.slot_names[slot] = name
+            if name is None:
+                self._slot_rank_scaling[slot] = (0, 0.0)
+                continue
+            weights = weight_store[name]
+            if weights.rank > self.max_lora_rank:
+                raise ValueError(f"adapter {name!r} rank {weights.rank} > max_lora_rank {self.max_lora_rank}")
+            self.buffers.ensure(weights)
+            self._slot_rank_scaling[slot] = (int(weights.rank), float(weights.scaling))
+            pairs.append((slot, weights))
+        self.buffers.write_many(pairs)
+        self.buffers.wait_load()
+
+    def build_batch_info(self, lora_names: List[LoraName]) -> BatchLoRAInfo:
+        """Slot per segment; rank and scaling per slot (empty slots: 0, 0.0)."""
+        k = self.max_loras_per_batch
+        ranks = [0] * k
+        scalings = [0.0] * k
+        for slot, (rank, scaling) in self._slot_rank_scaling.items():
+            ranks[slot] = rank
+            scalings[slot] = scaling
+        return BatchLoRAInfo(
+            weight_indices=[self.get_slot_id(n) for n in lora_names],
+            lora_ranks=ranks,
+            scalings=scalings,
+        )
+
+    def _alloc_slot(self, keep_names: set) -> int:
+        """An empty slot if any (lowest index), else the slot of an evicted adapter."""
+        for slot in range(self.max_loras_per_batch):
+            if slot not in self.slot_names:
+                return slot
+        candidates = {n for n in self.slot_names.values() if n not in keep_names and n is not None}
+        if not candidates:
+            base_free = any(n is None and n not in keep_names for n in self.slot_names.values())
+            if not base_free:
+                raise ValueError("no evictable slot: batch needs more adapters than max_loras_per_batch")
+            candidates = {None}
+        victim = self.eviction_policy.select_victim(candidates)
+        slot = self.name_to_slot.pop(victim)
+        self.eviction_policy.remove(victim)
+        del self.slot_names[slot]
+        self._slot_rank_scaling.pop(slot, None)
+        return slot
+

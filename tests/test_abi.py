@@ -1,0 +1,93 @@
+"""The C ABI library loads and exports what include/mlora_hip.h declares (CPU).
+
+No compute call is made here: argument-validation paths return before any
+HIP call, so they run without a GPU.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from multi_lora_amd import _ffi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(mlora_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_built():
+    assert _ffi.LIB_PATH.exists(), "run `python -m multi_lora_amd.build` first"
+
+
+def test_exports_every_declared_symbol():
+    lib = _ffi.lib()
+    declared = declared_functions()
+    assert declared, "no declarations parsed"
+    assert set(declared) == set(_ffi.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_empty_error():
+    lib = _ffi.lib()
+    assert lib.mlora_abi_version() == _ffi.ABI_VERSION
+    assert isinstance(lib.mlora_last_error(), bytes)
+
+
+def test_single_hip_runtime_mapped():
+    import torch  # noqa: F401  (torch maps its HIP runtime first)
+
+    _ffi.lib()
+    assert len(_ffi.hip_runtimes_mapped()) <= 1, _ffi.hip_runtimes_mapped()
+
+
+def _meta(bs=1, max_len=1, scal_dtype=_ffi.MLORA_BF16):
+    return _ffi.SegMeta(None, None, None, None, bs, max_len, 4, scal_dtype)
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    lib = _ffi.lib()
+    sl = _ffi.SliceArray()
+    m = _meta()
+    # bad dtype
+    rc = lib.mlora_shrink(None, 16, 4, 16, sl, 1, 8, 1, None, 8, ctypes.byref(m), 9, None, 0, None)
+    assert rc < 0 and b"dtype" in lib.mlora_last_error()
+    # null segment table with bs > 0
+    rc = lib.mlora_shrink(None, 16, 4, 16, sl, 1, 8, 1, None, 8, ctypes.byref(m), _ffi.MLORA_BF16, None, 0, None)
+    assert rc < 0 and b"null" in lib.mlora_last_error()
+    # Non-null placeholder addresses: validation fails before anything is read.
+    fake = _ffi.SegMeta(256, 512, 768, 1024, 1, 1, 4, _ffi.MLORA_BF16)
+    # too many slices
+    rc = lib.mlora_expand(None, 8, 4, sl, 5, 8, None, 16, ctypes.byref(fake), _ffi.MLORA_BF16, None)
+    assert rc < 0 and b"n_slices" in lib.mlora_last_error()
+    # mid row too narrow for the slices
+    rc = lib.mlora_expand(None, 4, 4, sl, 1, 8, None, 16, ctypes.byref(fake), _ffi.MLORA_BF16, None)
+    assert rc < 0 and b"mid row stride" in lib.mlora_last_error()
+    # unsupported rank width with several slices
+    rc = lib.mlora_shrink(4096, 64, 4, 64, sl, 2, 256, 1, 8192, 512, ctypes.byref(fake), _ffi.MLORA_BF16, None, 0, None)
+    assert rc < 0
+    # rmsnorm: bad hidden
+    rc = lib.mlora_rmsnorm(None, 0, 0, 1, None, 0, None, 0, 4, 0, 1e-6, 2, None)
+    assert rc < 0
+    # bs == 0 is a no-op success, with nothing launched
+    empty = _meta(bs=0, max_len=0)
+    rc = lib.mlora_shrink(None, 16, 4, 16, sl, 1, 8, 1, None, 8, ctypes.byref(empty), _ffi.MLORA_BF16, None, 0, None)
+    assert rc == 0
+
+
+def test_errors_map_to_reference_exception_types():
+    with pytest.raises(ValueError):
+        _ffi.lib()  # loads
+        m = _meta()
+        rc = _ffi.lib().mlora_expand(None, 4, 4, _ffi.SliceArray(), 1, 8, None, 16, ctypes.byref(m), _ffi.MLORA_BF16, None)
+        _ffi.check(rc, "mlora_expand")

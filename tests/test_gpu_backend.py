@@ -1,0 +1,134 @@
+"""Backend, layer and manager level on the GPU, against the oracle backend.
+
+Mirrors the reference's full-model checks (multi_lora/tests/test_triton_sgemm.py:74-88,
+test_phase4_backend.py:54-109, test_fused_qkv.py:90-103) with models and
+adapters built in the test instead of loaded through PEFT.
+"""
+
+import os
+
+import pytest
+import torch
+import torch.nn as nn
+
+from multi_lora_amd import AdapterWeights, HipLoRABackend, LinearWithLoRA, MultiLoRAManager, fuse_qkv_projections
+from multi_lora_amd import synthetic
+from oracle.lora_ref import TorchLoRABackend, apply_f64, lora_delta
+from tests.gpu_helpers import assert_tol_f64
+
+pytestmark = pytest.mark.gpu
+
+
+def _cpu_meta(meta):
+    return type(meta)(bs=meta.bs, seg_lens=meta.seg_lens.cpu(), seg_indptr=meta.seg_indptr.cpu(),
+                      weight_indices=meta.weight_indices.cpu(), lora_ranks=meta.lora_ranks.cpu(),
+                      scalings=meta.scalings.cpu(), max_len=meta.max_len)
+
+
+def test_backend_apply_lora_matches_oracle_backend(dev):
+    wl = synthetic.decode_q(device=dev, tokens=64, in_dim=2048, out=2048, n_slots=16, n_adapters=9, rank=16, seed=8)
+    hip = HipLoRABackend()
+    hip.set_kernel_input_metadata(wl.meta)
+    got = hip.apply_lora(wl.x, wl.a_stacks[0], wl.b_stacks[0], wl.clone_base())
+    torch.cuda.synchronize()
+    ref = TorchLoRABackend()
+    ref.set_kernel_input_metadata(_cpu_meta(wl.meta))
+    want = ref.apply_lora(wl.x.cpu(), wl.a_stacks[0].cpu(), wl.b_stacks[0].cpu(), wl.base.cpu().clone())
+    torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
+    assert_tol_f64(got.cpu(), apply_f64(wl.x.cpu(), [wl.a_stacks[0].cpu()], [wl.b_stacks[0].cpu()],
+                                        _cpu_meta(wl.meta), wl.base.cpu()))
+
+
+def test_apply_lora_multi_equals_per_slice_bitwise(dev):
+    wl = synthetic.decode_qkv(device=dev, tokens=48, hidden=1024, outs=[1024, 256, 256], n_slots=32, n_adapters=20,
+                              rank=32, seed=12)
+    hip = HipLoRABackend()
+    hip.set_kernel_input_metadata(wl.meta)
+    fused = wl.clone_base()
+    hip.apply_lora_multi(wl.x, wl.a_stacks, wl.b_stacks, fused, wl.col_offsets)
+    sep = wl.clone_base()
+    for a, b, c0 in zip(wl.a_stacks, wl.b_stacks, wl.col_offsets):
+        hip.apply_lora(wl.x, a, b, sep[:, c0:c0 + b.shape[1]])
+    torch.cuda.synchronize()
+    assert torch.equal(fused, sep)
+
+
+class ToyLM(nn.Module):
+    def __init__(self, d_in=64, d_out=128):
+        super().__init__()
+        self.lin = nn.Linear(d_in, d_out)
+
+    def forward(self, x):
+        return self.lin(x)
+
+
+def _adapter(seed, rank, d_in, d_out, scaling):
+    g = torch.Generator().manual_seed(seed)
+    return AdapterWeights(rank=rank, scaling=scaling,
+                          modules={"lin": (torch.randn(rank, d_in, generator=g) * 0.1,
+                                           torch.randn(d_out, rank, generator=g) * 0.1)})
+
+
+def test_manager_forward_matches_rowwise_reference(dev):
+    """multi_lora/tests/test_triton_sgemm.py:74-88 pattern, checked row by row like test_phase4_backend.py:54-82."""
+    torch.manual_seed(0)
+    model = ToyLM().to(dev, torch.bfloat16)
+    base = ToyLM().to(dev, torch.bfloat16)
+    base.load_state_dict(model.state_dict())
+    adapters = {"a": _adapter(1, 8, 64, 128, 2.0), "b": _adapter(2, 8, 64, 128, 2.0)}
+    raw = {k: (v.modules["lin"][0].clone(), v.modules["lin"][1].clone()) for k, v in adapters.items()}
+    mgr = MultiLoRAManager.from_adapters(model, adapters, max_loras_per_batch=3, max_lora_rank=16, lora_backend="hip")
+    x = torch.randn(8, 64, device=dev, dtype=torch.bfloat16)
+    pattern = ["a", None, "b", "a", None, "b", "a", "b"]
+    y = mgr.forward_with_lora(x=x, lora_names=pattern, seq_lens=[1] * len(pattern))
+    torch.cuda.synchronize()
+    yb = base(x).float().cpu()
+    for i, name in enumerate(pattern):
+        want = yb[i].double()
+        if name is not None:
+            a, b = raw[name]
+            a = a.to(torch.bfloat16).double()
+            b = b.to(torch.bfloat16).double()
+            want = want + lora_delta(x[i:i + 1].cpu().double(), a, b, 2.0, rank=8)[0]
+        torch.testing.assert_close(y[i].double().cpu(), want, atol=3e-2, rtol=2e-2)
+    # repeated forward is stable (test_phase4_backend.py:98-109), here bit-for-bit
+    y2 = mgr.forward_with_lora(x=x, lora_names=pattern, seq_lens=[1] * len(pattern))
+    assert torch.equal(y, y2)
+    # grouping adjacent rows: ["a","a","b","b"] becomes two segments
+    meta = mgr.build_kernel_input_metadata(["a", "a", "b", "b"], seq_lens=[])
+    assert meta.bs == 2 and meta.max_len == 2
+
+
+def test_fused_qkv_with_hip_multi_slice_equals_separate(dev):
+    """multi_lora/tests/test_fused_qkv.py:90-103 on the GPU: fused base GEMM + one multi-slice LoRA."""
+    prefix = "model.layers.0.self_attn."
+    dims = {"q_proj": 256, "k_proj": 64, "v_proj": 64}
+    torch.manual_seed(0)
+    wrappers = {prefix + n: LinearWithLoRA(nn.Linear(128, d, bias=False).to(dev, torch.bfloat16))
+                for n, d in dims.items()}
+    hip = HipLoRABackend()
+    wl = synthetic.decode_q(device=dev, tokens=16, in_dim=128, out=256, n_slots=4, n_adapters=3, rank=8, seed=3)
+    hip.set_kernel_input_metadata(wl.meta)
+    g = torch.Generator().manual_seed(4)
+    for n, d in dims.items():
+        a = (torch.randn(4, 8, 128, generator=g) * 0.1).to(dev, torch.bfloat16)
+        b = (torch.randn(4, d, 8, generator=g) * 0.1).to(dev, torch.bfloat16)
+        wrappers[prefix + n].set_lora_info(hip, a, b)
+    x = torch.randn(16, 1, 128, device=dev, dtype=torch.bfloat16)
+    order = [prefix + n for n in dims]
+    ref = [wrappers[k](x).clone() for k in order]
+    assert fuse_qkv_projections(wrappers) == 1
+    got = [wrappers[k](x) for k in order]
+    torch.cuda.synchronize()
+    for g_, r_ in zip(got, ref):
+        # F.linear on the fused weight may tile differently from three GEMMs;
+        # the LoRA part is identical, so the results agree to bf16 rounding.
+        torch.testing.assert_close(g_, r_, atol=2e-2, rtol=1e-2)
+
+
+def test_no_cpu_fallback():
+    hip = HipLoRABackend()
+    wl = synthetic.cpu_small()
+    hip.set_kernel_input_metadata(wl.meta)
+    with pytest.raises(RuntimeError):
+        hip.apply_lora(wl.x, wl.a_stacks[0], wl.b_stacks[0], wl.clone_base())

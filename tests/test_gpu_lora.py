@@ -1,0 +1,265 @@
+"""HIP shrink/expand parity against the oracle (GPU).
+
+Every case runs the library's kernels through the C ABI (via the
+``sgemm_lora_*`` entry points) on seeded inputs and compares with
+* the float64 closed form (``apply_f64``) at the path's tolerance, and
+* the oracle's restatement of the kernels' rounding sequence
+  (``apply_kernel_numerics``) to within one unit in the last place.
+"""
+
+import pytest
+import torch
+
+from multi_lora_amd import synthetic
+from multi_lora_amd.kernels import (
+    sgemm_lora_a_fwd,
+    sgemm_lora_a_multi_fwd,
+    sgemm_lora_b_fwd,
+    sgemm_lora_b_multi_fwd,
+)
+from multi_lora_amd.synthetic import make_meta
+from oracle.lora_ref import TorchLoRABackend, apply_f64, apply_kernel_numerics
+from tests.gpu_helpers import assert_tol_f64, assert_ulp_close
+
+pytestmark = pytest.mark.gpu
+
+
+def run_hip(x, a_stacks, b_stacks, meta, base, cols=None):
+    """Shrink then expand on the GPU; returns (mid, out) on the CPU."""
+    r_max = a_stacks[0].shape[1]
+    mid = torch.full((x.shape[0], len(a_stacks) * r_max), float("nan"), dtype=x.dtype, device=x.device)
+    out = base.clone()
+    if len(a_stacks) == 1:
+        sgemm_lora_a_fwd(x, a_stacks[0], meta, mid)
+        sgemm_lora_b_fwd(mid, b_stacks[0], meta, base_output=out)
+    else:
+        sgemm_lora_a_multi_fwd(x, a_stacks, meta, mid)
+        sgemm_lora_b_multi_fwd(mid, b_stacks, meta, out, cols)
+    torch.cuda.synchronize()
+    return mid.cpu(), out.cpu()
+
+
+def cpu_meta(meta):
+    return type(meta)(
+        bs=meta.bs, seg_lens=meta.seg_lens.cpu(), seg_indptr=meta.seg_indptr.cpu(),
+        weight_indices=meta.weight_indices.cpu(), lora_ranks=meta.lora_ranks.cpu(),
+        scalings=meta.scalings.cpu(), max_len=meta.max_len)
+
+
+def check_workload(wl, tight=True):
+    cols = wl.col_offsets
+    mid, out = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base, cols)
+    cm = cpu_meta(wl.meta)
+    xs, As, Bs, base = wl.x.cpu(), [a.cpu() for a in wl.a_stacks], [b.cpu() for b in wl.b_stacks], wl.base.cpu()
+    want64 = apply_f64(xs, As, Bs, cm, base, cols)
+    assert_tol_f64(out, want64, f"{wl.name} vs float64")
+    if tight:
+        kmid, kout = apply_kernel_numerics(xs, As, Bs, cm, base, cols)
+        valid = torch.zeros(mid.shape[0], dtype=torch.bool)
+        for s, n in enumerate(wl.seg_lens):
+            st = sum(wl.seg_lens[:s])
+            valid[st:st + n] = True
+        assert_ulp_close(mid[valid], kmid[valid], what=f"{wl.name} mid")
+        assert_ulp_close(out, kout, what=f"{wl.name} out")
+    return mid, out
+
+
+def test_decode_q_llama8b_shape(dev):
+    """Decode q_proj 4096->4096 bf16, 128 single-token segments, 32 of 64 slots at rank 16."""
+    check_workload(synthetic.decode_q(device=dev))
+
+
+def test_cpu_small_config_in_fp32_on_gpu(dev):
+    """The fp32 1024->1024 case: segments [5,17,42] -> slots [2,0,3], rank 8."""
+    wl = synthetic.cpu_small(device=dev)
+    mid, out = check_workload(wl)
+    # also equal (to fp32 rounding) to the reference's per-segment PyTorch path
+    be = TorchLoRABackend()
+    be.set_kernel_input_metadata(cpu_meta(wl.meta))
+    ref = be.apply_lora(wl.x.cpu(), wl.a_stacks[0].cpu(), wl.b_stacks[0].cpu(), wl.base.cpu().clone())
+    torch.testing.assert_close(out, ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_decode_q_dtypes_small(dev, dtype):
+    check_workload(synthetic.decode_q(device=dev, dtype=dtype, tokens=40, in_dim=512, out=768, n_slots=8,
+                                      n_adapters=5, rank=16, seed=11))
+
+
+def test_decode_qkv_multi_slice(dev):
+    """Fused q|k|v [4096,1024,1024], 256 tokens over 128 rank-32 adapters in a 256-slot pool."""
+    check_workload(synthetic.decode_qkv(device=dev))
+
+
+def test_prefill_gate_up_reduced(dev):
+    wl = synthetic.prefill_mlp(device=dev, part="gate_up", n_seg=4, min_len=17, max_len=200, hidden=1024,
+                               inter=2816, seed=21)
+    check_workload(wl)
+
+
+def test_prefill_down_reduced(dev):
+    wl = synthetic.prefill_mlp(device=dev, part="down", n_seg=5, min_len=1, max_len=150, hidden=768,
+                               inter=3584, seed=22)
+    check_workload(wl)
+
+
+@pytest.mark.parametrize("part", ["gate_up", "down"])
+def test_prefill_full_size_sampled_rows(dev, part):
+    """Full prefill MLP shapes (~4k tokens); a sample of rows checked against float64."""
+    wl = synthetic.prefill_mlp(device=dev, part=part)
+    mid, out = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base, wl.col_offsets)
+    g = torch.Generator().manual_seed(0)
+    rows = torch.randint(0, wl.tokens, (48,), generator=g).tolist()
+    starts = [sum(wl.seg_lens[:i]) for i in range(len(wl.seg_lens))]
+    x, base = wl.x.cpu().double(), wl.base.cpu().double()
+    for t in rows:
+        seg = max(i for i, s in enumerate(starts) if s <= t)
+        slot = wl.seg_slots[seg]
+        r = wl.slot_ranks[slot]
+        want = base[t].clone()
+        for a, b, c0 in zip(wl.a_stacks, wl.b_stacks, wl.col_offsets):
+            y = x[t] @ a[slot, :r].cpu().double().T
+            want[c0:c0 + b.shape[1]] += 2.0 * (y @ b[slot, :, :r].cpu().double().T)
+        torch.testing.assert_close(out[t].double(), want, atol=2e-2, rtol=1e-2, msg=f"row {t}")
+
+
+@pytest.mark.parametrize("rows_per_adapter", [2, 8])
+def test_grouped_matches_rowwise_decode(dev, rows_per_adapter):
+    """multi_lora/tests/test_grouped_rows.py:92-134 on the HIP kernels."""
+    dt = torch.bfloat16
+    torch.manual_seed(0)
+    in_dim, out_dim, max_rank = 96, 256, 64
+    ranks, scalings = [8, 16], [1.0, 2.0]
+    a_stack = (torch.randn(2, max_rank, in_dim) * 0.1).to(dev, dt)
+    b_stack = (torch.randn(2, out_dim, max_rank) * 0.1).to(dev, dt)
+    rows = rows_per_adapter * 2
+    x = torch.randn(rows, in_dim).to(dev, dt)
+    widx_rows = [0] * rows_per_adapter + [1] * rows_per_adapter
+    base = torch.randn(rows, out_dim).to(dev, dt)
+    meta_group = make_meta([rows_per_adapter] * 2, [0, 1], ranks, scalings, dev, torch.float32)
+    meta_row = make_meta([1] * rows, widx_rows, ranks, scalings, dev, torch.float32)
+    assert meta_group.max_len > 1 and meta_row.max_len == 1
+    outs = {}
+    for tag, meta in (("group", meta_group), ("row", meta_row)):
+        mid = torch.zeros(rows, max_rank, device=dev, dtype=dt)
+        mid = sgemm_lora_a_fwd(x, a_stack, meta, mid)
+        y = sgemm_lora_b_fwd(mid, b_stack, meta, base_output=base.clone())
+        outs[tag] = (mid, y)
+    for tag in ("group", "row"):
+        mid = outs[tag][0]
+        for row, slot in enumerate(widx_rows):
+            assert (mid[row, ranks[slot]:] == 0).all(), (tag, row)
+    ref = apply_f64(x.cpu(), [a_stack.cpu()], [b_stack.cpu()], cpu_meta(meta_row), base.cpu())
+    torch.testing.assert_close(outs["group"][1].cpu(), outs["row"][1].cpu(), rtol=2e-2, atol=2e-2)
+    assert_tol_f64(outs["group"][1].cpu(), ref)
+    assert_tol_f64(outs["row"][1].cpu(), ref)
+    # grouping changes only the tiling, never the per-row arithmetic
+    assert torch.equal(outs["group"][1], outs["row"][1])
+
+
+def test_grouped_matches_rowwise_prefill(dev):
+    """multi_lora/tests/test_grouped_rows.py:137-165 on the HIP kernels."""
+    dt = torch.bfloat16
+    torch.manual_seed(1)
+    in_dim, out_dim, max_rank = 96, 256, 64
+    ranks, scalings = [8, 16], [1.0, 2.0]
+    a_stack = (torch.randn(2, max_rank, in_dim) * 0.1).to(dev, dt)
+    b_stack = (torch.randn(2, out_dim, max_rank) * 0.1).to(dev, dt)
+    row_lens = [5, 5, 3, 3]
+    total = sum(row_lens)
+    x = torch.randn(total, in_dim).to(dev, dt)
+    base = torch.randn(total, out_dim).to(dev, dt)
+    meta_group = make_meta([10, 6], [0, 1], ranks, scalings, dev, torch.float32)
+    meta_row = make_meta(row_lens, [0, 0, 1, 1], ranks, scalings, dev, torch.float32)
+    outs = {}
+    for tag, meta in (("group", meta_group), ("row", meta_row)):
+        mid = torch.zeros(total, max_rank, device=dev, dtype=dt)
+        mid = sgemm_lora_a_fwd(x, a_stack, meta, mid)
+        outs[tag] = sgemm_lora_b_fwd(mid, b_stack, meta, base_output=base.clone())
+    torch.testing.assert_close(outs["group"], outs["row"], rtol=2e-2, atol=2e-2)
+    assert torch.equal(outs["group"], outs["row"])
+
+
+@pytest.mark.parametrize(
+    "in_dim,out_dim,r_max,ranks",
+    [
+        (100, 1000, 16, [16, 5, 0]),     # unaligned rows, out not a multiple of 256, odd rank
+        (16, 32, 8, [4, 8, 1]),          # tiny toy shapes
+        (64, 128, 16, [8, 16, 3]),
+        (4104, 520, 24, [24, 17, 9]),    # r_max not a power of two, in just past 4096
+        (14336, 384, 64, [64, 48, 33]),  # long reduction -> split-K path
+    ],
+)
+def test_odd_shapes_and_stale_tails(dev, in_dim, out_dim, r_max, ranks):
+    """Stale data past each slot's rank (as a reused slot holds) must never be read."""
+    g = torch.Generator().manual_seed(in_dim + out_dim)
+    n_slots = len(ranks)
+    lens = [3, 1, 0, 7, 2, 19]
+    slots = [0, 1, 2, 1, 0, 2]
+    x = torch.randn(sum(lens), in_dim, generator=g).bfloat16()
+    a = (torch.randn(n_slots, r_max, in_dim, generator=g) * in_dim ** -0.5).bfloat16()
+    b = (torch.randn(n_slots, out_dim, r_max, generator=g) * 0.05).bfloat16()
+    base = torch.randn(sum(lens), out_dim, generator=g).bfloat16()
+    scal = [1.5, 0.75, 2.0]
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", torch.bfloat16)
+    want = apply_f64(x, [a], [b], meta_cpu, base)
+    kmid, kout = apply_kernel_numerics(x, [a], [b], meta_cpu, base)
+    mid, out = run_hip(x.to(dev), [a.to(dev)], [b.to(dev)], make_meta(lens, slots, ranks, scal, dev, torch.bfloat16),
+                       base.to(dev))
+    assert_tol_f64(out, want)
+    assert_ulp_close(out, kout, what="out")
+    live = torch.zeros(sum(lens), dtype=torch.bool)
+    st = 0
+    for n, s in zip(lens, slots):
+        live[st:st + n] = True
+        st += n
+    assert_ulp_close(mid[live], kmid[live], what="mid")
+
+
+def test_rank0_empty_and_out_of_range_slots_leave_output_untouched(dev):
+    dt = torch.bfloat16
+    lens = [2, 0, 3, 1, 4]
+    slots = [1, 0, 7, -1, 1]  # slot 1 has rank 0; 7 and -1 are outside the 3-slot pool
+    ranks = [8, 0, 8]
+    x = torch.randn(sum(lens), 64).to(dev, dt)
+    a = torch.randn(3, 8, 64).to(dev, dt)
+    b = torch.randn(3, 256, 8).to(dev, dt)
+    base = torch.randn(sum(lens), 256).to(dev, dt)
+    meta = make_meta(lens, slots, ranks, [1.0, 1.0, 1.0], dev, dt)
+    mid, out = run_hip(x, [a], [b], meta, base)
+    assert torch.equal(out, base.cpu())
+    assert torch.count_nonzero(mid) == 0  # every row in a segment is written, and all are zero
+
+
+def test_strided_output_view(dev):
+    """Output is a column slice of a wider row (the fused-QKV case, row stride 6144)."""
+    dt = torch.bfloat16
+    wl = synthetic.decode_q(device=dev, tokens=24, in_dim=1024, out=1024, n_slots=8, n_adapters=6, rank=16, seed=5)
+    wide = torch.randn(24, 6144, generator=torch.Generator().manual_seed(9)).to(dev, dt)
+    view = wide[:, 4096:5120]
+    assert not view.is_contiguous()
+    before = wide.clone()
+    mid = torch.empty(24, 16, device=dev, dtype=dt)
+    sgemm_lora_a_fwd(wl.x, wl.a_stacks[0], wl.meta, mid)
+    sgemm_lora_b_fwd(mid, wl.b_stacks[0], wl.meta, base_output=view)
+    torch.cuda.synchronize()
+    cm = cpu_meta(wl.meta)
+    want = apply_f64(wl.x.cpu(), [wl.a_stacks[0].cpu()], [wl.b_stacks[0].cpu()], cm, before[:, 4096:5120].cpu())
+    assert_tol_f64(wide[:, 4096:5120].cpu(), want)
+    assert torch.equal(wide[:, :4096], before[:, :4096])
+    assert torch.equal(wide[:, 5120:], before[:, 5120:])
+
+
+def test_deterministic_and_workspace_counters_reset(dev):
+    from multi_lora_amd.kernels.lora_ops import _default_workspace
+
+    wl = synthetic.prefill_mlp(device=dev, part="down", n_seg=3, min_len=5, max_len=40, hidden=512, inter=14336,
+                               seed=4)
+    first = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
+    for _ in range(3):
+        again = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
+        assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
+    ws = _default_workspace(dev).buf
+    assert ws is not None, "this shape is expected to take the split-K path"
+    # counters: one int32 per (segment, row tile), at the start of the workspace
+    assert torch.count_nonzero(ws[: 4 * wl.meta.bs]) == 0

@@ -77,11 +77,11 @@ const char* mlora_last_error(void);
 
 /* Bytes of caller-owned workspace mlora_shrink needs for this launch shape
  * (0 when none is needed, or when the shape is invalid — mlora_shrink then
- * reports why).  The workspace starts with one int32 arrival counter per
- * (segment, row tile); it must be zero-filled when first allocated, and every
- * call leaves the counters zero again.  Calls that overlap in time (on
- * different streams) need separate workspaces. */
-size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices,
+ * reports why).  When the reduction is split over workgroups the workspace
+ * holds their fp32 sums, which a second launch adds in a fixed order; its
+ * contents need no initialisation.  Calls that overlap in time (on different
+ * streams) need separate workspaces. */
+size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
                                     int32_t bs, int32_t max_len, int32_t dtype);
 
 /* Segment shrink: mid[t, s*r_max + n] = sum_k x[t,k] * A_s[slot, n, k] for
@@ -110,6 +110,33 @@ int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t 
 int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices,
                  int32_t n_slices, int32_t r_max, void* out, int64_t out_row_stride,
                  const mlora_seg_meta* meta, int32_t dtype, void* stream);
+
+/* Bytes of workspace mlora_apply_grouped needs (fp32 sums of each 256-wide
+ * K chunk for every row and slice); 0 when the shape is not eligible. */
+size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
+                                     int32_t dtype);
+
+/* Slot-grouped shrink + expand for decode-shaped batches:
+ *   out[t, out_col_s + n] += round(scaling * round(x[t] . A_s[slot,:rank]) . B_s[slot, n, :rank])
+ * with the same roundings as mlora_shrink followed by mlora_expand; no `mid`
+ * is materialised.  Workgroups are indexed by (slot, chunk) and gather the
+ * rows of their slot from the segment table, so each referenced adapter's A
+ * and B are read from HBM once per call however many rows use it.
+ * `mode`: 1 = single launch (each workgroup of a slot repeats the slot's
+ * reduction; A shared through one XCD's L2; no workspace), 2 = two launches
+ * (K-chunk sums through the workspace), 0 = pick (currently two launches,
+ * the faster of the two on MI355X at the decode shapes measured).
+ * `phases` (two-launch mode only): 1 = shrink half (leaves its sums in the
+ * workspace), 2 = expand half (consumes them), 3 = both (normal use).
+ * Requirements (else -2 and nothing launched): bf16 or fp16; r_max <= 64 and
+ * a multiple of 8; 16-byte aligned rows of x, A, B and out (pointers, strides,
+ * in_dim and every out_dim multiples of 8 elements).
+ * Replaces LoRABackend.apply_lora (multi_lora/backend/base.py:60-89) with the
+ * reference's decode kernels (sgemm_lora_a.py:118-183, sgemm_lora_b.py:93-153). */
+int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                        const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                        int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                        size_t workspace_bytes, int32_t mode, int32_t phases, void* stream);
 
 /* Fused RMSNorm: y[row] = round(x[row] * rsqrt(mean(x[row]^2) + eps) * w) in
  * fp32, one rounding.  Row `row` of x starts at

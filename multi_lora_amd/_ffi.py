@@ -31,6 +31,8 @@ EXPORTS = (
     "mlora_shrink_workspace_bytes",
     "mlora_shrink",
     "mlora_expand",
+    "mlora_grouped_workspace_bytes",
+    "mlora_apply_grouped",
     "mlora_rmsnorm",
 )
 
@@ -74,7 +76,13 @@ _vp, _i32, _i64, _sz, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ct
 _SIGNATURES = {
     "mlora_abi_version": (ctypes.c_int, []),
     "mlora_last_error": (ctypes.c_char_p, []),
-    "mlora_shrink_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "mlora_shrink_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "mlora_grouped_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "mlora_apply_grouped": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _i32, ctypes.POINTER(Slice), _i32, _i32, _vp, _i64, ctypes.POINTER(SegMeta), _i32, _vp,
+         _sz, _i32, _i32, _vp],
+    ),
     "mlora_shrink": (
         ctypes.c_int,
         [_vp, _i64, _i32, _i32, ctypes.POINTER(Slice), _i32, _i32, _i32, _vp, _i64, ctypes.POINTER(SegMeta), _i32, _vp,

@@ -14,7 +14,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from ..kernels.lora_ops import Workspace, expand, shrink
+from ..kernels.lora_ops import GROUPED_MAX_LEN, Workspace, apply_grouped, expand, shrink
 from .base import LoRABackend
 
 
@@ -47,6 +47,17 @@ class HipLoRABackend(LoRABackend):
             base_output = torch.zeros((x.shape[0], weights.shape[-2]), device=x.device, dtype=x.dtype)
         return expand(x.contiguous(), [weights.contiguous()], meta, base_output, [0])
 
+    def apply_lora(
+        self, x: torch.Tensor, a_stack: torch.Tensor, b_stack: torch.Tensor, base_output: torch.Tensor
+    ) -> torch.Tensor:
+        """Add each segment's LoRA delta into ``base_output`` (in place) and return it.
+
+        Decode-shaped batches (every segment at most 16 rows) take the
+        slot-grouped path, which reads each referenced adapter once per call;
+        other batches run the segment shrink and expand.
+        """
+        return self.apply_lora_multi(x, [a_stack], [b_stack], base_output, [0])
+
     def apply_lora_multi(
         self,
         x: torch.Tensor,
@@ -69,8 +80,15 @@ class HipLoRABackend(LoRABackend):
             for b in b_stacks:
                 col_offsets.append(c)
                 c += b.shape[1]
+        x = x.contiguous()
+        a_stacks = [a.contiguous() for a in a_stacks]
+        b_stacks = [b.contiguous() for b in b_stacks]
+        if meta.max_len <= GROUPED_MAX_LEN and apply_grouped(
+            x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace
+        ):
+            return base_output
         n = len(a_stacks)
         r_max = a_stacks[0].shape[1]
         mid = self.mid_buffer(x.shape[0], n * r_max, x)
-        shrink(x.contiguous(), [a.contiguous() for a in a_stacks], meta, mid, workspace=self.workspace)
-        return expand(mid, [b.contiguous() for b in b_stacks], meta, base_output, col_offsets)
+        shrink(x, a_stacks, meta, mid, workspace=self.workspace)
+        return expand(mid, b_stacks, meta, base_output, col_offsets)

@@ -89,11 +89,11 @@ int mlora_abi_version(void) { return 1; }
 
 const char* mlora_last_error(void) { return g_err; }
 
-size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t bs,
+size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows, int32_t bs,
                                     int32_t max_len, int32_t dtype) {
   if (!valid_dtype(dtype)) return 0;
   mlora::ShrinkPlan p;
-  if (!mlora::plan_shrink(in_dim, r_max, n_slices, bs, max_len, dtype, num_cus(), &p)) return 0;
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, num_rows, bs, max_len, dtype, num_cus(), &p)) return 0;
   return p.ws_bytes;
 }
 
@@ -121,22 +121,16 @@ int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t 
   }
 
   mlora::ShrinkPlan plan;
-  if (!mlora::plan_shrink(in_dim, r_max, n_slices, meta->bs, meta->max_len, dtype, num_cus(), &plan))
-    return fail(kUnsupported, "shrink shape unsupported: r_max %d with %d slices (max 64 per slice with "
-                "several slices, 128 with one)", r_max, n_slices);
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, num_rows, meta->bs, meta->max_len, dtype, num_cus(), &plan))
+    return fail(kUnsupported, "shrink shape unsupported: %d slices x r_max %d exceeds 16 blocks of 16 rows",
+                n_slices, r_max);
   if (plan.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < plan.ws_bytes))
     return fail(kWorkspace, "shrink workspace too small: need %zu bytes, got %zu", plan.ws_bytes, workspace_bytes);
 
   const int vec = vec_elems(dtype);
-  const int eb = elem_bytes(dtype);
-  int align = 0;
-  if (al16(x) && x_row_stride % vec == 0 && in_dim % vec == 0) align |= mlora::kAlX;
-  bool ala = in_dim % vec == 0;
+  bool aligned = al16(x) && x_row_stride % vec == 0 && in_dim % vec == 0;
   for (int s = 0; s < n_slices; ++s)
-    ala = ala && al16(slices[s].a) && slices[s].a_slot_stride % vec == 0 && slices[s].a_row_stride % vec == 0;
-  if (ala) align |= mlora::kAlA;
-  if (al16(mid) && mid_row_stride % vec == 0 && r_max % vec == 0) align |= mlora::kAlMid;
-  (void)eb;
+    aligned = aligned && al16(slices[s].a) && slices[s].a_slot_stride % vec == 0 && slices[s].a_row_stride % vec == 0;
 
   mlora::ShrinkArgs args{};
   args.x = x;
@@ -150,14 +144,8 @@ int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t 
   args.mid = mid;
   args.mid_stride = mid_row_stride;
   args.meta = seg_view(meta);
-  args.align = align;
-  if (plan.ws_bytes > 0) {
-    const size_t tiles = static_cast<size_t>(meta->bs) * plan.m_tiles;
-    const size_t counter_bytes = (tiles * 4 + 255) / 256 * 256;
-    args.counters = static_cast<int*>(workspace);
-    args.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
-  }
-  hipError_t e = mlora::launch_shrink(plan, args, dtype, static_cast<hipStream_t>(stream));
+  args.partials = static_cast<float*>(workspace);
+  hipError_t e = mlora::launch_shrink(plan, args, dtype, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "shrink launch");
   return 0;
 }
@@ -180,8 +168,7 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
   const int eb = elem_bytes(dtype);
   mlora::ExpandArgs args{};
   int tiles = 0;
-  bool alb = r_max % vec == 0;
-  bool alo = out_row_stride % vec == 0;
+  bool aligned = r_max % vec == 0 && out_row_stride % vec == 0 && al16(mid) && mid_row_stride % vec == 0;
   for (int s = 0; s < n_slices; ++s) {
     const mlora_slice& sl = slices[s];
     if (sl.b == nullptr) return fail(kBadArg, "slice %d: B is null", s);
@@ -192,14 +179,10 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
     args.slices[s] = slice_view(sl);
     args.tile_base[s] = tiles;
     tiles += mlora::cdiv(sl.out_dim, mlora::kExpandBN);
-    alb = alb && al16(sl.b) && sl.b_slot_stride % vec == 0 && sl.b_row_stride % vec == 0;
-    alo = alo && al16(static_cast<const char*>(out) + static_cast<int64_t>(sl.out_col) * eb) && sl.out_dim % vec == 0;
+    aligned = aligned && al16(sl.b) && sl.b_slot_stride % vec == 0 && sl.b_row_stride % vec == 0 &&
+              al16(static_cast<const char*>(out) + static_cast<int64_t>(sl.out_col) * eb) && sl.out_dim % vec == 0;
   }
   args.tile_base[n_slices] = tiles;
-  int align = 0;
-  if (alb) align |= mlora::kAlB;
-  if (alo) align |= mlora::kAlOut;
-  if (al16(mid) && mid_row_stride % vec == 0 && r_max % vec == 0) align |= mlora::kAlMid;
 
   const int bm = (dtype == MLORA_F32 || meta->max_len <= 16) ? 16 : 64;
   args.mid = mid;
@@ -212,9 +195,89 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
   args.meta = seg_view(meta);
   args.m_tiles = mlora::cdiv(meta->max_len > 0 ? meta->max_len : 1, bm);
   args.n_tiles = tiles;
-  args.align = align;
-  hipError_t e = mlora::launch_expand(bm, args, dtype, static_cast<hipStream_t>(stream));
+  hipError_t e = mlora::launch_expand(bm, args, dtype, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "expand launch");
+  return 0;
+}
+
+size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
+                                     int32_t dtype) {
+  int kc, k_chunk, nbt;
+  size_t ws = 0;
+  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &ws)) return 0;
+  return ws;
+}
+
+int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                        const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                        int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                        size_t workspace_bytes, int32_t mode, int32_t phases, void* stream) {
+  g_err[0] = '\0';
+  if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
+  if (int rc = check_meta(meta)) return rc;
+  if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
+  if (slices == nullptr) return fail(kBadArg, "slices is null");
+  if (in_dim <= 0 || r_max <= 0 || num_rows < 0) return fail(kBadArg, "in_dim %d, r_max %d, num_rows %d", in_dim, r_max, num_rows);
+  if (x_row_stride < in_dim) return fail(kBadArg, "x row stride %lld < in_dim %d", (long long)x_row_stride, in_dim);
+  if (phases < 1 || phases > 3) return fail(kBadArg, "phases %d not in 1..3", phases);
+  if (mode < 0 || mode > 2) return fail(kBadArg, "mode %d not in 0..2", mode);
+  if (meta->bs == 0 || num_rows == 0 || meta->num_slots == 0) return 0;
+  if (x == nullptr || out == nullptr) return fail(kBadArg, "x or out is null");
+  int kc, k_chunk, nbt;
+  size_t ws = 0;
+  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &ws))
+    return fail(kUnsupported, "grouped path needs bf16/fp16, r_max <= %d and a multiple of 8, in_dim a multiple of 8",
+                mlora::kGroupMaxRank);
+  const size_t slot_a_bytes = static_cast<size_t>(r_max) * in_dim * elem_bytes(dtype);
+  const bool single = (mode == 1) || (mode == 0 && slot_a_bytes <= mlora::kFusedMaxSlotBytes);
+  if (single && phases != 3) return fail(kBadArg, "the single-launch path has one phase (use phases=3)");
+  if (!single && (workspace == nullptr || workspace_bytes < ws))
+    return fail(kWorkspace, "grouped workspace too small: need %zu bytes, got %zu", ws, workspace_bytes);
+  const int vec = vec_elems(dtype);
+  const int eb = elem_bytes(dtype);
+  bool aligned = al16(x) && x_row_stride % vec == 0 && out_row_stride % vec == 0 && al16(workspace);
+  mlora::GroupedArgs args{};
+  int tiles = 0;
+  for (int s = 0; s < n_slices; ++s) {
+    const mlora_slice& sl = slices[s];
+    if (sl.a == nullptr || sl.b == nullptr) return fail(kBadArg, "slice %d: A or B is null", s);
+    if (sl.out_dim <= 0 || sl.out_col < 0) return fail(kBadArg, "slice %d: out_dim %d, out_col %d", s, sl.out_dim, sl.out_col);
+    if (sl.a_row_stride < in_dim || sl.a_slot_stride < static_cast<int64_t>(r_max) * sl.a_row_stride ||
+        sl.b_row_stride < r_max || sl.b_slot_stride < static_cast<int64_t>(sl.out_dim) * sl.b_row_stride)
+      return fail(kBadArg, "slice %d: A/B strides do not hold their [r_max, in] / [out, r_max] rows", s);
+    aligned = aligned && al16(sl.a) && sl.a_slot_stride % vec == 0 && sl.a_row_stride % vec == 0 && al16(sl.b) &&
+              sl.b_slot_stride % vec == 0 && sl.b_row_stride % vec == 0 && sl.out_dim % vec == 0 &&
+              al16(static_cast<const char*>(out) + static_cast<int64_t>(sl.out_col) * eb);
+    args.slices[s] = slice_view(sl);
+    args.tile_base[s] = tiles;
+    tiles += mlora::cdiv(sl.out_dim, mlora::kExpandBN);
+  }
+  if (!aligned)
+    return fail(kUnsupported, "grouped path needs 16-byte aligned rows (pointers, strides and widths)");
+  args.tile_base[n_slices] = tiles;
+  args.x = x;
+  args.x_stride = x_row_stride;
+  args.rows = num_rows;
+  args.in_dim = in_dim;
+  args.n_slices = n_slices;
+  args.r_max = r_max;
+  args.out = out;
+  args.out_stride = out_row_stride;
+  args.meta = seg_view(meta);
+  args.partials = static_cast<float*>(workspace);
+  args.kc = kc;
+  args.k_chunk = k_chunk;
+  args.n_tiles = tiles;
+  hipError_t e;
+  if (single) {
+    int dims[MLORA_MAX_SLICES];
+    for (int s = 0; s < n_slices; ++s) dims[s] = slices[s].out_dim;
+    args.n_tiles = mlora::fused_chunks(dims, n_slices, args.tile_base);
+    e = mlora::launch_fused_decode(args, dtype, static_cast<hipStream_t>(stream));
+  } else {
+    e = mlora::launch_grouped(args, dtype, nbt, phases, static_cast<hipStream_t>(stream));
+  }
+  if (e != hipSuccess) return hip_fail(e, "grouped launch");
   return 0;
 }
 

@@ -16,6 +16,8 @@
 // The output tile is prefetched into registers before the MFMA loop so its
 // HBM latency overlaps the B/mid reads; the rounded deltas go through LDS so
 // the read-modify-write of `out` is done with row-contiguous 16-byte chunks.
+// All loads are unconditional (rows clamped, chunks masked), so they issue
+// back to back.
 #include "kernels.h"
 #include "loads.h"
 
@@ -23,7 +25,7 @@ namespace mlora {
 
 namespace {
 
-template <class T, int BM>
+template <class T, int BM, bool AL>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -60,27 +62,32 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   const int n0 = (nt_g - a.tile_base[s]) * BN;
   const int out_dim = a.slices[s].out_dim;
   const float scale = load_scaling(a.meta.scalings, slot, a.meta.scal_dtype);
-  const bool alo = (a.align & kAlOut) != 0;
-  const bool alb = (a.align & kAlB) != 0;
-  const bool alm = (a.align & kAlMid) != 0;
 
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
 
-  // Prefetch this thread's share of the output tile.
+  // Prefetch this thread's share of the output tile (rows clamped to the
+  // segment; chunks past out_dim read the row start and are masked).
   u32x4 ov[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int c = tid + i * 256;
     const int row = c / CPR;
     const int n = n0 + (c - row * CPR) * VEC;
-    const int t = row0 + row;
-    ov[i] = (t < end) ? load_chunk<T>(out + static_cast<int64_t>(t) * a.out_stride + n, out_dim - n, alo)
-                      : zero_chunk();
+    const int t = min(row0 + row, end - 1);
+    ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
   }
 
   const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
-  const raw* mid = static_cast<const raw*>(a.mid) + s * a.r_max;
   const int64_t brs = a.slices[s].b_row_stride;
+  const raw* brow[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+    brow[nb] = B + static_cast<int64_t>(min(n0 + (wave * 4 + nb) * 16 + r16, out_dim - 1)) * brs;
+  const raw* mrow[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+    mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
+               static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
 
   f32x4 acc[4][TB];
 #pragma unroll
@@ -93,16 +100,10 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     const int valid = rank - kk;
     u32x4 yv[TB];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int t = row0 + tb * 16 + r16;
-      yv[tb] = (t < end) ? load_chunk<T>(mid + static_cast<int64_t>(t) * a.mid_stride + kk, valid, alm)
-                         : zero_chunk();
-    }
+    for (int tb = 0; tb < TB; ++tb) yv[tb] = load_row_chunk<T, AL>(mrow[tb], kk, valid);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const int n = n0 + (wave * 4 + nb) * 16 + r16;
-      const u32x4 bv = (n < out_dim) ? load_chunk<T>(B + static_cast<int64_t>(n) * brs + kk, valid, alb)
-                                     : zero_chunk();
+      const u32x4 bv = load_row_chunk<T, AL>(brow[nb], kk, valid);
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = T::mma(acc[nb][tb], bv, yv[tb]);
     }
@@ -143,26 +144,31 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       float f[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(ov[i], e) + chunk_elem<T>(d, e);
-      store_chunk<T>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n, alo);
+      store_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n);
     }
   }
 }
 
-template <class T, int BM>
+template <class T, int BM, bool AL>
 hipError_t launch_t(const ExpandArgs& args, hipStream_t stream) {
   const int64_t blocks = static_cast<int64_t>(args.meta.bs) * args.m_tiles * args.n_tiles;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((expand_kernel<T, BM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
+  hipLaunchKernelGGL((expand_kernel<T, BM, AL>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
   return hipGetLastError();
+}
+
+template <class T, int BM>
+hipError_t launch_al(const ExpandArgs& args, bool aligned, hipStream_t stream) {
+  return aligned ? launch_t<T, BM, true>(args, stream) : launch_t<T, BM, false>(args, stream);
 }
 
 }  // namespace
 
-hipError_t launch_expand(int bm, ExpandArgs args, int dtype, hipStream_t stream) {
+hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream) {
   switch (dtype) {
-    case MLORA_BF16: return bm == 16 ? launch_t<BF16, 16>(args, stream) : launch_t<BF16, 64>(args, stream);
-    case MLORA_F16: return bm == 16 ? launch_t<F16, 16>(args, stream) : launch_t<F16, 64>(args, stream);
-    default: return launch_t<F32, 16>(args, stream);
+    case MLORA_BF16: return bm == 16 ? launch_al<BF16, 16>(args, aligned, stream) : launch_al<BF16, 64>(args, aligned, stream);
+    case MLORA_F16: return bm == 16 ? launch_al<F16, 16>(args, aligned, stream) : launch_al<F16, 64>(args, aligned, stream);
+    default: return launch_al<F32, 16>(args, aligned, stream);
   }
 }
 

@@ -1,20 +1,14 @@
 // Launch-side contracts between the C ABI layer (api.hip) and the kernel
-// translation units.  Every struct here is passed to a kernel by value.
+// translation units.  Every *Args struct is passed to a kernel by value.
 #pragma once
 
 #include "common.h"
 
 namespace mlora {
 
-// Flags for operands whose rows can be read/written as 16-byte chunks.
-enum AlignBits : int {
-  kAlX = 1,
-  kAlA = 2,
-  kAlB = 4,
-  kAlMid = 8,
-  kAlOut = 16,
-};
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// -------------------------------------------------------------- shrink
 struct ShrinkArgs {
   const void* x;
   int64_t x_stride;
@@ -30,27 +24,24 @@ struct ShrinkArgs {
   int m_tiles;      // row tiles per segment
   int ks;           // K splits per row tile
   int k_per_split;  // reduction elements per split (multiple of KSTEP)
-  int* counters;    // [bs * m_tiles] arrival counters (ks > 1), zero between calls
-  float* partials;  // [bs * m_tiles][ks][WM][n_slices * nb_slice][64] f32x4
-  int nb_slice;     // 16-wide n-blocks per slice = cdiv(r_max, 16)
-  int align;        // AlignBits
+  float* partials;  // ks > 1: [ks][rows][n_slices * r_max] fp32 split sums
 };
 
 struct ShrinkPlan {
-  int bm;        // 16 or 64 token rows per tile
+  int bm;     // 16 or 64 token rows per tile
   int m_tiles;
   int ks;
   int k_per_split;
-  int nbs;       // compiled n-blocks per slice (1, 4 or 8)
-  int maxs;      // compiled slice count (1 or 4)
+  int nbt;    // compiled bound on 16-row blocks of A over all slices
   size_t ws_bytes;
 };
 
-// Chooses the tile shape for a shrink launch; returns false if unsupported.
-bool plan_shrink(int in_dim, int r_max, int n_slices, int bs, int max_len, int dtype, int num_cus,
+bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_len, int dtype, int num_cus,
                  ShrinkPlan* plan);
-hipError_t launch_shrink(const ShrinkPlan& plan, ShrinkArgs args, int dtype, hipStream_t stream);
+// Launches the shrink and, when K is split, the in-order split reduction.
+hipError_t launch_shrink(const ShrinkPlan& plan, ShrinkArgs args, int dtype, bool aligned, hipStream_t stream);
 
+// -------------------------------------------------------------- expand
 constexpr int kExpandBN = 256;  // output columns per tile
 
 struct ExpandArgs {
@@ -66,11 +57,52 @@ struct ExpandArgs {
   int m_tiles;
   int n_tiles;                     // n-tiles over all slices
   int tile_base[kMaxSlices + 1];   // first n-tile of each slice
-  int align;
 };
 
-hipError_t launch_expand(int bm, ExpandArgs args, int dtype, hipStream_t stream);
+hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream);
 
+// -------------------------------------------------------------- grouped decode
+// Slot-grouped shrink+expand: workgroups are indexed by (slot, chunk), find
+// their slot's rows by scanning the segment table, and read each slot's A / B
+// once per chunk.  Two launches; the first leaves fp32 split sums in
+// `partials`, the second reduces them in order and applies the expand.
+constexpr int kGroupRows = 256;  // rows gathered per pass
+constexpr int kGroupSteps = 2;   // K-steps per wave per chunk (chunk = 4 waves x 2 steps)
+
+struct GroupedArgs {
+  const void* x;
+  int64_t x_stride;
+  int rows;
+  int in_dim;
+  SliceView slices[kMaxSlices];
+  int n_slices;
+  int r_max;
+  void* out;
+  int64_t out_stride;
+  SegView meta;
+  float* partials;   // [kc][rows][n_slices * r_max]
+  int kc;            // K chunks
+  int k_chunk;       // reduction elements per chunk
+  int n_tiles;
+  int tile_base[kMaxSlices + 1];
+};
+
+// Largest r_max (per slice) the grouped path handles.
+constexpr int kGroupMaxRank = 64;
+
+bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
+                  size_t* ws_bytes);
+hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int phases, hipStream_t stream);
+
+// Single-launch variant (fused.hip): workgroup = (slot, 512 output columns),
+// each recomputing its slot's reduction.  `n_tiles` / `tile_base` count
+// 512-column chunks; the workspace is not used.
+int fused_chunks(const int* out_dims, int n_slices, int* tile_base);
+hipError_t launch_fused_decode(GroupedArgs args, int dtype, hipStream_t stream);
+// A bytes of one slot and slice at or below which the single launch is chosen.
+constexpr size_t kFusedMaxSlotBytes = 0;  // single launch only on request until it beats two launches
+
+// -------------------------------------------------------------- rmsnorm
 struct RmsArgs {
   const void* x;
   int64_t x_stride_outer;
@@ -84,11 +116,22 @@ struct RmsArgs {
   int hidden;
   float eps;
   int tpr;      // threads per row (power of two, 16..256)
-  int aligned;  // x rows, y rows and w readable as 16-byte chunks
+  int aligned;  // x rows and y rows readable as 16-byte chunks
 };
 
 hipError_t launch_rmsnorm(RmsArgs args, int dtype, hipStream_t stream);
 
-inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+// Base pointer of slice `s`'s A (or B) for one slot, selected with
+// compile-time indexing so the kernel-argument array is never indexed
+// dynamically.
+template <class R>
+__device__ __forceinline__ const R* slice_a(const SliceView (&sl)[kMaxSlices], int s, int slot, int n) {
+  const SliceView* p = &sl[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSlices; ++i)
+    if (s == i) p = &sl[i];
+  return static_cast<const R*>(p->a) + static_cast<int64_t>(slot) * p->a_slot_stride +
+         static_cast<int64_t>(n) * p->a_row_stride;
+}
 
 }  // namespace mlora

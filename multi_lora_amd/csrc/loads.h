@@ -1,43 +1,64 @@
-// Masked 16-byte chunk loads/stores used where an operand row may be
-// unaligned or end inside a chunk.  `aligned` is a launch-uniform flag
-// computed on the host (base address, strides and row width all multiples of
-// the chunk), so the branch costs nothing on the fast path.
+// Chunk loads/stores for the kernels' operand rows.
+//
+// Fast path (`AL` true: base, strides and row width are multiples of the
+// 16-byte chunk): every load is unconditional.  Callers clamp row indices to
+// a row that exists and pass the number of valid elements; an invalid chunk
+// is read from the row start (always in bounds) and zeroed by a select.  No
+// branch surrounds a load, so a wave keeps many loads in flight.
+//
+// Slow path (`AL` false): element-wise loads/stores of the valid elements.
 #pragma once
 
 #include "common.h"
 
 namespace mlora {
 
-// Load up to VEC elements starting at p; elements at or past `valid` read as 0.
+// Word masks keeping the first `valid` elements of a chunk (computed without
+// touching the loaded data, so the AND can sit at the point of use).
 template <class T>
-__device__ __forceinline__ u32x4 load_chunk(const typename T::raw_t* p, int valid, bool aligned) {
-  if (valid <= 0) return zero_chunk();
-  if (aligned) {
-    u32x4 v = ld_chunk(p);
-    return valid >= T::VEC ? v : chunk_keep<T>(v, valid);
-  }
-  u32x4 v = zero_chunk();
+__device__ __forceinline__ u32x4 keep_mask(int valid) {
+  u32x4 m;
   if constexpr (sizeof(typename T::raw_t) == 2) {
 #pragma unroll
-    for (int e = 0; e < T::VEC; ++e) {
-      if (e < valid) {
-        uint32_t h = static_cast<uint32_t>(p[e]);
-        v[e >> 1] |= (e & 1) ? (h << 16) : h;
-      }
-    }
+    for (int w = 0; w < 4; ++w)
+      m[w] = (2 * w < valid ? 0x0000ffffu : 0u) | (2 * w + 1 < valid ? 0xffff0000u : 0u);
   } else {
 #pragma unroll
-    for (int e = 0; e < T::VEC; ++e)
-      if (e < valid) v[e] = __float_as_uint(p[e]);
+    for (int w = 0; w < 4; ++w) m[w] = (w < valid) ? 0xffffffffu : 0u;
   }
-  return v;
+  return m;
 }
 
-// Store the first `valid` elements of a chunk at p.
-template <class T>
-__device__ __forceinline__ void store_chunk(typename T::raw_t* p, u32x4 v, int valid, bool aligned) {
+template <class T, bool AL>
+__device__ __forceinline__ u32x4 load_row_chunk(const typename T::raw_t* row, int kk, int valid) {
+  if constexpr (AL) {
+    const u32x4 v = ld_chunk(row + (valid > 0 ? kk : 0));
+    return v & keep_mask<T>(valid);
+  } else {
+    u32x4 v = zero_chunk();
+    const typename T::raw_t* p = row + kk;
+    if constexpr (sizeof(typename T::raw_t) == 2) {
+#pragma unroll
+      for (int e = 0; e < T::VEC; ++e) {
+        if (e < valid) {
+          const uint32_t h = static_cast<uint32_t>(p[e]);
+          v[e >> 1] |= (e & 1) ? (h << 16) : h;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < T::VEC; ++e)
+        if (e < valid) v[e] = __float_as_uint(p[e]);
+    }
+    return v;
+  }
+}
+
+// Store the first `valid` elements of a chunk at p (p must be in bounds when valid > 0).
+template <class T, bool AL>
+__device__ __forceinline__ void store_row_chunk(typename T::raw_t* p, u32x4 v, int valid) {
   if (valid <= 0) return;
-  if (aligned && valid >= T::VEC) {
+  if (AL && valid >= T::VEC) {
     st_chunk(p, v);
     return;
   }
@@ -50,6 +71,31 @@ __device__ __forceinline__ void store_chunk(typename T::raw_t* p, u32x4 v, int v
     for (int e = 0; e < T::VEC; ++e)
       if (e < valid) p[e] = __uint_as_float(v[e]);
   }
+}
+
+// Exclusive prefix sum of `v` over a 256-thread workgroup; `*total` gets the sum.
+// `tmp` is 4 ints of LDS.  Every thread of the workgroup must call it.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) tmp[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int t = tmp[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + x - v;
 }
 
 }  // namespace mlora

@@ -21,7 +21,7 @@ __device__ __forceinline__ float load_w(const void* w, int dtype, int idx) {
   return load_scaling(w, idx, dtype);
 }
 
-template <class T>
+template <class T, bool AL>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -36,7 +36,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   const bool row_ok = row < a.rows;
   const int hidden = a.hidden;
   const int nch = (hidden + VEC - 1) / VEC;
-  const bool al = a.aligned != 0;
 
   const raw* x = static_cast<const raw*>(a.x);
   const int64_t r = row_ok ? row : 0;
@@ -47,7 +46,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
 #pragma unroll
   for (int j = 0; j < kMaxCached; ++j) {
     const int c = li + j * tpr;
-    cache[j] = (row_ok && c < nch) ? load_chunk<T>(xrow + c * VEC, hidden - c * VEC, al) : zero_chunk();
+    cache[j] = load_row_chunk<T, AL>(xrow, c * VEC, (row_ok && c < nch) ? hidden - c * VEC : 0);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float v = chunk_elem<T>(cache[j], e);
@@ -55,7 +54,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     }
   }
   for (int c = li + kMaxCached * tpr; row_ok && c < nch; c += tpr) {
-    const u32x4 v = load_chunk<T>(xrow + c * VEC, hidden - c * VEC, al);
+    const u32x4 v = load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float f = chunk_elem<T>(v, e);
@@ -86,7 +85,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
       const float wv = (col < hidden) ? load_w(a.w, a.w_dtype, col) : 0.f;
       f[e] = chunk_elem<T>(v, e) * rstd * wv;
     }
-    store_chunk<T>(yrow + c * VEC, pack_chunk<T>(f), hidden - c * VEC, al);
+    store_row_chunk<T, AL>(yrow + c * VEC, pack_chunk<T>(f), hidden - c * VEC);
   };
 #pragma unroll
   for (int j = 0; j < kMaxCached; ++j) {
@@ -94,7 +93,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     if (c < nch) emit(c, cache[j]);
   }
   for (int c = li + kMaxCached * tpr; c < nch; c += tpr)
-    emit(c, load_chunk<T>(xrow + c * VEC, hidden - c * VEC, al));
+    emit(c, load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC));
 }
 
 template <class T>
@@ -102,7 +101,10 @@ hipError_t launch_t(const RmsArgs& args, hipStream_t stream) {
   const int rpb = 256 / args.tpr;
   const int64_t blocks = (args.rows + rpb - 1) / rpb;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((rmsnorm_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
+  if (args.aligned)
+    hipLaunchKernelGGL((rmsnorm_kernel<T, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<T, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
   return hipGetLastError();
 }
 

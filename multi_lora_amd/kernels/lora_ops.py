@@ -30,11 +30,10 @@ _WORKSPACES: Dict[Tuple[str, int], torch.Tensor] = {}
 
 
 class Workspace:
-    """Caller-owned scratch for the split-K shrink (zero-initialised, grown on demand).
+    """Caller-owned scratch (fp32 split sums), grown on demand, reused across calls.
 
-    The library leaves its counter words zero after every call, so one
-    workspace can serve any number of sequential launches on one stream.
-    Launches that overlap on different streams need separate workspaces.
+    Sequential launches on one stream may share a workspace; launches that
+    overlap on different streams need separate workspaces.
     """
 
     def __init__(self) -> None:
@@ -148,7 +147,7 @@ def shrink(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], meta: KernelInputM
     lib = _ffi.lib()
     dt = _ffi.dtype_code(x.dtype)
     ws = workspace or _default_workspace(dev)
-    need = lib.mlora_shrink_workspace_bytes(in_dim, r_max, n, m.bs, m.max_len, dt)
+    need = lib.mlora_shrink_workspace_bytes(in_dim, r_max, n, x.shape[0], m.bs, m.max_len, dt)
     ws_ptr, ws_bytes = ws.get(need, dev)
     sl = _slices(a_stacks, [None] * n, [0] * n)
     rc = lib.mlora_shrink(
@@ -193,6 +192,56 @@ def expand(mid: torch.Tensor, b_stacks: Sequence[torch.Tensor], meta: KernelInpu
     _ffi.check(rc, "mlora_expand")
     del keep
     return out
+
+
+GROUPED_MAX_LEN = 16
+
+
+def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],
+                  meta: KernelInputMetaData, out: torch.Tensor, out_cols: Sequence[int],
+                  workspace: Optional[Workspace] = None, phases: int = 3, mode: int = 0) -> bool:
+    """Slot-grouped shrink+expand into ``out``; returns False (nothing launched) if the shape is not eligible.
+
+    ``mode`` 1 = single launch, 2 = two launches, 0 = chosen by the library
+    from the size of one slot's A.  With two launches, ``phases`` 1 / 2 run
+    only the shrink / expand half (the workspace carries the sums between
+    them); 3 runs both.
+    """
+    _require_gpu(x, "x")
+    dev = x.device
+    n = len(a_stacks)
+    if len(b_stacks) != n or not 1 <= n <= _ffi.MAX_SLICES:
+        raise ValueError("need matching A and B stacks (1..4 slices)")
+    if x.dim() != 2 or x.stride(1) != 1 or out.dim() != 2 or out.stride(1) != 1:
+        return False
+    in_dim, r_max = x.shape[1], a_stacks[0].shape[1]
+    for i, (a, b) in enumerate(zip(a_stacks, b_stacks)):
+        _check_stack(a, f"A[{i}]", x.dtype, dev)
+        _check_stack(b, f"B[{i}]", x.dtype, dev)
+        if a.shape[1] != r_max or a.shape[2] != in_dim or b.shape[2] != r_max:
+            raise ValueError(f"slice {i}: A {tuple(a.shape)} / B {tuple(b.shape)} do not match r_max={r_max}, in={in_dim}")
+        if out_cols[i] < 0 or out_cols[i] + b.shape[1] > out.shape[1]:
+            raise ValueError(f"slice {i}: columns outside the output")
+    if out.shape[0] < x.shape[0] or out.dtype != x.dtype or out.device != dev:
+        raise ValueError("output must cover x's rows with x's dtype and device")
+    lib = _ffi.lib()
+    dt = _ffi.dtype_code(x.dtype)
+    need = lib.mlora_grouped_workspace_bytes(in_dim, r_max, n, x.shape[0], dt)
+    if need == 0:
+        return False
+    m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
+    ws = workspace or _default_workspace(dev)
+    ws_ptr, ws_bytes = ws.get(need, dev)
+    sl = _slices(a_stacks, b_stacks, out_cols)
+    rc = lib.mlora_apply_grouped(
+        x.data_ptr(), x.stride(0), x.shape[0], in_dim, sl, n, r_max, out.data_ptr(), out.stride(0), ctypes.byref(m),
+        dt, ws_ptr, ws_bytes, int(mode), int(phases), _ffi.stream_ptr(dev),
+    )
+    del keep
+    if rc == -2:
+        return False
+    _ffi.check(rc, "mlora_apply_grouped")
+    return True
 
 
 def sgemm_lora_a_fwd(x: torch.Tensor, weights: torch.Tensor, kernel_input_metadata: KernelInputMetaData,

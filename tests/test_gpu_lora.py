@@ -250,16 +250,12 @@ def test_strided_output_view(dev):
     assert torch.equal(wide[:, 5120:], before[:, 5120:])
 
 
-def test_deterministic_and_workspace_counters_reset(dev):
-    from multi_lora_amd.kernels.lora_ops import _default_workspace
-
+def test_split_k_is_deterministic(dev):
+    """A long reduction takes the split-K path; splits are summed in a fixed order."""
     wl = synthetic.prefill_mlp(device=dev, part="down", n_seg=3, min_len=5, max_len=40, hidden=512, inter=14336,
                                seed=4)
     first = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
     for _ in range(3):
         again = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
         assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
-    ws = _default_workspace(dev).buf
-    assert ws is not None, "this shape is expected to take the split-K path"
-    # counters: one int32 per (segment, row tile), at the start of the workspace
-    assert torch.count_nonzero(ws[: 4 * wl.meta.bs]) == 0
+    check_workload(wl)

@@ -111,23 +111,33 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
                  int32_t n_slices, int32_t r_max, void* out, int64_t out_row_stride,
                  const mlora_seg_meta* meta, int32_t dtype, void* stream);
 
-/* Bytes of workspace mlora_apply_grouped needs (fp32 sums of each 256-wide
- * K chunk for every row and slice); 0 when the shape is not eligible. */
+/* Bytes of workspace mlora_apply_grouped needs for this shape and `mode`;
+ * 0 when the shape is not eligible (or mode is not 0..2).  Two launches: fp32
+ * sums of each 256-wide K chunk for every row and slice.  Single launch: a
+ * 256-byte header (error word) and the same sums as 64-bit tagged words.
+ * `num_slots` is accepted for layouts that depend on it; none does now. */
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
-                                     int32_t dtype);
+                                     int32_t num_slots, int32_t dtype, int32_t mode);
 
 /* Slot-grouped shrink + expand for decode-shaped batches:
  *   out[t, out_col_s + n] += round(scaling * round(x[t] . A_s[slot,:rank]) . B_s[slot, n, :rank])
  * with the same roundings as mlora_shrink followed by mlora_expand; no `mid`
- * is materialised.  Workgroups are indexed by (slot, chunk) and gather the
+ * is materialised.  Work items are indexed by (slot, chunk) and gather the
  * rows of their slot from the segment table, so each referenced adapter's A
  * and B are read from HBM once per call however many rows use it.
- * `mode`: 1 = single launch (each workgroup of a slot repeats the slot's
- * reduction; A shared through one XCD's L2; no workspace), 2 = two launches
- * (K-chunk sums through the workspace), 0 = pick (currently two launches,
- * the faster of the two on MI355X at the decode shapes measured).
- * `phases` (two-launch mode only): 1 = shrink half (leaves its sums in the
- * workspace), 2 = expand half (consumes them), 3 = both (normal use).
+ * `mode`: 2 = two launches (shrink items, then expand items; the workspace
+ * carries fp32 K-chunk sums and may be any scratch);
+ * 1 = single launch (expand items wait, with a bounded spin, on the sums
+ * the shrink items of the same launch publish, each tagged with the launch's
+ * dispatch id on its hardware queue).  The single-launch workspace must be
+ * zero-filled before its first use, passed to nothing but mode 0/1 calls
+ * afterwards, and used from one stream only (give each stream its own); it
+ * is never cleared between calls.  Its first int32 is a sticky error word
+ * that becomes non-zero if a wait ever timed out (results of that launch are
+ * then unreliable).  Calls sharing a workspace must not overlap.
+ * 0 = the library's choice (currently the single launch).
+ * `phases` (two-launch mode only; must be 3 otherwise): 1 = shrink half
+ * (leaves its sums in the workspace), 2 = expand half (consumes them), 3 = both.
  * Requirements (else -2 and nothing launched): bf16 or fp16; r_max <= 64 and
  * a multiple of 8; 16-byte aligned rows of x, A, B and out (pointers, strides,
  * in_dim and every out_dim multiples of 8 elements).

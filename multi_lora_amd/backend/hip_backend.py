@@ -14,7 +14,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from ..kernels.lora_ops import GROUPED_MAX_LEN, Workspace, apply_grouped, expand, shrink
+from ..kernels.lora_ops import GROUPED_MAX_LEN, LinkedWorkspace, Workspace, apply_grouped, expand, shrink
 from .base import LoRABackend
 
 
@@ -24,6 +24,7 @@ class HipLoRABackend(LoRABackend):
     def __init__(self) -> None:
         super().__init__()
         self.workspace = Workspace()
+        self.linked_workspace = LinkedWorkspace()
 
     def _meta(self):
         if self.kernel_input_metadata is None:
@@ -84,7 +85,8 @@ class HipLoRABackend(LoRABackend):
         a_stacks = [a.contiguous() for a in a_stacks]
         b_stacks = [b.contiguous() for b in b_stacks]
         if meta.max_len <= GROUPED_MAX_LEN and apply_grouped(
-            x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace
+            x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace,
+            linked_workspace=self.linked_workspace,
         ):
             return base_output
         n = len(a_stacks)

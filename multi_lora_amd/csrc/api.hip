@@ -46,6 +46,10 @@ int num_cus() {
   return cached[dev];
 }
 
+// The ABI's grouped `mode` (0 = library's choice) to a schedule.  The
+// library picks the single launch.
+int grouped_schedule(int mode) { return mode == 2 ? mlora::kGroupTwo : mlora::kGroupLinked; }
+
 int check_meta(const mlora_seg_meta* m) {
   if (m == nullptr) return fail(kBadArg, "segment metadata is null");
   if (m->bs < 0 || m->max_len < 0 || m->num_slots < 0)
@@ -85,7 +89,7 @@ mlora::SliceView slice_view(const mlora_slice& s) {
 
 extern "C" {
 
-int mlora_abi_version(void) { return 1; }
+int mlora_abi_version(void) { return 2; }
 
 const char* mlora_last_error(void) { return g_err; }
 
@@ -201,10 +205,12 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
 }
 
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
-                                     int32_t dtype) {
+                                     int32_t num_slots, int32_t dtype, int32_t mode) {
   int kc, k_chunk, nbt;
   size_t ws = 0;
-  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &ws)) return 0;
+  if (mode < 0 || mode > 2) return 0;
+  const int m = grouped_schedule(mode);
+  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, num_slots, dtype, m, &kc, &k_chunk, &nbt, &ws)) return 0;
   return ws;
 }
 
@@ -223,15 +229,14 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   if (mode < 0 || mode > 2) return fail(kBadArg, "mode %d not in 0..2", mode);
   if (meta->bs == 0 || num_rows == 0 || meta->num_slots == 0) return 0;
   if (x == nullptr || out == nullptr) return fail(kBadArg, "x or out is null");
+  const int m = grouped_schedule(mode);
+  if (m == mlora::kGroupLinked && phases != 3) return fail(kBadArg, "the single-launch path has one phase (use phases=3)");
   int kc, k_chunk, nbt;
   size_t ws = 0;
-  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &ws))
+  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, meta->num_slots, dtype, m, &kc, &k_chunk, &nbt, &ws))
     return fail(kUnsupported, "grouped path needs bf16/fp16, r_max <= %d and a multiple of 8, in_dim a multiple of 8",
                 mlora::kGroupMaxRank);
-  const size_t slot_a_bytes = static_cast<size_t>(r_max) * in_dim * elem_bytes(dtype);
-  const bool single = (mode == 1) || (mode == 0 && slot_a_bytes <= mlora::kFusedMaxSlotBytes);
-  if (single && phases != 3) return fail(kBadArg, "the single-launch path has one phase (use phases=3)");
-  if (!single && (workspace == nullptr || workspace_bytes < ws))
+  if (workspace == nullptr || workspace_bytes < ws)
     return fail(kWorkspace, "grouped workspace too small: need %zu bytes, got %zu", ws, workspace_bytes);
   const int vec = vec_elems(dtype);
   const int eb = elem_bytes(dtype);
@@ -268,15 +273,7 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   args.kc = kc;
   args.k_chunk = k_chunk;
   args.n_tiles = tiles;
-  hipError_t e;
-  if (single) {
-    int dims[MLORA_MAX_SLICES];
-    for (int s = 0; s < n_slices; ++s) dims[s] = slices[s].out_dim;
-    args.n_tiles = mlora::fused_chunks(dims, n_slices, args.tile_base);
-    e = mlora::launch_fused_decode(args, dtype, static_cast<hipStream_t>(stream));
-  } else {
-    e = mlora::launch_grouped(args, dtype, nbt, phases, static_cast<hipStream_t>(stream));
-  }
+  const hipError_t e = mlora::launch_grouped(args, dtype, nbt, m, phases, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "grouped launch");
   return 0;
 }

@@ -3,31 +3,60 @@
 // The reference launches one program per segment and, in decode, streams
 // the segment's whole A / B slice per token (multi_lora/kernels/sgemm_lora_a.py:118-183,
 // sgemm_lora_b.py:93-153), so an adapter used by n tokens is read n times.
-// Here workgroups are indexed by (slot, chunk) instead: each finds the rows
+// Here work items are indexed by (slot, chunk) instead: each finds the rows
 // its slot owns with a workgroup-wide scan of the segment table (stable: the
-// rows come out in ascending order), and reads that slot's A / B chunk once
-// for all of them.  No planning pass and no host-side state are involved, so
-// the two launches are safe to capture in a HIP graph.
+// rows come out in ascending order) and reads that slot's A / B chunk once
+// for all of them.  No planning pass and no host-side state are involved.
 //
-//   grouped_shrink  workgroup = (slot, 256-wide K chunk); the 4 waves take
-//                   2 K-steps each, A fragments stay in registers while the
-//                   slot's rows go by 16 at a time; the four wave sums are
-//                   added in LDS and the chunk's fp32 sums are stored per row.
-//   grouped_expand  workgroup = (slot, 256 output columns of one slice);
-//                   B fragments are loaded first, then for each 16-row tile
-//                   the K-chunk sums are added in chunk order, rounded to
-//                   the storage type (the reference's `mid` rounding,
-//                   sgemm_lora_a.py:109), multiplied with B on MFMA, scaled
-//                   and rounded (sgemm_lora_b.py:84-89), and added into the
-//                   output rows through an LDS transpose.
+//   shrink item  (slot, 256-wide K chunk): the 4 waves take 2 K-steps each,
+//                A fragments stay in registers while the slot's rows go by
+//                16 at a time; the four wave sums are added in LDS and the
+//                chunk's fp32 sums are published per (chunk, row, column).
+//   expand item  (slot, 256 output columns of one slice): B fragments and
+//                the output rows are requested first; the K-chunk sums are
+//                added in chunk order and rounded to the storage type (the
+//                reference's `mid` rounding, sgemm_lora_a.py:109), multiplied
+//                with B on MFMA, scaled and rounded (sgemm_lora_b.py:84-89),
+//                and added into the output rows through an LDS transpose.
+//
+// Two schedules share these bodies:
+//   two launches  shrink items, then expand items; the kernel boundary
+//                 orders them and the sums travel as plain fp32.
+//   linked        one launch holding the shrink items followed by the expand
+//                 items.  Each sum is published as one 64-bit word
+//                 {tag, fp32 bits} with an atomic store; the tag is an odd
+//                 32-bit function of this launch's dispatch id (the packet
+//                 index on its hardware queue, fresh for every launch and
+//                 every graph replay) and of the queue.  An expand item first
+//                 waits, one lane per K chunk, for one sentinel word of each
+//                 chunk, then reads every word it needs and checks every tag,
+//                 waiting on any word still missing.  Words left by earlier
+//                 launches carry other tags, so the workspace is never
+//                 cleared and no counter is kept.  Two launches on one queue
+//                 get equal tags only 2^31 packets apart: a word would have
+//                 to stay unwritten that long and then be read by exactly
+//                 such a launch.  Each wait is bounded: on timeout the item
+//                 raises the workspace's error word and goes on, so no wave
+//                 can hang.  Shrink items never wait and workgroups are
+//                 dispatched in index order, so every shrink item is placed
+//                 before any expand item that waits on it.  Every
+//                 cross-workgroup access is a relaxed agent-scope atomic on a
+//                 single word: device-coherent on gfx950 without any cache
+//                 flush, and a word's tag and value always arrive together.
+//                 Segments that overlap (one row in two segments, outside the
+//                 reference's contract too) can make a wait time out; the
+//                 error word reports it.
 // Arithmetic per row is the same as the segment kernels' (fp32 sums, two
-// roundings), only the split of the K reduction differs.
+// roundings); only the split of the K reduction differs.
 #include "kernels.h"
 #include "loads.h"
 
 namespace mlora {
 
 namespace {
+
+constexpr int kSpinLimit = 1 << 20;   // polls before an expand item gives up
+constexpr int kPollBatch = 16;        // K-chunk words requested together
 
 // One thread's view of one segment of the table: its slot and row range.
 struct SegEntry {
@@ -42,8 +71,8 @@ __device__ __forceinline__ SegEntry load_seg(const SegView& m, int seg) {
 
 // Rows owned by `slot` in ascending order.  Positions [w0, w0 + kGroupRows)
 // of that list go to `list`; returns the full count.  `first` is this
-// thread's entry of the first 256 segments, loaded by the caller at kernel
-// start so the table read overlaps the other first loads.  All threads call it.
+// thread's entry of the first 256 segments, loaded at kernel start so the
+// table read overlaps the other first loads.  All threads call it.
 __device__ int slot_rows(const SegView& m, const SegEntry& first, int rows, int slot, int w0, int* list, int* tmp) {
   int total = 0;
   for (int base = 0; base < m.bs; base += 256) {
@@ -54,7 +83,7 @@ __device__ int slot_rows(const SegView& m, const SegEntry& first, int rows, int 
       len = max(min(e.p1, rows) - st, 0);
     }
     int sum;
-    const int off = block_exclusive_scan(len, tmp, &sum) + total;
+    const int off = block_exclusive_scan<4>(len, tmp, &sum) + total;
     const int lo = max(w0 - off, 0);
     const int hi = min(w0 + kGroupRows - off, len);
     for (int i = lo; i < hi; ++i) list[off + i - w0] = st + i;
@@ -65,26 +94,47 @@ __device__ int slot_rows(const SegView& m, const SegEntry& first, int rows, int 
 }
 
 __device__ __forceinline__ int slot_rank(const GroupedArgs& a, int slot) {
-  int r = (slot < a.meta.num_slots) ? a.meta.ranks[slot] : 0;
+  const int r = (slot < a.meta.num_slots) ? a.meta.ranks[slot] : 0;
   return max(min(r, a.r_max), 0);
 }
 
-template <class T, int NBT>
-__global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
+__device__ uint64_t hw_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+// This launch's tag: odd (a zero-filled workspace never matches), equal for
+// every workgroup of the launch, different for launches on one queue fewer
+// than 2^31 packets apart; the queue address salts it.
+__device__ __forceinline__ uint32_t launch_tag() {
+  const uint64_t q = reinterpret_cast<uint64_t>(__builtin_amdgcn_queue_ptr());
+  const uint32_t salt = static_cast<uint32_t>(q ^ (q >> 32)) * 0x9E3779B1u;
+  return ((static_cast<uint32_t>(hw_dispatch_id()) + salt) << 1) | 1u;
+}
+
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
+  return (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
+}
+
+// Linked-schedule workspace: [error word | pad to 256 B][tagged sums
+// [kc][rows][n_slices * r_max]].
+struct LinkedView {
+  int* error;
+  uint64_t* sums;
+};
+
+__device__ __forceinline__ LinkedView linked_view(const GroupedArgs& a) {
+  char* base = reinterpret_cast<char*>(a.partials);
+  return LinkedView{reinterpret_cast<int*>(base), reinterpret_cast<uint64_t*>(base + kLinkedHeader)};
+}
+
+template <class T, int NBT, bool LINKED>
+__device__ void shrink_item(const GroupedArgs& a, int slot, int c, int* s_rows, int* s_tmp, f32x4 (*red)[kWave]) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   constexpr int KSTEP = T::KSTEP;
-  __shared__ int s_rows[kGroupRows];
-  __shared__ int s_tmp[4];
-  __shared__ f32x4 red[3 * NBT][kWave];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int slot = blockIdx.x / a.kc;
-  const int c = blockIdx.x - slot * a.kc;
 
   // First loads, issued together: the slot's rank and this thread's entry of
   // the segment table.
@@ -140,13 +190,22 @@ __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
           for (int j = 0; j < NBT; ++j)
             if (j < nbt) acc[j] += red[w2 * NBT + j][lane];
         if (tt + r16 < cnt) {
-          float* prow = a.partials + (static_cast<int64_t>(c) * a.rows + s_rows[tt + r16]) * ncols;
+          const int64_t rowoff = (static_cast<int64_t>(c) * a.rows + s_rows[tt + r16]) * ncols;
 #pragma unroll
           for (int j = 0; j < NBT; ++j) {
             if (j >= nbt) break;
             const int s = j / nb_act;
             const int n = (j - s * nb_act) * 16 + 4 * g;
-            if (n < a.r_max) *reinterpret_cast<f32x4*>(prow + s * a.r_max + n) = acc[j];
+            if (n >= a.r_max) continue;
+            if constexpr (LINKED) {
+              uint64_t* p = linked_view(a).sums + rowoff + s * a.r_max + n;
+              const uint32_t tag = launch_tag();
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                __hip_atomic_store(p + q, tagged(tag, acc[j][q]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+              *reinterpret_cast<f32x4*>(a.partials + rowoff + s * a.r_max + n) = acc[j];
+            }
           }
         }
       }
@@ -155,8 +214,68 @@ __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
   }
 }
 
+// Bounded wait for one linked word to carry the tag; returns the word (its
+// value is unreliable if the wait timed out, which raises the error word).
+__device__ uint64_t wait_word(const LinkedView& lv, const uint64_t* p, uint32_t tag) {
+  for (int spin = 0;; ++spin) {
+    const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (static_cast<uint32_t>(w >> 32) == tag) return w;
+    if (spin >= kSpinLimit) {
+      __hip_atomic_store(lv.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return w;
+    }
+    // Once any wait has timed out, every other wait of the launch ends
+    // within 1024 polls instead of running to its own limit.
+    if ((spin & 1023) == 1023 && __hip_atomic_load(lv.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return w;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Sum over the K chunks, in chunk order, of the sums published for one
+// (row, column) at word `idx`; chunk z's word sits at idx + z * zstride.  In
+// the linked schedule every word's tag is checked, and a word that has not
+// arrived yet is waited for.
+template <bool LINKED>
+__device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, int64_t zstride) {
+  float sum = 0.f;
+  for (int z0 = 0; z0 < a.kc; z0 += kPollBatch) {
+    float v[kPollBatch];
+    if constexpr (LINKED) {
+      const LinkedView lv = linked_view(a);
+      const uint32_t tag = launch_tag();
+      const uint64_t* p = lv.sums + idx;
+      uint64_t w[kPollBatch];
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u)
+        w[u] = (z0 + u < a.kc) ? __hip_atomic_load(p + (z0 + u) * zstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : tagged(tag, 0.f);
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u)
+        if (static_cast<uint32_t>(w[u] >> 32) != tag) w[u] = wait_word(lv, p + (z0 + u) * zstride, tag);
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u) v[u] = __uint_as_float(static_cast<uint32_t>(w[u]));
+    } else {
+      const float* p = a.partials + idx;
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? p[(z0 + u) * zstride] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPollBatch; ++u) sum += v[u];
+  }
+  return sum;
+}
+
 template <class T>
-__global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
+struct ExpandLds {
+  using raw = typename T::raw_t;
+  raw delta[16 * (kExpandBN + T::VEC)];
+  raw ytile[16 * (kGroupMaxRank + T::VEC)];
+  int rows[kGroupRows];
+  int tmp[4];
+};
+
+template <class T, bool LINKED>
+__device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<T>& lds) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   constexpr int KSTEP = T::KSTEP;
@@ -166,18 +285,12 @@ __global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
   constexpr int RPT = 16 * CPR / 256;
   constexpr int YS = kGroupMaxRank + VEC;
   constexpr int RS = kGroupMaxRank / KSTEP;
-  __shared__ __attribute__((aligned(16))) raw delta[16 * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) raw ytile[16 * YS];
-  __shared__ int s_rows[kGroupRows];
-  __shared__ int s_tmp[4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int slot = blockIdx.x / a.n_tiles;
-  const int nt_g = blockIdx.x - slot * a.n_tiles;
 
   const SegEntry first = load_seg(a.meta, tid);
   const int rank = slot_rank(a, slot);
@@ -203,11 +316,12 @@ __global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
 
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
   const int ncols = a.n_slices * a.r_max;
-  const int yrow = tid >> 4;
-  const int ycol = (tid & 15) * 4;
-  int total = slot_rows(a.meta, first, a.rows, slot, 0, s_rows, s_tmp);
+  const int64_t zstride = static_cast<int64_t>(a.rows) * ncols;
+  // Columns the shrink items publish: whole 16-column blocks up to the rank.
+  const int live = min(((rank + 15) >> 4) * 16, a.r_max);
+  int total = slot_rows(a.meta, first, a.rows, slot, 0, lds.rows, lds.tmp);
   for (int w0 = 0; w0 < total; w0 += kGroupRows) {
-    if (w0 > 0) total = slot_rows(a.meta, first, a.rows, slot, w0, s_rows, s_tmp);
+    if (w0 > 0) total = slot_rows(a.meta, first, a.rows, slot, w0, lds.rows, lds.tmp);
     const int cnt = min(kGroupRows, total - w0);
     for (int tt = 0; tt < cnt; tt += 16) {
       u32x4 ov[RPT];
@@ -216,29 +330,34 @@ __global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
         const int cidx = tid + i * 256;
         const int row = cidx / CPR;
         const int n = n0 + (cidx - row * CPR) * VEC;
-        const int t = s_rows[min(tt + row, cnt - 1)];
+        const int t = lds.rows[min(tt + row, cnt - 1)];
         ov[i] = load_row_chunk<T, true>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
       }
-      // y = in-order sum of the K-chunk sums, rounded like the reference's mid.
-      if (ycol < a.r_max) {
-        const int t = s_rows[min(tt + yrow, cnt - 1)];
-        const float* p = a.partials + static_cast<int64_t>(t) * ncols + s * a.r_max + ycol;
-        const int64_t zstride = static_cast<int64_t>(a.rows) * ncols;
-        // Issue the chunk loads in groups of 8 before adding, keeping the
-        // addition order z = 0, 1, 2, ... (the loads are independent).
-        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-        int z = 0;
-        for (; z + 8 <= a.kc; z += 8) {
-          f32x4 v[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f32x4*>(p + (z + u) * zstride);
-#pragma unroll
-          for (int u = 0; u < 8; ++u) sum += v[u];
+      const int rows_here = min(16, cnt - tt);
+      if constexpr (LINKED) {
+        // Light polling first: one lane per K chunk waits for the word its
+        // shrink item stores last for this tile (last row, last live column
+        // of the last slice); the full read below then rarely finds a word
+        // missing.  Polling every word would flood the memory system the
+        // shrink items are reading from.
+        if (wave == 0) {
+          const int64_t sidx = static_cast<int64_t>(lds.rows[tt + rows_here - 1]) * ncols +
+                               (a.n_slices - 1) * a.r_max + live - 1;
+          const LinkedView lv = linked_view(a);
+          const uint32_t tag = launch_tag();
+          for (int z = lane; z < a.kc; z += kWave) wait_word(lv, lv.sums + z * zstride + sidx, tag);
         }
-        for (; z < a.kc; ++z) sum += *reinterpret_cast<const f32x4*>(p + z * zstride);
-        raw* yp = ytile + yrow * YS + ycol;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) yp[q] = T::from_f32(ycol + q < rank ? sum[q] : 0.f);
+        __syncthreads();
+      }
+      // y = in-order sum of the K-chunk sums, rounded like the reference's
+      // mid; zero at and past the rank.  One (row, column) per thread.
+      for (int idx = tid; idx < 16 * a.r_max; idx += 256) {
+        const int yr = idx / a.r_max;
+        const int yc = idx - yr * a.r_max;
+        float v = 0.f;
+        if (yr < rows_here && yc < live)
+          v = chunk_sum<LINKED>(a, static_cast<int64_t>(lds.rows[tt + yr]) * ncols + s * a.r_max + yc, zstride);
+        lds.ytile[yr * YS + yc] = T::from_f32(yc < rank ? v : 0.f);
       }
       __syncthreads();
 
@@ -249,7 +368,7 @@ __global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
       for (int ks = 0; ks < RS; ++ks) {
         if (ks * KSTEP >= rank) break;
         const int kk = ks * KSTEP + g * VEC;
-        const u32x4 yv = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(ytile + r16 * YS + kk) : zero_chunk();
+        const u32x4 yv = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(lds.ytile + r16 * YS + kk) : zero_chunk();
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) acc[nb] = T::mma(acc[nb], bf[ks][nb], yv);
       }
@@ -259,7 +378,7 @@ __global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
         uint2 w;
         w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) | (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
         w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) | (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
-        *reinterpret_cast<uint2*>(delta + r16 * LDS_STRIDE + (wave * 4 + nb) * 16 + 4 * g) = w;
+        *reinterpret_cast<uint2*>(lds.delta + r16 * LDS_STRIDE + (wave * 4 + nb) * 16 + 4 * g) = w;
       }
       __syncthreads();
 #pragma unroll
@@ -269,22 +388,65 @@ __global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
         const int cc = cidx - row * CPR;
         const int n = n0 + cc * VEC;
         if (tt + row < cnt && n < out_dim) {
-          const u32x4 d = *reinterpret_cast<const u32x4*>(delta + row * LDS_STRIDE + cc * VEC);
+          const u32x4 d = *reinterpret_cast<const u32x4*>(lds.delta + row * LDS_STRIDE + cc * VEC);
           float f[VEC];
 #pragma unroll
           for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(ov[i], e) + chunk_elem<T>(d, e);
-          st_chunk(out + static_cast<int64_t>(s_rows[tt + row]) * a.out_stride + n, pack_chunk<T>(f));
+          st_chunk(out + static_cast<int64_t>(lds.rows[tt + row]) * a.out_stride + n, pack_chunk<T>(f));
         }
       }
+      __syncthreads();
     }
+  }
+
+}
+
+template <class T, int NBT>
+__global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
+  __shared__ int s_rows[kGroupRows];
+  __shared__ int s_tmp[4];
+  __shared__ f32x4 red[3 * NBT][kWave];
+  const int slot = blockIdx.x / a.kc;
+  shrink_item<T, NBT, false>(a, slot, blockIdx.x - slot * a.kc, s_rows, s_tmp, red);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
+  __shared__ __attribute__((aligned(16))) ExpandLds<T> lds;
+  const int slot = blockIdx.x / a.n_tiles;
+  expand_item<T, false>(a, slot, blockIdx.x - slot * a.n_tiles, lds);
+}
+
+// Shrink items are workgroups [0, num_slots * kc); expand items follow.
+// Four waves per SIMD (at most 128 VGPRs) keep four workgroups resident per
+// CU, so expand items are placed, and run their prologue, while the shrink
+// items still run; with 8 or more A blocks the A fragments alone need more.
+template <class T, int NBT>
+__global__ __launch_bounds__(256, NBT >= 8 ? 1 : 4) void grouped_linked_kernel(GroupedArgs a) {
+  __shared__ __attribute__((aligned(16))) ExpandLds<T> lds;
+  __shared__ f32x4 red[3 * NBT][kWave];
+  const int ns = a.meta.num_slots * a.kc;
+  const int b = blockIdx.x;
+  if (b < ns) {
+    const int slot = b / a.kc;
+    shrink_item<T, NBT, true>(a, slot, b - slot * a.kc, lds.rows, lds.tmp, red);
+  } else {
+    const int e = b - ns;
+    const int slot = e / a.n_tiles;
+    expand_item<T, true>(a, slot, e - slot * a.n_tiles, lds);
   }
 }
 
 template <class T, int NBT>
-hipError_t launch_t(const GroupedArgs& args, int phases, hipStream_t stream) {
+hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t stream) {
   const int64_t g1 = static_cast<int64_t>(args.meta.num_slots) * args.kc;
   const int64_t g2 = static_cast<int64_t>(args.meta.num_slots) * args.n_tiles;
   if (g1 <= 0 || g2 <= 0) return hipSuccess;
+  if (mode == kGroupLinked) {
+    hipLaunchKernelGGL((grouped_linked_kernel<T, NBT>), dim3(static_cast<unsigned>(g1 + g2)), dim3(256), 0, stream,
+                       args);
+    return hipGetLastError();
+  }
   if (phases & 1) {
     hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT>), dim3(static_cast<unsigned>(g1)), dim3(256), 0, stream, args);
     hipError_t e = hipGetLastError();
@@ -298,22 +460,22 @@ hipError_t launch_t(const GroupedArgs& args, int phases, hipStream_t stream) {
 }
 
 template <class T>
-hipError_t launch_dtype(const GroupedArgs& args, int nbt, int phases, hipStream_t stream) {
+hipError_t launch_dtype(const GroupedArgs& args, int nbt, int mode, int phases, hipStream_t stream) {
   switch (nbt) {
-    case 1: return launch_t<T, 1>(args, phases, stream);
-    case 2: return launch_t<T, 2>(args, phases, stream);
-    case 4: return launch_t<T, 4>(args, phases, stream);
-    case 8: return launch_t<T, 8>(args, phases, stream);
-    default: return launch_t<T, 16>(args, phases, stream);
+    case 1: return launch_t<T, 1>(args, mode, phases, stream);
+    case 2: return launch_t<T, 2>(args, mode, phases, stream);
+    case 4: return launch_t<T, 4>(args, mode, phases, stream);
+    case 8: return launch_t<T, 8>(args, mode, phases, stream);
+    default: return launch_t<T, 16>(args, mode, phases, stream);
   }
 }
 
 }  // namespace
 
-bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
-                  size_t* ws_bytes) {
+bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int num_slots, int dtype, int mode, int* kc,
+                  int* k_chunk, int* nbt, size_t* ws_bytes) {
   if (dtype != MLORA_BF16 && dtype != MLORA_F16) return false;
-  if (in_dim <= 0 || rows <= 0 || n_slices < 1 || n_slices > kMaxSlices) return false;
+  if (in_dim <= 0 || rows <= 0 || num_slots < 0 || n_slices < 1 || n_slices > kMaxSlices) return false;
   if (r_max <= 0 || r_max > kGroupMaxRank || r_max % 8 != 0 || in_dim % 8 != 0) return false;
   const int blocks = n_slices * cdiv(r_max, 16);
   int b = 1;
@@ -322,13 +484,17 @@ bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int*
   *nbt = b;
   *k_chunk = 4 * kGroupSteps * BF16::KSTEP;
   *kc = cdiv(in_dim, *k_chunk);
-  *ws_bytes = static_cast<size_t>(*kc) * rows * n_slices * r_max * sizeof(float);
+  const size_t words = static_cast<size_t>(*kc) * rows * n_slices * r_max;
+  if (mode == kGroupLinked)
+    *ws_bytes = kLinkedHeader + words * sizeof(uint64_t);
+  else
+    *ws_bytes = words * sizeof(float);
   return true;
 }
 
-hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int phases, hipStream_t stream) {
-  if (dtype == MLORA_BF16) return launch_dtype<BF16>(args, nbt, phases, stream);
-  return launch_dtype<F16>(args, nbt, phases, stream);
+hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int mode, int phases, hipStream_t stream) {
+  if (dtype == MLORA_BF16) return launch_dtype<BF16>(args, nbt, mode, phases, stream);
+  return launch_dtype<F16>(args, nbt, mode, phases, stream);
 }
 
 }  // namespace mlora

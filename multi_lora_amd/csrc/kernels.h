@@ -62,12 +62,15 @@ struct ExpandArgs {
 hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream);
 
 // -------------------------------------------------------------- grouped decode
-// Slot-grouped shrink+expand: workgroups are indexed by (slot, chunk), find
+// Slot-grouped shrink+expand: work items are indexed by (slot, chunk), find
 // their slot's rows by scanning the segment table, and read each slot's A / B
-// once per chunk.  Two launches; the first leaves fp32 split sums in
-// `partials`, the second reduces them in order and applies the expand.
+// once per chunk.  Shrink items leave fp32 K-chunk sums in the workspace;
+// expand items add them in chunk order and apply the expand.
 constexpr int kGroupRows = 256;  // rows gathered per pass
 constexpr int kGroupSteps = 2;   // K-steps per wave per chunk (chunk = 4 waves x 2 steps)
+constexpr int kGroupLinked = 1;  // mode: one launch, sums passed as tagged words
+constexpr int kGroupTwo = 2;     // mode: two launches, sums passed as plain fp32
+constexpr size_t kLinkedHeader = 256;  // linked workspace: error word, padded
 
 struct GroupedArgs {
   const void* x;
@@ -80,27 +83,19 @@ struct GroupedArgs {
   void* out;
   int64_t out_stride;
   SegView meta;
-  float* partials;   // [kc][rows][n_slices * r_max]
+  float* partials;   // two launches: [kc][rows][n_slices * r_max]; linked: the linked workspace
   int kc;            // K chunks
   int k_chunk;       // reduction elements per chunk
-  int n_tiles;
+  int n_tiles;       // expand items per slot (256-column tiles over all slices)
   int tile_base[kMaxSlices + 1];
 };
 
 // Largest r_max (per slice) the grouped path handles.
 constexpr int kGroupMaxRank = 64;
 
-bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
-                  size_t* ws_bytes);
-hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int phases, hipStream_t stream);
-
-// Single-launch variant (fused.hip): workgroup = (slot, 512 output columns),
-// each recomputing its slot's reduction.  `n_tiles` / `tile_base` count
-// 512-column chunks; the workspace is not used.
-int fused_chunks(const int* out_dims, int n_slices, int* tile_base);
-hipError_t launch_fused_decode(GroupedArgs args, int dtype, hipStream_t stream);
-// A bytes of one slot and slice at or below which the single launch is chosen.
-constexpr size_t kFusedMaxSlotBytes = 0;  // single launch only on request until it beats two launches
+bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int num_slots, int dtype, int mode, int* kc,
+                  int* k_chunk, int* nbt, size_t* ws_bytes);
+hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int mode, int phases, hipStream_t stream);
 
 // -------------------------------------------------------------- rmsnorm
 struct RmsArgs {

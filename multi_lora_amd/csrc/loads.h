@@ -73,8 +73,9 @@ __device__ __forceinline__ void store_row_chunk(typename T::raw_t* p, u32x4 v, i
   }
 }
 
-// Exclusive prefix sum of `v` over a 256-thread workgroup; `*total` gets the sum.
-// `tmp` is 4 ints of LDS.  Every thread of the workgroup must call it.
+// Exclusive prefix sum of `v` over a workgroup of NW wave64s; `*total` gets
+// the sum.  `tmp` is NW ints of LDS.  Every thread of the workgroup must call it.
+template <int NW>
 __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -88,7 +89,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
   __syncthreads();
   int before = 0, all = 0;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const int t = tmp[w];
     before += (w < wave) ? t : 0;
     all += t;

@@ -48,11 +48,37 @@ class Workspace:
         return self.buf.data_ptr(), self.buf.numel()
 
 
-def _default_workspace(device: torch.device) -> Workspace:
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+class LinkedWorkspace:
+    """Workspaces of the single-launch grouped path, one per stream.
+
+    Each buffer is zero-filled on allocation and used by nothing else: the
+    kernel tags the words it publishes with the launch's dispatch id on its
+    hardware queue, which keeps launches on one stream apart without ever
+    clearing the buffer; launches on different streams get separate buffers.
+    """
+
+    def __init__(self) -> None:
+        self.bufs: Dict[Tuple[torch.device, int], torch.Tensor] = {}
+
+    def get(self, nbytes: int, device: torch.device, stream: int) -> Tuple[int, int]:
+        key = (device, stream)
+        buf = self.bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = self.bufs[key] = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        return buf.data_ptr(), buf.numel()
+
+    def error_word(self) -> int:
+        """Sticky error word over all buffers (synchronises): non-zero once a
+        wait between work items of some launch timed out, after which that
+        launch's results are not trustworthy."""
+        return max((int(b[:4].view(torch.int32).item()) for b in self.bufs.values()), default=0)
+
+
+def _default_workspace(device: torch.device, linked: bool = False) -> Workspace:
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device(), linked)
     ws = _WORKSPACES.get(key)
     if ws is None:
-        ws = _WORKSPACES[key] = Workspace()
+        ws = _WORKSPACES[key] = LinkedWorkspace() if linked else Workspace()
     return ws
 
 
@@ -199,19 +225,22 @@ GROUPED_MAX_LEN = 16
 
 def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],
                   meta: KernelInputMetaData, out: torch.Tensor, out_cols: Sequence[int],
-                  workspace: Optional[Workspace] = None, phases: int = 3, mode: int = 0) -> bool:
+                  workspace: Optional[Workspace] = None, phases: int = 3, mode: int = 0,
+                  linked_workspace: Optional[LinkedWorkspace] = None) -> bool:
     """Slot-grouped shrink+expand into ``out``; returns False (nothing launched) if the shape is not eligible.
 
-    ``mode`` 1 = single launch, 2 = two launches, 0 = chosen by the library
-    from the size of one slot's A.  With two launches, ``phases`` 1 / 2 run
-    only the shrink / expand half (the workspace carries the sums between
-    them); 3 runs both.
+    ``mode`` 1 = single launch (shrink and expand work items linked through
+    ``linked_workspace``), 2 = two launches (sums through ``workspace``),
+    0 = the library's choice (the single launch).  With two launches,
+    ``phases`` 1 / 2 run only the shrink / expand half; 3 runs both.
     """
     _require_gpu(x, "x")
     dev = x.device
     n = len(a_stacks)
     if len(b_stacks) != n or not 1 <= n <= _ffi.MAX_SLICES:
         raise ValueError("need matching A and B stacks (1..4 slices)")
+    if mode not in (0, 1, 2):
+        raise ValueError(f"mode {mode} not in 0..2")
     if x.dim() != 2 or x.stride(1) != 1 or out.dim() != 2 or out.stride(1) != 1:
         return False
     in_dim, r_max = x.shape[1], a_stacks[0].shape[1]
@@ -226,16 +255,19 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
         raise ValueError("output must cover x's rows with x's dtype and device")
     lib = _ffi.lib()
     dt = _ffi.dtype_code(x.dtype)
-    need = lib.mlora_grouped_workspace_bytes(in_dim, r_max, n, x.shape[0], dt)
+    m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
+    need = lib.mlora_grouped_workspace_bytes(in_dim, r_max, n, x.shape[0], m.num_slots, dt, int(mode))
     if need == 0:
         return False
-    m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
-    ws = workspace or _default_workspace(dev)
-    ws_ptr, ws_bytes = ws.get(need, dev)
+    stream = _ffi.stream_ptr(dev)
+    if mode == 2:
+        ws_ptr, ws_bytes = (workspace or _default_workspace(dev)).get(need, dev)
+    else:
+        ws_ptr, ws_bytes = (linked_workspace or _default_workspace(dev, linked=True)).get(need, dev, stream or 0)
     sl = _slices(a_stacks, b_stacks, out_cols)
     rc = lib.mlora_apply_grouped(
         x.data_ptr(), x.stride(0), x.shape[0], in_dim, sl, n, r_max, out.data_ptr(), out.stride(0), ctypes.byref(m),
-        dt, ws_ptr, ws_bytes, int(mode), int(phases), _ffi.stream_ptr(dev),
+        dt, ws_ptr, ws_bytes, int(mode), int(phases), stream,
     )
     del keep
     if rc == -2:

@@ -91,3 +91,23 @@ def test_errors_map_to_reference_exception_types():
         m = _meta()
         rc = _ffi.lib().mlora_expand(None, 4, 4, _ffi.SliceArray(), 1, 8, None, 16, ctypes.byref(m), _ffi.MLORA_BF16, None)
         _ffi.check(rc, "mlora_expand")
+
+
+def test_grouped_workspace_sizes():
+    """Workspace sizes are host arithmetic: K chunks of 256 x rows x columns,
+    fp32 for two launches; 64-bit words plus a 256-byte header for the single
+    launch; 0 for ineligible shapes."""
+    lib = _ffi.lib()
+    bf = _ffi.MLORA_BF16
+    kc = 4096 // 256
+    two = lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 2)
+    assert two == kc * 128 * 16 * 4
+    one = lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 1)
+    assert one == 256 + kc * 128 * 16 * 8
+    assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 0) == one
+    assert lib.mlora_grouped_workspace_bytes(4104, 16, 3, 10, 65, bf, 1) == 256 + 17 * 10 * 48 * 8
+    assert lib.mlora_grouped_workspace_bytes(4100, 16, 1, 10, 65, bf, 1) == 0                # in_dim % 8
+    assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, _ffi.MLORA_F32, 1) == 0   # fp32 not grouped
+    assert lib.mlora_grouped_workspace_bytes(4096, 72, 1, 128, 64, bf, 1) == 0               # r_max > 64
+    assert lib.mlora_grouped_workspace_bytes(4096, 12, 1, 128, 64, bf, 2) == 0               # r_max % 8
+    assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 3) == 0               # bad mode

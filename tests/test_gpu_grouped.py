@@ -4,14 +4,17 @@ The grouped path reads each referenced adapter once per call and finds the
 rows of every slot with an in-kernel scan of the segment table; its
 arithmetic per row equals shrink-then-expand up to the order of the fp32
 K-reduction, so it is held to the float64 tolerance and to one unit of the
-kernels' rounding sequence.
+kernels' rounding sequence.  The single-launch mode links its shrink and
+expand work items through words tagged per launch: calls in a row on one
+workspace, of any shapes, must each match the oracle, with the workspace's
+error word still zero.
 """
 
 import pytest
 import torch
 
 from multi_lora_amd import HipLoRABackend, synthetic
-from multi_lora_amd.kernels.lora_ops import Workspace, apply_grouped
+from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, Workspace, apply_grouped
 from multi_lora_amd.synthetic import make_meta
 from oracle.lora_ref import apply_f64, apply_kernel_numerics
 from oracle.metadata_ref import slot_gather_order
@@ -21,15 +24,25 @@ from tests.test_gpu_lora import cpu_meta, run_hip
 pytestmark = pytest.mark.gpu
 
 
-def grouped(wl, phases_split=False, mode=0):
+def assert_linked_clean(lws: LinkedWorkspace):
+    """No wait between linked work items timed out."""
+    torch.cuda.synchronize()
+    assert lws.error_word() == 0, "a wait between linked work items timed out"
+
+
+def grouped(wl, phases_split=False, mode=0, lws=None):
     out = wl.clone_base()
     ws = Workspace()
+    lws = lws if lws is not None else LinkedWorkspace()
     if phases_split:
         assert apply_grouped(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, out, wl.col_offsets, ws, phases=1, mode=2)
         assert apply_grouped(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, out, wl.col_offsets, ws, phases=2, mode=2)
     else:
-        assert apply_grouped(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, out, wl.col_offsets, ws, mode=mode)
+        assert apply_grouped(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, out, wl.col_offsets, ws, mode=mode,
+                             linked_workspace=lws)
     torch.cuda.synchronize()
+    if mode != 2 and not phases_split:
+        assert_linked_clean(lws)
     return out.cpu()
 
 
@@ -120,6 +133,63 @@ def test_many_rows_per_slot_and_multi_row_segments(dev):
         st += n
 
 
+def test_linked_workspace_reused_across_shapes(dev):
+    """One single-launch workspace serves calls of different row counts, slot
+    counts, slice counts and ranks in a row; each call matches the oracle
+    although the words of the calls before it are still in the workspace."""
+    lws = LinkedWorkspace()
+    cases = [
+        synthetic.decode_q(device=dev, tokens=128, seed=11),
+        synthetic.decode_q(device=dev, tokens=24, in_dim=1024, out=768, n_slots=8, n_adapters=5, rank=32, seed=12),
+        synthetic.decode_qkv(device=dev),
+        synthetic.decode_q(device=dev, tokens=200, in_dim=2048, out=512, n_slots=40, n_adapters=30, rank=8, seed=13),
+        synthetic.decode_q(device=dev, tokens=7, seed=14),
+    ]
+    for wl in cases:
+        got = grouped(wl, mode=1, lws=lws)
+        cm = cpu_meta(wl.meta)
+        xs, As, Bs = wl.x.cpu(), [a.cpu() for a in wl.a_stacks], [b.cpu() for b in wl.b_stacks]
+        assert_ulp_close(got, apply_kernel_numerics(xs, As, Bs, cm, wl.base.cpu(), wl.col_offsets)[1], what=wl.name)
+
+
+def test_linked_repeated_calls_are_bit_identical(dev):
+    wl = synthetic.decode_q(device=dev, tokens=128, seed=21)
+    lws = LinkedWorkspace()
+    first = grouped(wl, mode=1, lws=lws)
+    for _ in range(5):
+        assert torch.equal(grouped(wl, mode=1, lws=lws), first)
+
+
+def test_linked_same_shape_new_inputs_each_call(dev):
+    """Calls of one shape in a row with new inputs: every word position still
+    holds the previous call's sum when the next call starts, and must not be
+    taken for the new one."""
+    lws = LinkedWorkspace()
+    for seed in range(30, 36):
+        wl = synthetic.decode_q(device=dev, tokens=128, seed=seed)
+        got = grouped(wl, mode=1, lws=lws)
+        cm = cpu_meta(wl.meta)
+        ref = apply_kernel_numerics(wl.x.cpu(), [wl.a_stacks[0].cpu()], [wl.b_stacks[0].cpu()], cm, wl.base.cpu())[1]
+        assert_ulp_close(got, ref, what=f"seed {seed}")
+
+
+def test_linked_workspace_keeps_streams_apart(dev):
+    """One LinkedWorkspace used from two streams holds one buffer per stream."""
+    lws = LinkedWorkspace()
+    wl = synthetic.decode_q(device=dev, tokens=64, seed=41)
+    ref = grouped(wl, mode=1, lws=lws)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        out = wl.clone_base()
+        assert apply_grouped(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, out, wl.col_offsets, mode=1,
+                             linked_workspace=lws)
+    torch.cuda.synchronize()
+    assert len(lws.bufs) == 2
+    assert torch.equal(out.cpu(), ref)
+    assert_linked_clean(lws)
+
+
 def test_ineligible_shapes_fall_back(dev):
     wl = synthetic.decode_q(device=dev, dtype=torch.float32, tokens=8, in_dim=256, out=256, n_slots=4, n_adapters=2,
                             rank=16)
@@ -166,6 +236,7 @@ def test_hip_graph_replays_match_eager_and_follow_metadata_rewrites(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+        assert_linked_clean(be.linked_workspace)
 
     # New slot assignment, written in place into the captured table.
     new_slots = [(s + 3) % 8 for s in wl.seg_slots]
@@ -181,3 +252,4 @@ def test_hip_graph_replays_match_eager_and_follow_metadata_rewrites(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager2)
+    assert_linked_clean(be.linked_workspace)

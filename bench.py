@@ -43,7 +43,100 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=2000, help="launches in each per-kernel timing")
+    ap.add_argument("--profile-traffic", action="store_true",
+                    help="launch only the headline kernel and a copy kernel of known size, for rocprofv3 --pmc runs")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn rocprofv3 FETCH_SIZE / WRITE_SIZE runs of --profile-traffic into the traffic file")
     return ap.parse_args()
+
+
+# --profile-traffic: the copy kernel used to calibrate the counters moves
+# COPY_ELEMS bf16 values (read once, written once).
+COPY_ELEMS = 32 << 20
+HEADLINE_KERNEL = "grouped_linked"
+TRAFFIC_FILE = ROOT / "profiles" / f"{HEADLINE_KERNEL}_decode_q_traffic.json"
+
+
+def profile_traffic(launches: int = 64, copies: int = 16) -> int:
+    """Headline kernel over rotating replicas, then a plain copy kernel."""
+    import torch
+
+    from multi_lora_amd import synthetic
+    from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, apply_grouped
+
+    dev = torch.device("cuda", 0)
+    host = synthetic.decode_q(device="cpu")
+    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+    reps = [(host.x.to(dev), host.a_stacks[0].to(dev), host.b_stacks[0].to(dev), host.base.to(dev)) for _ in range(32)]
+    lws = LinkedWorkspace()
+    for i in range(launches):
+        x, a, b, out = reps[i % len(reps)]
+        assert apply_grouped(x, [a], [b], meta, out, [0], mode=1, linked_workspace=lws)
+    torch.cuda.synchronize()
+    src = torch.randn(COPY_ELEMS, device=dev).bfloat16()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(copies):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"headline_launches": launches, "copy_launches": copies, "copy_bytes_each_way": COPY_ELEMS * 2}))
+    return 0
+
+
+def _pmc_means(directory: str, counter: str) -> dict:
+    """Mean per-dispatch value of `counter` for the headline and copy kernels."""
+    import csv
+
+    files = sorted(Path(directory).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    vals = {"headline": [], "copy": []}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                v = float(row["Counter_Value"])
+                if HEADLINE_KERNEL in name:
+                    vals["headline"].append(v)
+                elif "neg" in name:
+                    vals["copy"].append(v)
+    if not vals["headline"] or not vals["copy"]:
+        raise SystemExit(f"{counter}: kernels not found in {directory}")
+    return {k: sum(v) / len(v) for k, v in vals.items()} | {"dispatches": {k: len(v) for k, v in vals.items()}}
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+    fetch = _pmc_means(fetch_dir, "FETCH_SIZE")
+    write = _pmc_means(write_dir, "WRITE_SIZE")
+    copy_kib = COPY_ELEMS * 2 / 1024
+    f_scale = copy_kib / fetch["copy"]
+    w_scale = copy_kib / write["copy"]
+    fetch_b = fetch["headline"] * f_scale * 1024
+    write_b = write["headline"] * w_scale * 1024
+    out = {
+        "kernel": HEADLINE_KERNEL,
+        "workload": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters",
+        "hbm_bytes_per_launch": round(fetch_b + write_b),
+        "fetch_bytes_per_launch": round(fetch_b),
+        "write_bytes_per_launch": round(write_b),
+        "raw_kib_per_dispatch": {"FETCH_SIZE": fetch["headline"], "WRITE_SIZE": write["headline"]},
+        "copy_calibration": {
+            "bytes_each_way": COPY_ELEMS * 2,
+            "FETCH_SIZE_kib": fetch["copy"], "WRITE_SIZE_kib": write["copy"],
+            "fetch_scale": f_scale, "write_scale": w_scale,
+        },
+        "dispatches": {"FETCH_SIZE": fetch["dispatches"], "WRITE_SIZE": write["dispatches"]},
+        "commands": [
+            "timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d <FETCH_DIR> -f csv -- python3 bench.py --profile-traffic",
+            "timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d <WRITE_DIR> -f csv -- python3 bench.py --profile-traffic",
+            "python3 bench.py --summarize-pmc <FETCH_DIR> <WRITE_DIR>",
+        ],
+    }
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return 0
 
 
 def cpu_cores() -> int:
@@ -69,10 +162,15 @@ def cpu_model() -> str:
 
 def main() -> int:
     args = parse()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding of this path is design-only", file=sys.stderr)
         return 2
+
+    if args.profile_traffic:
+        return profile_traffic()
 
     import torch
 
@@ -161,9 +259,8 @@ def main() -> int:
     dom_name = "grouped_linked"
     dom = kernels[dom_name]
     traffic = None
-    tfile = ROOT / "profiles" / f"{dom_name}_decode_q_traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
 
     result = {
         "metric": METRIC,

@@ -43,11 +43,166 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-steps", type=int, default=2000, help="launches in each per-kernel timing")
+    ap.add_argument("--workload", choices=("decode_q",) + tuple(OTHER_WORKLOADS), default="decode_q",
+                    help="decode_q is the headline; the others print a line of the same form for their shape")
     ap.add_argument("--profile-traffic", action="store_true",
                     help="launch only the headline kernel and a copy kernel of known size, for rocprofv3 --pmc runs")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn rocprofv3 FETCH_SIZE / WRITE_SIZE runs of --profile-traffic into the traffic file")
     return ap.parse_args()
+
+
+OTHER_WORKLOADS = {
+    "prefill_gate_up": "prefill MLP gate|up 4096->2x14336, 8 segments of U[64,1024] tokens, ranks {16,32,64}, r_max 64",
+    "prefill_down": "prefill MLP down 14336->4096, 8 segments of U[64,1024] tokens, ranks {16,32,64}, r_max 64",
+    "decode_qkv": "RMSNorm then q|k|v 4096->[4096,1024,1024], 256 one-token segments, 256-slot pool, "
+                  "128 rank-32 adapters",
+}
+
+
+def time_graph(torch, g, calls: int, per_graph: int, stream) -> float:
+    """Milliseconds per call of a graph holding `per_graph` calls, replayed back to back."""
+    replays = max(1, calls // per_graph)
+    g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / (replays * per_graph)
+
+
+def capture(torch, fn, n: int):
+    """Graph of fn(0), ..., fn(n-1)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def bench_other(args) -> int:
+    """One line for a non-headline workload: the backend step and each of its kernels, graph-timed
+    over cold replicas (at least 600 MB in total, more than twice the 256 MB MALL)."""
+    import torch
+
+    from multi_lora_amd import HipLoRABackend, synthetic
+    from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, Workspace, apply_grouped, expand, shrink
+    from multi_lora_amd.kernels.rmsnorm import rmsnorm_fwd
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    name = args.workload
+    if name.startswith("prefill"):
+        host = synthetic.prefill_mlp(device="cpu", part=name.split("_", 1)[1])
+    else:
+        host = synthetic.decode_qkv(device="cpu")
+    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+    e = host.x.element_size()
+    rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + 2 * host.base.numel()) * e
+    n_rep = max(2, -(-600_000_000 // rep_bytes))
+    reps = []
+    for _ in range(n_rep):
+        reps.append((host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
+                     host.base.to(dev)))
+    S, in_dim, r_max, n = host.tokens, host.x.shape[1], host.a_stacks[0].shape[1], len(host.a_stacks)
+    cols = host.col_offsets
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(meta)
+    stream = torch.cuda.current_stream(dev)
+    lora_bytes = synthetic.algorithmic_bytes(host)
+    kernels = {}
+    calls = max(args.kernel_steps // 8, 4 * n_rep)
+
+    if name == "decode_qkv":
+        w = host.extra["norm_weight"].to(dev)
+        eps = host.extra["eps"]
+        xn = [torch.empty_like(r[0]) for r in reps]
+        norm_bytes = 2 * S * in_dim * e + in_dim * e
+        from multi_lora_amd import _ffi
+
+        lib = _ffi.lib()
+
+        def norm(i):
+            x = reps[i % n_rep][0]
+            _ffi.check(lib.mlora_rmsnorm(x.data_ptr(), x.stride(0), x.stride(0), 1, w.data_ptr(),
+                                         _ffi.dtype_code(w.dtype), xn[i % n_rep].data_ptr(), xn[i % n_rep].stride(0),
+                                         S, in_dim, eps, _ffi.dtype_code(x.dtype), _ffi.stream_ptr(dev)),
+                       "mlora_rmsnorm")
+
+        def lora(i):
+            _, a, b, out = reps[i % n_rep]
+            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=1,
+                                 linked_workspace=be.linked_workspace)
+
+        def step(i):
+            x, a, b, out = reps[i % n_rep]
+            y = rmsnorm_fwd(x, w, eps)
+            be.apply_lora_multi(y, a, b, out, cols)
+
+        total_bytes = lora_bytes + norm_bytes
+        parts = {"rmsnorm": (norm, norm_bytes), "grouped_linked (3 slices)": (lora, lora_bytes)}
+        path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-grouped, one linked launch)"
+    else:
+        mids = [torch.empty(S, n * r_max, dtype=host.x.dtype, device=dev) for _ in range(n_rep)]
+        ws = Workspace()
+        a_bytes = host.x.numel() * e + sum(host.slot_ranks[s] * in_dim * e * n for s in set(host.seg_slots))
+        b_bytes = lora_bytes - a_bytes
+
+        def sh(i):
+            x, a, _, _ = reps[i % n_rep]
+            shrink(x, a, meta, mids[i % n_rep], workspace=ws)
+
+        def ex(i):
+            _, _, b, out = reps[i % n_rep]
+            expand(mids[i % n_rep], b, meta, out, cols)
+
+        def step(i):
+            x, a, b, out = reps[i % n_rep]
+            be.apply_lora_multi(x, a, b, out, cols)
+
+        total_bytes = lora_bytes
+        parts = {"shrink": (sh, a_bytes), "expand": (ex, b_bytes)}
+        path = "HipLoRABackend.apply_lora_multi (segment shrink, then expand)"
+
+    for i in range(max(args.warmup // 10, 2 * n_rep)):
+        step(i)
+    torch.cuda.synchronize()
+    step_ms = time_graph(torch, capture(torch, step, n_rep), calls, n_rep, stream)
+    for k, (fn, nbytes) in parts.items():
+        ms = time_graph(torch, capture(torch, fn, n_rep), calls, n_rep, stream)
+        kernels[k] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9}
+    dom = max(kernels, key=lambda k: kernels[k]["us"])
+    fl = synthetic.flops(host)
+    result = {
+        "metric": METRIC,
+        "value": round(total_bytes / (step_ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": calls,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "us_per_step": step_ms * 1e3,
+        "tokens_per_s": S / (step_ms * 1e-3),
+        "tflops": fl / (step_ms * 1e-3) / 1e12,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": OTHER_WORKLOADS[name], "tokens": S, "segments": len(host.seg_lens),
+                   "algorithmic_bytes_per_step": total_bytes, "flops_per_step": fl, "replicas": n_rep,
+                   "timing": "HIP graph replay, HIP events on the launch stream", "path": path},
+        "kernels": kernels,
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(kernels[dom]["GB/s"], 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kernels[dom]["GB/s"] / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 # --profile-traffic: the copy kernel used to calibrate the counters moves
@@ -171,6 +326,8 @@ def main() -> int:
 
     if args.profile_traffic:
         return profile_traffic()
+    if args.workload != "decode_q":
+        return bench_other(args)
 
     import torch
 

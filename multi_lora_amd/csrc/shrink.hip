@@ -8,14 +8,16 @@
 // per-segment PyTorch path returns a zero-initialised tensor,
 // multi_lora/backend/torch_backend.py:30-48), so `mid` is fully defined.
 //
-// Work decomposition (one 256-thread workgroup = 4 wave64s):
-//   workgroup  = (segment, row tile of BM tokens, K split kz)
-//   wave       = 16 token rows (WM waves along M) x 1/WK of the K-steps
-//   MFMA tile  = 16 rank rows x 16 tokens, D[n][t] += A[n][k] * x[t][k]
-// The reduction runs in the MFMA accumulators; waves that share a tile are
-// summed through LDS in wave order.  When K is split over workgroups each
-// split stores fp32 sums and a second launch adds them in split order, so the
-// result is deterministic and no workgroup ever waits on another.
+// Work decomposition (one 256-thread workgroup = 4 wave64s); the MFMA tile
+// is 16 rank rows x 16 tokens, D[n][t] += A[n][k] * x[t][k]:
+//   short segments (<= 16 rows, shrink_kernel): workgroup = (segment, K
+//     split); the 4 waves take alternate K-steps of the same 16 rows and are
+//     summed through LDS in wave order.
+//   long segments (shrink_rows_kernel): workgroup = (segment, 64*RB-row
+//     tile, K split); each wave owns RB 16-row blocks and every rank block.
+// When K is split over workgroups each split stores fp32 sums and a second
+// launch adds them in split order, so the result is deterministic and no
+// workgroup ever waits on another.
 //
 // Loads in the K loop are unconditional: rows past the segment end or the
 // rank are clamped to a row that exists (their products are discarded), so a
@@ -26,6 +28,11 @@
 namespace mlora {
 
 namespace {
+
+// 16-row blocks per wave of the long-segment kernel, by the number of 16-row
+// A blocks: RB x NBT accumulator tiles stay at or below 16.
+template <int NBT>
+constexpr int kShrinkRb = NBT >= 16 ? 1 : (NBT >= 8 ? 2 : 4);
 
 template <class T>
 __device__ __forceinline__ void zero_mid_cols(const ShrinkArgs& a, int row0, int rows_here, int col_from) {
@@ -162,25 +169,170 @@ __global__ __launch_bounds__(256) void shrink_kernel(ShrinkArgs a) {
   if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, nb_act * 16);
 }
 
-// Sums the K splits of every live (row, column) in split order and rounds
-// once to the storage type.
-template <class T>
-__global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int bm) {
+template <class T, int RB, int NBT, bool AL>
+__device__ __forceinline__ void load_step(const typename T::raw_t* const (&xrow)[RB],
+                                          const typename T::raw_t* const (&arow)[NBT], int kk, u32x4 (&xv)[RB],
+                                          u32x4 (&av)[NBT]) {
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) xv[rb] = load_row_chunk<T, AL>(xrow[rb], kk, T::VEC);
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) av[j] = load_row_chunk<T, AL>(arow[j], kk, T::VEC);
+}
+
+template <class T, int RB, int NBT>
+__device__ __forceinline__ void mma_step(f32x4 (&acc)[RB][NBT], const u32x4 (&xv)[RB], const u32x4 (&av)[NBT]) {
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) acc[rb][j] = T::mma(acc[rb][j], av[j], xv[rb]);
+}
+
+// Long segments (prefill): workgroup = (segment, 64*RB-row tile, K split);
+// each wave owns RB 16-row blocks of the tile and every rank block, so x is
+// read once per workgroup and the A fragments, the same for all four waves,
+// come from L1.  No LDS and no barriers: waves run independently.
+template <class T, int NBT, int RB, bool AL>
+__global__ __launch_bounds__(256) void shrink_rows_kernel(ShrinkArgs a) {
   using raw = typename T::raw_t;
-  const int tile = blockIdx.x;
+  constexpr int BM = 64 * RB;
+  constexpr int VEC = T::VEC;
+  constexpr int KSTEP = T::KSTEP;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int bid = blockIdx.x;
+  const int kz = bid % a.ks;
+  const int tile = bid / a.ks;
   const int seg = tile / a.m_tiles;
   const int mt = tile - seg * a.m_tiles;
+
   const int start = max(a.meta.indptr[seg], 0);
   const int end = min(a.meta.indptr[seg + 1], a.rows);
-  const int row0 = start + mt * bm;
+  const int row0 = start + mt * BM;
   if (row0 >= end) return;
-  const int rows_here = min(bm, end - row0);
+  const int rows_here = min(BM, end - row0);
+
+  int slot, rank;
+  seg_slot_rank(a.meta, seg, a.r_max, a.rank_mult, &slot, &rank);
+  if (rank == 0) {
+    if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, 0);
+    return;
+  }
+  const int nb_act = (rank + 15) >> 4;
+  const int nbt = a.n_slices * nb_act;
+
+  const raw* arow[NBT];
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const int jj = j < nbt ? j : 0;
+    const int s = jj / nb_act;
+    arow[j] = slice_a<raw>(a.slices, s, slot, min((jj - s * nb_act) * 16 + r16, rank - 1));
+  }
+  const int wrow0 = row0 + wave * RB * 16;
+  const raw* xrow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+    xrow[rb] = static_cast<const raw*>(a.x) + static_cast<int64_t>(min(wrow0 + rb * 16 + r16, end - 1)) * a.x_stride;
+
+  f32x4 acc[RB][NBT];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) acc[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int kbeg = kz * a.k_per_split;
+  const int kend = min(a.in_dim, kbeg + a.k_per_split);
+  const int nfull = (kend - kbeg) / KSTEP;
+  // A wave whose row blocks all lie past the segment end has nothing to add.
+  // Two K-steps in flight per wave: step i+1's loads are issued before step
+  // i's MFMAs.  Every MFMA runs (blocks past the rank read a clamped row and
+  // are dropped at the store), so the loop body has no branches.
+  if (wrow0 < end && nfull > 0) {
+    u32x4 xv0[RB], av0[NBT], xv1[RB], av1[NBT];
+    load_step<T, RB, NBT, AL>(xrow, arow, kbeg + g * VEC, xv0, av0);
+    int i = 0;
+    // The scheduling barriers keep the compiler from sinking the next step's
+    // loads down to their first use, which would leave one step in flight.
+    for (; i + 2 <= nfull; i += 2) {
+      load_step<T, RB, NBT, AL>(xrow, arow, kbeg + (i + 1) * KSTEP + g * VEC, xv1, av1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step<T, RB, NBT>(acc, xv0, av0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_step<T, RB, NBT, AL>(xrow, arow, kbeg + min(i + 2, nfull - 1) * KSTEP + g * VEC, xv0, av0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step<T, RB, NBT>(acc, xv1, av1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < nfull) mma_step<T, RB, NBT>(acc, xv0, av0);
+  }
+  if (wrow0 < end && kbeg + nfull * KSTEP < kend) {
+    // Last, partial step of the reduction (in_dim not a multiple of KSTEP).
+    const int kk = kbeg + nfull * KSTEP + g * VEC;
+    const int valid = a.in_dim - kk;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const u32x4 xv = load_row_chunk<T, AL>(xrow[rb], kk, valid);
+#pragma unroll
+      for (int j = 0; j < NBT; ++j) acc[rb][j] = T::mma(acc[rb][j], load_row_chunk<T, AL>(arow[j], kk, valid), xv);
+    }
+  }
+
+  const int ncols = a.n_slices * a.r_max;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int t = wrow0 + rb * 16 + r16;
+    if (t >= end) continue;
+    raw* mrow = static_cast<raw*>(a.mid) + static_cast<int64_t>(t) * a.mid_stride;
+    float* prow = a.partials + (static_cast<int64_t>(kz) * a.rows + t) * ncols;
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) {
+      if (j >= nbt) break;
+      const int s = j / nb_act;
+      const int n = (j - s * nb_act) * 16 + 4 * g;
+      const int col = s * a.r_max + n;
+      f32x4 v = acc[rb][j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = (n + q < rank) ? v[q] : 0.f;
+      if (a.ks == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (n + q < a.r_max) mrow[col + q] = T::from_f32(v[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (n + q < a.r_max) prow[col + q] = v[q];
+      }
+    }
+  }
+  if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, nb_act * 16);
+}
+
+// Sums the K splits of every live (row, column) in split order and rounds
+// once to the storage type.  Workgroup = (segment, 16-row tile), whatever
+// the shrink's tile height, so the reduction is spread over many CUs.
+constexpr int kReduceRows = 16;
+
+template <class T>
+__global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int r_tiles) {
+  using raw = typename T::raw_t;
+  const int tile = blockIdx.x;
+  const int seg = tile / r_tiles;
+  const int mt = tile - seg * r_tiles;
+  const int start = max(a.meta.indptr[seg], 0);
+  const int end = min(a.meta.indptr[seg + 1], a.rows);
+  const int row0 = start + mt * kReduceRows;
+  if (row0 >= end) return;
+  const int rows_here = min(kReduceRows, end - row0);
   int slot, rank;
   seg_slot_rank(a.meta, seg, a.r_max, a.rank_mult, &slot, &rank);
   if (rank == 0) return;
   const int live = min(((rank + 15) >> 4) * 16, a.r_max);
   const int ncols = a.n_slices * a.r_max;
   const int per_row = a.n_slices * live;
+  const int64_t zs = static_cast<int64_t>(a.rows) * ncols;
   raw* mid = static_cast<raw*>(a.mid);
   for (int i = threadIdx.x; i < rows_here * per_row; i += blockDim.x) {
     const int r = i / per_row;
@@ -191,7 +343,6 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int bm
     const int col = s * a.r_max + n;
     // Independent loads issued together; added in split order.
     const float* p = a.partials + static_cast<int64_t>(t) * ncols + col;
-    const int64_t zs = static_cast<int64_t>(a.rows) * ncols;
     float v[16];
 #pragma unroll
     for (int z = 0; z < 16; ++z) v[z] = (z < a.ks) ? p[z * zs] : 0.f;
@@ -202,35 +353,42 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int bm
   }
 }
 
-template <class T, int WM, int NBT, bool AL>
-hipError_t launch_t(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+// Launches `kern` over every (segment, row tile, K split) and, when K is
+// split, the in-order reduction.
+template <class T>
+hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
   const int64_t tiles = static_cast<int64_t>(args.meta.bs) * p.m_tiles;
   if (tiles <= 0) return hipSuccess;
-  hipLaunchKernelGGL((shrink_kernel<T, WM, NBT, AL>), dim3(static_cast<unsigned>(tiles * p.ks)), dim3(256), 0,
-                     stream, args);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * p.ks)), dim3(256), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
-  hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, args,
-                     p.bm);
+  const int r_tiles = p.m_tiles * (p.bm / kReduceRows);
+  hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(args.meta.bs * int64_t{r_tiles})), dim3(256),
+                     0, stream, args, r_tiles);
   return hipGetLastError();
 }
 
-template <class T, int WM, bool AL>
-hipError_t launch_nbt(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+template <class T, int NBT, bool AL>
+hipError_t launch_nbt_al(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+  if (p.bm == 16) return launch_with<T>(shrink_kernel<T, 1, NBT, AL>, p, args, stream);
+  if (p.bm == 64 * kShrinkRb<NBT>) return launch_with<T>(shrink_rows_kernel<T, NBT, kShrinkRb<NBT>, AL>, p, args, stream);
+  return hipErrorInvalidValue;
+}
+
+template <class T, bool AL>
+hipError_t launch_al(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
   switch (p.nbt) {
-    case 1: return launch_t<T, WM, 1, AL>(p, args, stream);
-    case 2: return launch_t<T, WM, 2, AL>(p, args, stream);
-    case 4: return launch_t<T, WM, 4, AL>(p, args, stream);
-    case 8: return launch_t<T, WM, 8, AL>(p, args, stream);
-    default: return launch_t<T, WM, 16, AL>(p, args, stream);
+    case 1: return launch_nbt_al<T, 1, AL>(p, args, stream);
+    case 2: return launch_nbt_al<T, 2, AL>(p, args, stream);
+    case 4: return launch_nbt_al<T, 4, AL>(p, args, stream);
+    case 8: return launch_nbt_al<T, 8, AL>(p, args, stream);
+    default: return launch_nbt_al<T, 16, AL>(p, args, stream);
   }
 }
 
 template <class T>
 hipError_t launch_dtype(const ShrinkPlan& p, const ShrinkArgs& args, bool aligned, hipStream_t stream) {
-  if (p.bm == 16)
-    return aligned ? launch_nbt<T, 1, true>(p, args, stream) : launch_nbt<T, 1, false>(p, args, stream);
-  return aligned ? launch_nbt<T, 4, true>(p, args, stream) : launch_nbt<T, 4, false>(p, args, stream);
+  return aligned ? launch_al<T, true>(p, args, stream) : launch_al<T, false>(p, args, stream);
 }
 
 }  // namespace
@@ -245,12 +403,14 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
   p.nbt = 1;
   while (p.nbt < blocks) p.nbt *= 2;
   if (p.nbt > 16) return false;
-  p.bm = (max_len <= 16) ? 16 : 64;
+  const int rb = p.nbt >= 16 ? 1 : (p.nbt >= 8 ? 2 : 4);  // kShrinkRb
+  p.bm = (max_len <= 16) ? 16 : 64 * rb;
   p.m_tiles = cdiv(max_len > 0 ? max_len : 1, p.bm);
   const int ksteps = cdiv(in_dim, kstep);
   const int64_t base = static_cast<int64_t>(bs) * p.m_tiles;
-  // Enough workgroups to cover the chip, with at least a few K-steps per wave.
-  const int min_steps = (p.bm == 16) ? 16 : 4;
+  // Enough workgroups to cover the chip twice, with enough K-steps per split
+  // to keep the loads streaming.
+  const int min_steps = (p.bm == 16) ? 16 : 8;
   int ks = 1;
   while (ks < 16 && base * ks < 2LL * num_cus && cdiv(ksteps, ks * 2) >= min_steps) ks *= 2;
   const int steps_per_split = cdiv(ksteps, ks);

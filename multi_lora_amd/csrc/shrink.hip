@@ -29,10 +29,10 @@ namespace mlora {
 
 namespace {
 
-// 16-row blocks per wave of the long-segment kernel, by the number of 16-row
-// A blocks: RB x NBT accumulator tiles stay at or below 16.
+// 16-row blocks per wave of the long-segment kernels, by the number of
+// 16-row A blocks (keeps the LDS tiles of shrink_lds_kernel within 70 KB).
 template <int NBT>
-constexpr int kShrinkRb = NBT >= 16 ? 1 : (NBT >= 8 ? 2 : 4);
+constexpr int kShrinkRb = NBT >= 8 ? 1 : 2;
 
 template <class T>
 __device__ __forceinline__ void zero_mid_cols(const ShrinkArgs& a, int row0, int rows_here, int col_from) {
@@ -310,6 +310,147 @@ __global__ __launch_bounds__(256) void shrink_rows_kernel(ShrinkArgs a) {
   if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, nb_act * 16);
 }
 
+// Long segments, 16-bit types, 16-byte aligned rows: x and A tiles staged
+// through LDS.  A stage is 64*RB rows x kLdsKt reduction elements; each row's
+// 2*kLdsKt bytes are read by 16 consecutive lanes, so every row is streamed
+// in 256-byte pieces rather than the 64-byte pieces that MFMA-layout loads
+// give.  The next stage's loads are in flight in registers while the waves
+// run the current stage's MFMAs from LDS.  Wave w owns rows
+// [w*16*RB, (w+1)*16*RB) of the tile and every rank block.
+constexpr int kLdsKt = 128;             // reduction elements per stage
+constexpr int kLdsStride = kLdsKt + 8;  // LDS row stride (elements): 16-byte pad, conflict-free fragment reads
+
+template <class T, int NBT, int RB>
+__global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
+  using raw = typename T::raw_t;
+  static_assert(sizeof(raw) == 2, "16-bit types only");
+  constexpr int BM = 64 * RB;
+  constexpr int NA = NBT * 16;
+  constexpr int CPR = kLdsKt / 8;     // 16-byte chunks per row per stage
+  constexpr int XC = BM * CPR / 256;  // x chunks per thread per stage
+  constexpr int AC = NA * CPR / 256;  // A chunks per thread per stage
+  static_assert(XC >= 1 && AC >= 1, "tile too small for 256 threads");
+  __shared__ __attribute__((aligned(16))) raw xs[BM * kLdsStride];
+  __shared__ __attribute__((aligned(16))) raw as[NA * kLdsStride];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int bid = blockIdx.x;
+  const int kz = bid % a.ks;
+  const int tile = bid / a.ks;
+  const int seg = tile / a.m_tiles;
+  const int mt = tile - seg * a.m_tiles;
+
+  const int start = max(a.meta.indptr[seg], 0);
+  const int end = min(a.meta.indptr[seg + 1], a.rows);
+  const int row0 = start + mt * BM;
+  if (row0 >= end) return;
+  const int rows_here = min(BM, end - row0);
+
+  int slot, rank;
+  seg_slot_rank(a.meta, seg, a.r_max, a.rank_mult, &slot, &rank);
+  if (rank == 0) {
+    if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, 0);
+    return;
+  }
+  const int nb_act = (rank + 15) >> 4;
+  const int nbt = a.n_slices * nb_act;
+
+  // Source rows of this thread's chunks (clamped into the segment / rank).
+  // Chunk i of this thread is row tid/CPR + i*(256/CPR) of the tile, at
+  // column (tid % CPR) * 8 of the stage.
+  const int col = (tid % CPR) * 8;
+  const raw* xsrc[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i)
+    xsrc[i] = static_cast<const raw*>(a.x) +
+              static_cast<int64_t>(min(row0 + (tid + i * 256) / CPR, end - 1)) * a.x_stride;
+  const raw* asrc[AC];
+#pragma unroll
+  for (int i = 0; i < AC; ++i) {
+    const int ar = (tid + i * 256) / CPR;
+    const int j = min(ar >> 4, nbt - 1);
+    const int s = j / nb_act;
+    asrc[i] = slice_a<raw>(a.slices, s, slot, min((j - s * nb_act) * 16 + (ar & 15), rank - 1));
+  }
+
+  const int kbeg = kz * a.k_per_split;
+  const int kend = min(a.in_dim, kbeg + a.k_per_split);
+  const int nst = (kend - kbeg + kLdsKt - 1) / kLdsKt;
+
+  u32x4 xr[XC], ar[AC];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < XC; ++i) xr[i] = load_row_chunk<T, true>(xsrc[i], k0 + col, kend - (k0 + col));
+#pragma unroll
+    for (int i = 0; i < AC; ++i) ar[i] = load_row_chunk<T, true>(asrc[i], k0 + col, kend - (k0 + col));
+  };
+
+  f32x4 acc[RB][NBT];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) acc[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  fetch(kbeg);
+  for (int st = 0; st < nst; ++st) {
+#pragma unroll
+    for (int i = 0; i < XC; ++i) *reinterpret_cast<u32x4*>(xs + ((tid + i * 256) / CPR) * kLdsStride + col) = xr[i];
+#pragma unroll
+    for (int i = 0; i < AC; ++i) *reinterpret_cast<u32x4*>(as + ((tid + i * 256) / CPR) * kLdsStride + col) = ar[i];
+    __syncthreads();
+    if (st + 1 < nst) fetch(kbeg + (st + 1) * kLdsKt);
+#pragma unroll
+    for (int ks = 0; ks < kLdsKt / 32; ++ks) {
+      const int kk = ks * 32 + g * 8;
+      u32x4 xf[RB], af[NBT];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        xf[rb] = *reinterpret_cast<const u32x4*>(xs + (wave * RB * 16 + rb * 16 + r16) * kLdsStride + kk);
+#pragma unroll
+      for (int j = 0; j < NBT; ++j) af[j] = *reinterpret_cast<const u32x4*>(as + (j * 16 + r16) * kLdsStride + kk);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int j = 0; j < NBT; ++j) acc[rb][j] = T::mma(acc[rb][j], af[j], xf[rb]);
+    }
+    __syncthreads();
+  }
+
+  const int ncols = a.n_slices * a.r_max;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int t = row0 + wave * RB * 16 + rb * 16 + r16;
+    if (t >= end) continue;
+    raw* mrow = static_cast<raw*>(a.mid) + static_cast<int64_t>(t) * a.mid_stride;
+    float* prow = a.partials + (static_cast<int64_t>(kz) * a.rows + t) * ncols;
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) {
+      if (j >= nbt) break;
+      const int s = j / nb_act;
+      const int n = (j - s * nb_act) * 16 + 4 * g;
+      const int col = s * a.r_max + n;
+      f32x4 v = acc[rb][j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = (n + q < rank) ? v[q] : 0.f;
+      if (a.ks == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (n + q < a.r_max) mrow[col + q] = T::from_f32(v[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (n + q < a.r_max) prow[col + q] = v[q];
+      }
+    }
+  }
+  if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, nb_act * 16);
+}
+
 // Sums the K splits of every live (row, column) in split order and rounds
 // once to the storage type.  Workgroup = (segment, 16-row tile), whatever
 // the shrink's tile height, so the reduction is spread over many CUs.
@@ -370,9 +511,12 @@ hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const Shri
 
 template <class T, int NBT, bool AL>
 hipError_t launch_nbt_al(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+  constexpr int RB = kShrinkRb<NBT>;
   if (p.bm == 16) return launch_with<T>(shrink_kernel<T, 1, NBT, AL>, p, args, stream);
-  if (p.bm == 64 * kShrinkRb<NBT>) return launch_with<T>(shrink_rows_kernel<T, NBT, kShrinkRb<NBT>, AL>, p, args, stream);
-  return hipErrorInvalidValue;
+  if (p.bm != 64 * RB) return hipErrorInvalidValue;
+  if constexpr (AL && sizeof(typename T::raw_t) == 2 && NBT <= 8)
+    return launch_with<T>(shrink_lds_kernel<T, NBT, RB>, p, args, stream);
+  return launch_with<T>(shrink_rows_kernel<T, NBT, RB, AL>, p, args, stream);
 }
 
 template <class T, bool AL>
@@ -403,16 +547,25 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
   p.nbt = 1;
   while (p.nbt < blocks) p.nbt *= 2;
   if (p.nbt > 16) return false;
-  const int rb = p.nbt >= 16 ? 1 : (p.nbt >= 8 ? 2 : 4);  // kShrinkRb
+  const int rb = p.nbt >= 8 ? 1 : 2;  // kShrinkRb
   p.bm = (max_len <= 16) ? 16 : 64 * rb;
   p.m_tiles = cdiv(max_len > 0 ? max_len : 1, p.bm);
   const int ksteps = cdiv(in_dim, kstep);
   const int64_t base = static_cast<int64_t>(bs) * p.m_tiles;
-  // Enough workgroups to cover the chip twice, with enough K-steps per split
-  // to keep the loads streaming.
-  const int min_steps = (p.bm == 16) ? 16 : 8;
   int ks = 1;
-  while (ks < 16 && base * ks < 2LL * num_cus && cdiv(ksteps, ks * 2) >= min_steps) ks *= 2;
+  if (p.bm == 16) {
+    // Decode-shaped rows: enough workgroups to cover the chip twice.
+    while (ks < 16 && base * ks < 2LL * num_cus && cdiv(ksteps, ks * 2) >= 16) ks *= 2;
+  } else {
+    // Long segments: up to three workgroups per CU, at least 512 reduction
+    // elements per split, and split sums (written and read back as fp32,
+    // 8 bytes per column and split) costing at most half the x bytes.
+    const int ncols = n_slices * r_max;
+    const int64_t x_row_bytes = static_cast<int64_t>(in_dim) * (dtype == MLORA_F32 ? 4 : 2);
+    while (ks < 16 && base * ks < 3LL * num_cus && cdiv(ksteps, ks * 2) * kstep >= 512 &&
+           static_cast<int64_t>(ks * 2) * ncols * 8 <= x_row_bytes / 2)
+      ks *= 2;
+  }
   const int steps_per_split = cdiv(ksteps, ks);
   p.k_per_split = steps_per_split * kstep;
   p.ks = cdiv(ksteps, steps_per_split);

@@ -112,10 +112,11 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
                  const mlora_seg_meta* meta, int32_t dtype, void* stream);
 
 /* Bytes of workspace mlora_apply_grouped needs for this shape and `mode`;
- * 0 when the shape is not eligible (or mode is not 0..2).  Two launches: fp32
- * sums of each 256-wide K chunk for every row and slice.  Single launch: a
- * 256-byte header (error word) and the same sums as 64-bit tagged words.
- * `num_slots` is accepted for layouts that depend on it; none does now. */
+ * 0 when the shape is not eligible (or mode is not 0..2).  mode 2 (two
+ * launches): fp32 sums of each 256-wide K chunk for every row and slice.
+ * modes 1 and 0: a 256-byte header (error word) and the same sums as 64-bit
+ * tagged words.  `num_slots` is accepted for layouts that depend on it; none
+ * does now. */
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
                                      int32_t num_slots, int32_t dtype, int32_t mode);
 
@@ -129,13 +130,17 @@ size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_sl
  * carries fp32 K-chunk sums and may be any scratch);
  * 1 = single launch (expand items wait, with a bounded spin, on the sums
  * the shrink items of the same launch publish, each tagged with the launch's
- * dispatch id on its hardware queue).  The single-launch workspace must be
- * zero-filled before its first use, passed to nothing but mode 0/1 calls
- * afterwards, and used from one stream only (give each stream its own); it
- * is never cleared between calls.  Its first int32 is a sticky error word
- * that becomes non-zero if a wait ever timed out (results of that launch are
- * then unreliable).  Calls sharing a workspace must not overlap.
- * 0 = the library's choice (currently the single launch).
+ * dispatch id on its hardware queue);
+ * 0 = the library's choice per call: the single launch while all work items
+ * fit on the chip at once (num_slots * items per slot <= 16 per CU), else
+ * two launches that pass their sums as words tagged 0 in the same workspace
+ * (single-launch tags are odd, so neither schedule mistakes the other's).
+ * The workspace of modes 0 and 1 must be zero-filled before its first use,
+ * passed to nothing but calls of the same mode afterwards, and used from one
+ * stream only (give each stream its own); it is never cleared between calls.
+ * Its first int32 is a sticky error word that becomes non-zero if a wait ever
+ * timed out (results of that launch are then unreliable).  Calls sharing a
+ * workspace must not overlap.
  * `phases` (two-launch mode only; must be 3 otherwise): 1 = shrink half
  * (leaves its sums in the workspace), 2 = expand half (consumes them), 3 = both.
  * Requirements (else -2 and nothing launched): bf16 or fp16; r_max <= 64 and

@@ -46,10 +46,6 @@ int num_cus() {
   return cached[dev];
 }
 
-// The ABI's grouped `mode` (0 = library's choice) to a schedule.  The
-// library picks the single launch.
-int grouped_schedule(int mode) { return mode == 2 ? mlora::kGroupTwo : mlora::kGroupLinked; }
-
 int check_meta(const mlora_seg_meta* m) {
   if (m == nullptr) return fail(kBadArg, "segment metadata is null");
   if (m->bs < 0 || m->max_len < 0 || m->num_slots < 0)
@@ -206,12 +202,13 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
 
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
                                      int32_t num_slots, int32_t dtype, int32_t mode) {
-  int kc, k_chunk, nbt;
-  size_t ws = 0;
+  (void)num_slots;
+  int kc, k_chunk, nbt, s_groups;
+  size_t linked = 0, plain = 0;
   if (mode < 0 || mode > 2) return 0;
-  const int m = grouped_schedule(mode);
-  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, num_slots, dtype, m, &kc, &k_chunk, &nbt, &ws)) return 0;
-  return ws;
+  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &s_groups, &linked, &plain))
+    return 0;
+  return (mode == mlora::kGroupTwo) ? plain : linked;
 }
 
 int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
@@ -229,13 +226,14 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   if (mode < 0 || mode > 2) return fail(kBadArg, "mode %d not in 0..2", mode);
   if (meta->bs == 0 || num_rows == 0 || meta->num_slots == 0) return 0;
   if (x == nullptr || out == nullptr) return fail(kBadArg, "x or out is null");
-  const int m = grouped_schedule(mode);
-  if (m == mlora::kGroupLinked && phases != 3) return fail(kBadArg, "the single-launch path has one phase (use phases=3)");
-  int kc, k_chunk, nbt;
-  size_t ws = 0;
-  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, meta->num_slots, dtype, m, &kc, &k_chunk, &nbt, &ws))
+  if (mode != mlora::kGroupTwo && phases != 3)
+    return fail(kBadArg, "phases %d: only the two-launch mode runs one half (use phases=3)", phases);
+  int kc, k_chunk, nbt, s_groups;
+  size_t linked = 0, plain = 0;
+  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &s_groups, &linked, &plain))
     return fail(kUnsupported, "grouped path needs bf16/fp16, r_max <= %d and a multiple of 8, in_dim a multiple of 8",
                 mlora::kGroupMaxRank);
+  const size_t ws = (mode == mlora::kGroupTwo) ? plain : linked;
   if (workspace == nullptr || workspace_bytes < ws)
     return fail(kWorkspace, "grouped workspace too small: need %zu bytes, got %zu", ws, workspace_bytes);
   const int vec = vec_elems(dtype);
@@ -269,9 +267,16 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   args.out = out;
   args.out_stride = out_row_stride;
   args.meta = seg_view(meta);
+  int m = mode;
+  if (m == mlora::kGroupAuto) {
+    const int64_t items = static_cast<int64_t>(meta->num_slots) * (s_groups * kc + tiles);
+    m = (items <= static_cast<int64_t>(mlora::kLinkedItemsPerCu) * num_cus()) ? mlora::kGroupLinked : mlora::kGroupTwo;
+  }
   args.partials = static_cast<float*>(workspace);
+  args.word64 = (mode == mlora::kGroupAuto && m == mlora::kGroupTwo) ? 1 : 0;
   args.kc = kc;
   args.k_chunk = k_chunk;
+  args.s_groups = s_groups;
   args.n_tiles = tiles;
   const hipError_t e = mlora::launch_grouped(args, dtype, nbt, m, phases, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "grouped launch");

@@ -55,6 +55,10 @@ namespace mlora {
 
 namespace {
 
+// How shrink items pass their K-chunk sums to expand items.
+constexpr int kSumF32 = 0;     // two launches: fp32 words
+constexpr int kSumWord0 = 1;   // two launches on a single-launch workspace: 64-bit words tagged 0
+constexpr int kSumLinked = 2;  // one launch: 64-bit words tagged with the launch, polled
 constexpr int kSpinLimit = 1 << 20;   // polls before an expand item gives up
 constexpr int kPollBatch = 16;        // K-chunk words requested together
 
@@ -125,8 +129,11 @@ __device__ __forceinline__ LinkedView linked_view(const GroupedArgs& a) {
   return LinkedView{reinterpret_cast<int*>(base), reinterpret_cast<uint64_t*>(base + kLinkedHeader)};
 }
 
-template <class T, int NBT, bool LINKED>
-__device__ void shrink_item(const GroupedArgs& a, int slot, int c, int* s_rows, int* s_tmp, f32x4 (*red)[kWave]) {
+// Shrink item (slot, slice group sg, K chunk c).  With a.s_groups == 1 the
+// item covers every slice; otherwise slice sg only.
+template <class T, int NBT, int FMT>
+__device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* s_rows, int* s_tmp,
+                            f32x4 (*red)[kWave]) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   constexpr int KSTEP = T::KSTEP;
@@ -142,7 +149,8 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int c, int* s_rows, 
   const int rank = slot_rank(a, slot);
   if (rank == 0) return;
   const int nb_act = (rank + 15) >> 4;
-  const int nbt = a.n_slices * nb_act;
+  const int s_first = (a.s_groups == 1) ? 0 : sg;
+  const int nbt = ((a.s_groups == 1) ? a.n_slices : 1) * nb_act;
   const int kbeg = c * a.k_chunk;
 
   // This wave's A fragments for the chunk, kept for every row tile.
@@ -150,8 +158,8 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int c, int* s_rows, 
 #pragma unroll
   for (int j = 0; j < NBT; ++j) {
     const int jj = j < nbt ? j : 0;
-    const int s = jj / nb_act;
-    const raw* arow = slice_a<raw>(a.slices, s, slot, min((jj - s * nb_act) * 16 + r16, rank - 1));
+    const int sl = jj / nb_act;  // slice within the item
+    const raw* arow = slice_a<raw>(a.slices, s_first + sl, slot, min((jj - sl * nb_act) * 16 + r16, rank - 1));
 #pragma unroll
     for (int sp = 0; sp < kGroupSteps; ++sp) {
       const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
@@ -184,7 +192,8 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int c, int* s_rows, 
       }
       __syncthreads();
       if (wave == 0) {
-#pragma unroll
+        // One wave's sums at a time keeps the register peak at two sets.
+#pragma unroll 1
         for (int w2 = 0; w2 < 3; ++w2)
 #pragma unroll
           for (int j = 0; j < NBT; ++j)
@@ -194,15 +203,21 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int c, int* s_rows, 
 #pragma unroll
           for (int j = 0; j < NBT; ++j) {
             if (j >= nbt) break;
-            const int s = j / nb_act;
-            const int n = (j - s * nb_act) * 16 + 4 * g;
+            const int sl = j / nb_act;  // slice within the item
+            const int s = s_first + sl;
+            const int n = (j - sl * nb_act) * 16 + 4 * g;
             if (n >= a.r_max) continue;
-            if constexpr (LINKED) {
+            if constexpr (FMT == kSumLinked) {
               uint64_t* p = linked_view(a).sums + rowoff + s * a.r_max + n;
               const uint32_t tag = launch_tag();
 #pragma unroll
               for (int q = 0; q < 4; ++q)
                 __hip_atomic_store(p + q, tagged(tag, acc[j][q]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else if constexpr (FMT == kSumWord0) {
+              // Tag 0 is even: no single launch's (odd) tag ever matches it.
+              uint64_t* p = linked_view(a).sums + rowoff + s * a.r_max + n;
+#pragma unroll
+              for (int q = 0; q < 4; ++q) p[q] = tagged(0u, acc[j][q]);
             } else {
               *reinterpret_cast<f32x4*>(a.partials + rowoff + s * a.r_max + n) = acc[j];
             }
@@ -235,12 +250,12 @@ __device__ uint64_t wait_word(const LinkedView& lv, const uint64_t* p, uint32_t 
 // (row, column) at word `idx`; chunk z's word sits at idx + z * zstride.  In
 // the linked schedule every word's tag is checked, and a word that has not
 // arrived yet is waited for.
-template <bool LINKED>
+template <int FMT>
 __device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, int64_t zstride) {
   float sum = 0.f;
   for (int z0 = 0; z0 < a.kc; z0 += kPollBatch) {
     float v[kPollBatch];
-    if constexpr (LINKED) {
+    if constexpr (FMT == kSumLinked) {
       const LinkedView lv = linked_view(a);
       const uint32_t tag = launch_tag();
       const uint64_t* p = lv.sums + idx;
@@ -254,6 +269,11 @@ __device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, in
         if (static_cast<uint32_t>(w[u] >> 32) != tag) w[u] = wait_word(lv, p + (z0 + u) * zstride, tag);
 #pragma unroll
       for (int u = 0; u < kPollBatch; ++u) v[u] = __uint_as_float(static_cast<uint32_t>(w[u]));
+    } else if constexpr (FMT == kSumWord0) {
+      const uint64_t* p = linked_view(a).sums + idx;
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u)
+        v[u] = (z0 + u < a.kc) ? __uint_as_float(static_cast<uint32_t>(p[(z0 + u) * zstride])) : 0.f;
     } else {
       const float* p = a.partials + idx;
 #pragma unroll
@@ -274,7 +294,7 @@ struct ExpandLds {
   int tmp[4];
 };
 
-template <class T, bool LINKED>
+template <class T, int FMT>
 __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<T>& lds) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -334,15 +354,14 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
         ov[i] = load_row_chunk<T, true>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
       }
       const int rows_here = min(16, cnt - tt);
-      if constexpr (LINKED) {
+      if constexpr (FMT == kSumLinked) {
         // Light polling first: one lane per K chunk waits for the word its
-        // shrink item stores last for this tile (last row, last live column
-        // of the last slice); the full read below then rarely finds a word
+        // shrink item stores last for this tile and slice (last row, last
+        // live column); the full read below then rarely finds a word
         // missing.  Polling every word would flood the memory system the
         // shrink items are reading from.
         if (wave == 0) {
-          const int64_t sidx = static_cast<int64_t>(lds.rows[tt + rows_here - 1]) * ncols +
-                               (a.n_slices - 1) * a.r_max + live - 1;
+          const int64_t sidx = static_cast<int64_t>(lds.rows[tt + rows_here - 1]) * ncols + s * a.r_max + live - 1;
           const LinkedView lv = linked_view(a);
           const uint32_t tag = launch_tag();
           for (int z = lane; z < a.kc; z += kWave) wait_word(lv, lv.sums + z * zstride + sidx, tag);
@@ -356,7 +375,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
         const int yc = idx - yr * a.r_max;
         float v = 0.f;
         if (yr < rows_here && yc < live)
-          v = chunk_sum<LINKED>(a, static_cast<int64_t>(lds.rows[tt + yr]) * ncols + s * a.r_max + yc, zstride);
+          v = chunk_sum<FMT>(a, static_cast<int64_t>(lds.rows[tt + yr]) * ncols + s * a.r_max + yc, zstride);
         lds.ytile[yr * YS + yc] = T::from_f32(yc < rank ? v : 0.f);
       }
       __syncthreads();
@@ -401,20 +420,22 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
 
 }
 
-template <class T, int NBT>
+template <class T, int NBT, int FMT>
 __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
   __shared__ int s_rows[kGroupRows];
   __shared__ int s_tmp[4];
   __shared__ f32x4 red[3 * NBT][kWave];
-  const int slot = blockIdx.x / a.kc;
-  shrink_item<T, NBT, false>(a, slot, blockIdx.x - slot * a.kc, s_rows, s_tmp, red);
+  const int per_slot = a.s_groups * a.kc;
+  const int slot = blockIdx.x / per_slot;
+  const int rem = blockIdx.x - slot * per_slot;
+  shrink_item<T, NBT, FMT>(a, slot, rem / a.kc, rem % a.kc, s_rows, s_tmp, red);
 }
 
-template <class T>
-__global__ __launch_bounds__(256) void grouped_expand_kernel(GroupedArgs a) {
+template <class T, int FMT>
+__global__ __launch_bounds__(256, 4) void grouped_expand_kernel(GroupedArgs a) {
   __shared__ __attribute__((aligned(16))) ExpandLds<T> lds;
   const int slot = blockIdx.x / a.n_tiles;
-  expand_item<T, false>(a, slot, blockIdx.x - slot * a.n_tiles, lds);
+  expand_item<T, FMT>(a, slot, blockIdx.x - slot * a.n_tiles, lds);
 }
 
 // Shrink items are workgroups [0, num_slots * kc); expand items follow.
@@ -425,21 +446,23 @@ template <class T, int NBT>
 __global__ __launch_bounds__(256, NBT >= 8 ? 1 : 4) void grouped_linked_kernel(GroupedArgs a) {
   __shared__ __attribute__((aligned(16))) ExpandLds<T> lds;
   __shared__ f32x4 red[3 * NBT][kWave];
-  const int ns = a.meta.num_slots * a.kc;
+  const int per_slot = a.s_groups * a.kc;
+  const int ns = a.meta.num_slots * per_slot;
   const int b = blockIdx.x;
   if (b < ns) {
-    const int slot = b / a.kc;
-    shrink_item<T, NBT, true>(a, slot, b - slot * a.kc, lds.rows, lds.tmp, red);
+    const int slot = b / per_slot;
+    const int rem = b - slot * per_slot;
+    shrink_item<T, NBT, kSumLinked>(a, slot, rem / a.kc, rem % a.kc, lds.rows, lds.tmp, red);
   } else {
     const int e = b - ns;
     const int slot = e / a.n_tiles;
-    expand_item<T, true>(a, slot, e - slot * a.n_tiles, lds);
+    expand_item<T, kSumLinked>(a, slot, e - slot * a.n_tiles, lds);
   }
 }
 
 template <class T, int NBT>
 hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t stream) {
-  const int64_t g1 = static_cast<int64_t>(args.meta.num_slots) * args.kc;
+  const int64_t g1 = static_cast<int64_t>(args.meta.num_slots) * args.s_groups * args.kc;
   const int64_t g2 = static_cast<int64_t>(args.meta.num_slots) * args.n_tiles;
   if (g1 <= 0 || g2 <= 0) return hipSuccess;
   if (mode == kGroupLinked) {
@@ -448,12 +471,22 @@ hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t s
     return hipGetLastError();
   }
   if (phases & 1) {
-    hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT>), dim3(static_cast<unsigned>(g1)), dim3(256), 0, stream, args);
+    if (args.word64)
+      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumWord0>), dim3(static_cast<unsigned>(g1)), dim3(256), 0,
+                         stream, args);
+    else
+      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumF32>), dim3(static_cast<unsigned>(g1)), dim3(256), 0,
+                         stream, args);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (phases & 2) {
-    hipLaunchKernelGGL((grouped_expand_kernel<T>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream, args);
+    if (args.word64)
+      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumWord0>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
+                         args);
+    else
+      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumF32>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
+                         args);
     return hipGetLastError();
   }
   return hipSuccess;
@@ -465,30 +498,30 @@ hipError_t launch_dtype(const GroupedArgs& args, int nbt, int mode, int phases, 
     case 1: return launch_t<T, 1>(args, mode, phases, stream);
     case 2: return launch_t<T, 2>(args, mode, phases, stream);
     case 4: return launch_t<T, 4>(args, mode, phases, stream);
-    case 8: return launch_t<T, 8>(args, mode, phases, stream);
-    default: return launch_t<T, 16>(args, mode, phases, stream);
+    default: return launch_t<T, 4>(args, mode, phases, stream);
   }
 }
 
 }  // namespace
 
-bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int num_slots, int dtype, int mode, int* kc,
-                  int* k_chunk, int* nbt, size_t* ws_bytes) {
+bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
+                  int* s_groups, size_t* linked_bytes, size_t* plain_bytes) {
   if (dtype != MLORA_BF16 && dtype != MLORA_F16) return false;
-  if (in_dim <= 0 || rows <= 0 || num_slots < 0 || n_slices < 1 || n_slices > kMaxSlices) return false;
+  if (in_dim <= 0 || rows <= 0 || n_slices < 1 || n_slices > kMaxSlices) return false;
   if (r_max <= 0 || r_max > kGroupMaxRank || r_max % 8 != 0 || in_dim % 8 != 0) return false;
+  // More than four 16-row A blocks in all: one shrink item per slice, so an
+  // item never holds more than four blocks of A fragments.
   const int blocks = n_slices * cdiv(r_max, 16);
+  *s_groups = (blocks > 4) ? n_slices : 1;
+  const int item_blocks = blocks / *s_groups;
   int b = 1;
-  while (b < blocks) b *= 2;
-  if (b > 16) return false;
+  while (b < item_blocks) b *= 2;
   *nbt = b;
   *k_chunk = 4 * kGroupSteps * BF16::KSTEP;
   *kc = cdiv(in_dim, *k_chunk);
   const size_t words = static_cast<size_t>(*kc) * rows * n_slices * r_max;
-  if (mode == kGroupLinked)
-    *ws_bytes = kLinkedHeader + words * sizeof(uint64_t);
-  else
-    *ws_bytes = words * sizeof(float);
+  *linked_bytes = kLinkedHeader + words * sizeof(uint64_t);
+  *plain_bytes = words * sizeof(float);
   return true;
 }
 

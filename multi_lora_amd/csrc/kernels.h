@@ -68,8 +68,14 @@ hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipSt
 // expand items add them in chunk order and apply the expand.
 constexpr int kGroupRows = 256;  // rows gathered per pass
 constexpr int kGroupSteps = 2;   // K-steps per wave per chunk (chunk = 4 waves x 2 steps)
+constexpr int kGroupAuto = 0;    // mode: the library picks one of the two below
 constexpr int kGroupLinked = 1;  // mode: one launch, sums passed as tagged words
 constexpr int kGroupTwo = 2;     // mode: two launches, sums passed as plain fp32
+// kGroupAuto takes the single launch while num_slots * (shrink + expand items
+// per slot) is at most this many per CU: beyond that the items no longer fit
+// on the chip at once, and expand items left waiting cost more than the
+// second launch.
+constexpr int kLinkedItemsPerCu = 16;
 constexpr size_t kLinkedHeader = 256;  // linked workspace: error word, padded
 
 struct GroupedArgs {
@@ -86,6 +92,8 @@ struct GroupedArgs {
   float* partials;   // two launches: [kc][rows][n_slices * r_max]; linked: the linked workspace
   int kc;            // K chunks
   int k_chunk;       // reduction elements per chunk
+  int s_groups;      // shrink items per (slot, chunk): 1 (all slices) or n_slices (one each)
+  int word64;        // two launches: sums as tag-0 words of a single-launch workspace
   int n_tiles;       // expand items per slot (256-column tiles over all slices)
   int tile_base[kMaxSlices + 1];
 };
@@ -93,8 +101,11 @@ struct GroupedArgs {
 // Largest r_max (per slice) the grouped path handles.
 constexpr int kGroupMaxRank = 64;
 
-bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int num_slots, int dtype, int mode, int* kc,
-                  int* k_chunk, int* nbt, size_t* ws_bytes);
+// Shape check and plan.  Workspaces: linked_bytes for the single launch
+// (header + tagged words, also used by the auto mode whichever schedule it
+// picks), plain_bytes for two launches (fp32 sums).
+bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
+                  int* s_groups, size_t* linked_bytes, size_t* plain_bytes);
 hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int mode, int phases, hipStream_t stream);
 
 // -------------------------------------------------------------- rmsnorm

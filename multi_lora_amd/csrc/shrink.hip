@@ -475,6 +475,31 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int r_
   const int per_row = a.n_slices * live;
   const int64_t zs = static_cast<int64_t>(a.rows) * ncols;
   raw* mid = static_cast<raw*>(a.mid);
+  if (a.r_max % 4 == 0) {
+    // Four columns per thread (live and r_max are multiples of 4 here), so
+    // every split load is 16 bytes.
+    const int quads = per_row / 4;
+    for (int i = threadIdx.x; i < rows_here * quads; i += blockDim.x) {
+      const int r = i / quads;
+      const int c = (i - r * quads) * 4;
+      const int s = c / live;
+      const int n = c - s * live;
+      const int t = row0 + r;
+      const int col = s * a.r_max + n;
+      const f32x4* p = reinterpret_cast<const f32x4*>(a.partials + static_cast<int64_t>(t) * ncols + col);
+      const int64_t zq = zs / 4;
+      f32x4 v[16];
+#pragma unroll
+      for (int z = 0; z < 16; ++z) v[z] = (z < a.ks) ? p[z * zq] : f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int z = 0; z < 16; ++z) sum += v[z];
+      raw* m = mid + static_cast<int64_t>(t) * a.mid_stride + col;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m[q] = T::from_f32(n + q < rank ? sum[q] : 0.f);
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < rows_here * per_row; i += blockDim.x) {
     const int r = i / per_row;
     const int c = i - r * per_row;
@@ -494,8 +519,6 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int r_
   }
 }
 
-// Launches `kern` over every (segment, row tile, K split) and, when K is
-// split, the in-order reduction.
 template <class T>
 hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
   const int64_t tiles = static_cast<int64_t>(args.meta.bs) * p.m_tiles;

@@ -152,6 +152,26 @@ def test_linked_workspace_reused_across_shapes(dev):
         assert_ulp_close(got, apply_kernel_numerics(xs, As, Bs, cm, wl.base.cpu(), wl.col_offsets)[1], what=wl.name)
 
 
+def test_auto_mode_switches_schedules_on_one_workspace(dev):
+    """Mode 0 takes the single launch for small batches and two launches for
+    large ones (words tagged 0 in the same workspace); alternating between
+    them, with shapes changing, every call still matches the oracle."""
+    from multi_lora_amd import _ffi
+
+    lws = LinkedWorkspace()
+    small = synthetic.decode_q(device=dev, tokens=64, seed=51)
+    large = synthetic.decode_qkv(device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    n_large = large.a_stacks[0].shape[0] * (3 * 16 + 16 + 4 + 4)   # slots x (shrink + expand items)
+    assert n_large > 16 * cus, "the large case must exceed the single-launch limit"
+    for wl in (small, large, small, large, small):
+        got = grouped(wl, mode=0, lws=lws)
+        cm = cpu_meta(wl.meta)
+        xs, As, Bs = wl.x.cpu(), [a.cpu() for a in wl.a_stacks], [b.cpu() for b in wl.b_stacks]
+        assert_ulp_close(got, apply_kernel_numerics(xs, As, Bs, cm, wl.base.cpu(), wl.col_offsets)[1], what=wl.name)
+    assert _ffi.ABI_VERSION == 2
+
+
 def test_linked_repeated_calls_are_bit_identical(dev):
     wl = synthetic.decode_q(device=dev, tokens=128, seed=21)
     lws = LinkedWorkspace()

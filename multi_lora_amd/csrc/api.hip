@@ -309,8 +309,11 @@ int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
   a.hidden = hidden;
   a.eps = eps;
   a.tpr = tpr;
+  a.nc = 1;
+  while (a.nc < 8 && a.nc * tpr < nch) a.nc *= 2;
   a.aligned = al16(x) && al16(y) && hidden % vec == 0 && x_stride_outer % vec == 0 &&
               x_stride_inner % vec == 0 && y_row_stride % vec == 0;
+  a.w_vec = (w_dtype == dtype) && al16(w) && hidden % vec == 0;
   hipError_t e = mlora::launch_rmsnorm(a, dtype, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
   return 0;

@@ -122,7 +122,9 @@ struct RmsArgs {
   int hidden;
   float eps;
   int tpr;      // threads per row (power of two, 16..256)
+  int nc;       // 16-byte chunks per thread held in registers (1, 2, 4 or 8)
   int aligned;  // x rows and y rows readable as 16-byte chunks
+  int w_vec;    // weight has x's dtype and is readable as 16-byte chunks
 };
 
 hipError_t launch_rmsnorm(RmsArgs args, int dtype, hipStream_t stream);

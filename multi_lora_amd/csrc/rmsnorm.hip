@@ -5,9 +5,10 @@
 // (r / inner) * stride_outer + (r % inner) * stride_inner.
 //
 // `tpr` threads cooperate on one row (a power of two from 16 to 256), each
-// holding up to 8 16-byte chunks of the row in registers so x is read from
-// HBM once.  The sum of squares is reduced with xor shuffles inside the wave
-// and, for rows wider than one wave, through LDS.
+// holding NC (1, 2, 4 or 8) 16-byte chunks of the row and of the weight in
+// registers, requested together, so x is read from HBM once.  The sum of
+// squares is reduced with xor shuffles inside the wave and, for rows wider
+// than one wave, through LDS.
 #include "kernels.h"
 #include "loads.h"
 
@@ -15,18 +16,31 @@ namespace mlora {
 
 namespace {
 
-constexpr int kMaxCached = 8;
-
-__device__ __forceinline__ float load_w(const void* w, int dtype, int idx) {
-  return load_scaling(w, idx, dtype);
+// Weight chunk `c` as floats: one 16-byte load when the weight has the data
+// type of x and is 16-byte aligned (WV), else element by element.
+template <class T, bool WV>
+__device__ __forceinline__ void weight_chunk(const RmsArgs& a, int c, float (&wf)[T::VEC]) {
+  constexpr int VEC = T::VEC;
+  if constexpr (WV) {
+    const u32x4 v = load_row_chunk<T, true>(static_cast<const typename T::raw_t*>(a.w), c * VEC, a.hidden - c * VEC);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) wf[e] = chunk_elem<T>(v, e);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const int col = c * VEC + e;
+      wf[e] = (col < a.hidden) ? load_scaling(a.w, col, a.w_dtype) : 0.f;
+    }
+  }
 }
 
-template <class T, bool AL>
+// NC = 16-byte chunks of the row held per thread (tpr * NC covers the row
+// when the host can make it so; wider rows stream the rest a second time).
+template <class T, int NC, bool AL, bool WV>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   __shared__ float red[4];
-
   const int tid = threadIdx.x;
   const int tpr = a.tpr;
   const int rpb = 256 / tpr;
@@ -36,24 +50,29 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   const bool row_ok = row < a.rows;
   const int hidden = a.hidden;
   const int nch = (hidden + VEC - 1) / VEC;
-
   const raw* x = static_cast<const raw*>(a.x);
   const int64_t r = row_ok ? row : 0;
   const raw* xrow = x + (r / a.inner) * a.x_stride_outer + (r % a.inner) * a.x_stride_inner;
 
-  u32x4 cache[kMaxCached];
-  float ss = 0.f;
+  // The row's chunks and the matching weight chunks, all requested at once.
+  u32x4 cache[NC];
+  float wf[NC][VEC];
 #pragma unroll
-  for (int j = 0; j < kMaxCached; ++j) {
+  for (int j = 0; j < NC; ++j) {
     const int c = li + j * tpr;
     cache[j] = load_row_chunk<T, AL>(xrow, c * VEC, (row_ok && c < nch) ? hidden - c * VEC : 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NC; ++j) weight_chunk<T, WV>(a, li + j * tpr, wf[j]);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float v = chunk_elem<T>(cache[j], e);
       ss += v * v;
     }
-  }
-  for (int c = li + kMaxCached * tpr; row_ok && c < nch; c += tpr) {
+  for (int c = li + NC * tpr; row_ok && c < nch; c += tpr) {
     const u32x4 v = load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -61,7 +80,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
       ss += f * f;
     }
   }
-
   const int width = tpr < kWave ? tpr : kWave;
   for (int off = 1; off < width; off <<= 1) ss += __shfl_xor(ss, off, kWave);
   if (tpr > kWave) {
@@ -74,26 +92,40 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     for (int w = 0; w < wpr; ++w) ss += red[w0 + w];
   }
   if (!row_ok) return;
-
   const float rstd = rsqrtf(ss / static_cast<float>(hidden) + a.eps);
   raw* yrow = static_cast<raw*>(a.y) + row * a.y_stride;
-  auto emit = [&](int c, const u32x4& v) {
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = li + j * tpr;
+    if (c >= nch) break;
     float f[VEC];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const int col = c * VEC + e;
-      const float wv = (col < hidden) ? load_w(a.w, a.w_dtype, col) : 0.f;
-      f[e] = chunk_elem<T>(v, e) * rstd * wv;
-    }
+    for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(cache[j], e) * rstd * wf[j][e];
     store_row_chunk<T, AL>(yrow + c * VEC, pack_chunk<T>(f), hidden - c * VEC);
-  };
-#pragma unroll
-  for (int j = 0; j < kMaxCached; ++j) {
-    const int c = li + j * tpr;
-    if (c < nch) emit(c, cache[j]);
   }
-  for (int c = li + kMaxCached * tpr; c < nch; c += tpr)
-    emit(c, load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC));
+  for (int c = li + NC * tpr; c < nch; c += tpr) {
+    const u32x4 v = load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
+    float w1[VEC];
+    weight_chunk<T, WV>(a, c, w1);
+    float f[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(v, e) * rstd * w1[e];
+    store_row_chunk<T, AL>(yrow + c * VEC, pack_chunk<T>(f), hidden - c * VEC);
+  }
+}
+
+template <class T, int NC, bool AL>
+hipError_t launch_w(const RmsArgs& args, dim3 grid, hipStream_t stream) {
+  if (args.w_vec)
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NC, AL, true>), grid, dim3(256), 0, stream, args);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NC, AL, false>), grid, dim3(256), 0, stream, args);
+  return hipGetLastError();
+}
+
+template <class T, int NC>
+hipError_t launch_nc(const RmsArgs& args, dim3 grid, hipStream_t stream) {
+  return args.aligned ? launch_w<T, NC, true>(args, grid, stream) : launch_w<T, NC, false>(args, grid, stream);
 }
 
 template <class T>
@@ -101,11 +133,13 @@ hipError_t launch_t(const RmsArgs& args, hipStream_t stream) {
   const int rpb = 256 / args.tpr;
   const int64_t blocks = (args.rows + rpb - 1) / rpb;
   if (blocks <= 0) return hipSuccess;
-  if (args.aligned)
-    hipLaunchKernelGGL((rmsnorm_kernel<T, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
-  else
-    hipLaunchKernelGGL((rmsnorm_kernel<T, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
-  return hipGetLastError();
+  const dim3 grid(static_cast<unsigned>(blocks));
+  switch (args.nc) {
+    case 1: return launch_nc<T, 1>(args, grid, stream);
+    case 2: return launch_nc<T, 2>(args, grid, stream);
+    case 4: return launch_nc<T, 4>(args, grid, stream);
+    default: return launch_nc<T, 8>(args, grid, stream);
+  }
 }
 
 }  // namespace

@@ -184,7 +184,7 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
   }
   args.tile_base[n_slices] = tiles;
 
-  const int bm = (dtype == MLORA_F32 || meta->max_len <= 16) ? 16 : 64;
+  const int bm = (dtype == MLORA_F32 || meta->max_len <= 16) ? 16 : mlora::kExpandLongBM;
   args.mid = mid;
   args.mid_stride = mid_row_stride;
   args.rows = num_rows;

@@ -166,8 +166,10 @@ hipError_t launch_al(const ExpandArgs& args, bool aligned, hipStream_t stream) {
 
 hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream) {
   switch (dtype) {
-    case MLORA_BF16: return bm == 16 ? launch_al<BF16, 16>(args, aligned, stream) : launch_al<BF16, 64>(args, aligned, stream);
-    case MLORA_F16: return bm == 16 ? launch_al<F16, 16>(args, aligned, stream) : launch_al<F16, 64>(args, aligned, stream);
+    case MLORA_BF16:
+      return bm == 16 ? launch_al<BF16, 16>(args, aligned, stream) : launch_al<BF16, kExpandLongBM>(args, aligned, stream);
+    case MLORA_F16:
+      return bm == 16 ? launch_al<F16, 16>(args, aligned, stream) : launch_al<F16, kExpandLongBM>(args, aligned, stream);
     default: return launch_al<F32, 16>(args, aligned, stream);
   }
 }

@@ -43,6 +43,10 @@ hipError_t launch_shrink(const ShrinkPlan& plan, ShrinkArgs args, int dtype, boo
 
 // -------------------------------------------------------------- expand
 constexpr int kExpandBN = 256;  // output columns per tile
+// Token rows per tile for long segments: 32 keeps the accumulators at 32
+// registers a lane, so four workgroups fit on a CU and their output tiles
+// are in flight together.
+constexpr int kExpandLongBM = 32;
 
 struct ExpandArgs {
   const void* mid;

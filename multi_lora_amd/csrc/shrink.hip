@@ -32,7 +32,7 @@ namespace {
 // 16-row blocks per wave of the long-segment kernels, by the number of
 // 16-row A blocks (keeps the LDS tiles of shrink_lds_kernel within 70 KB).
 template <int NBT>
-constexpr int kShrinkRb = NBT >= 8 ? 1 : 2;
+constexpr int kShrinkRb = 1;
 
 template <class T>
 __device__ __forceinline__ void zero_mid_cols(const ShrinkArgs& a, int row0, int rows_here, int col_from) {
@@ -570,7 +570,7 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
   p.nbt = 1;
   while (p.nbt < blocks) p.nbt *= 2;
   if (p.nbt > 16) return false;
-  const int rb = p.nbt >= 8 ? 1 : 2;  // kShrinkRb
+  const int rb = 1;  // kShrinkRb
   p.bm = (max_len <= 16) ? 16 : 64 * rb;
   p.m_tiles = cdiv(max_len > 0 ? max_len : 1, p.bm);
   const int ksteps = cdiv(in_dim, kstep);

@@ -163,6 +163,39 @@ int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
                   int64_t y_row_stride, int64_t rows, int32_t hidden, float eps,
                   int32_t dtype, void* stream);
 
+/* Layout of one module key in the slot pool and in a staged bank, for
+ * mlora_pool_scatter.  A[key] is [num_slots, max_rank, in_dim] and B[key] is
+ * [num_slots, out_dim, max_rank] (multi_lora/pool.py:146-155); a bank holds
+ * the key's A block [rank, in_dim] at a_off and its B block [out_dim, rank]
+ * at b_off (elements), as multi_lora/pool.py:23-58 packs them. */
+typedef struct mlora_pool_key {
+  void* a;
+  int64_t a_slot_stride;   /* elements between slots of A[key] (max_rank * in_dim) */
+  int64_t a_off;
+  void* b;
+  int64_t b_slot_stride;   /* elements between slots of B[key] (out_dim * max_rank) */
+  int64_t b_row_stride;    /* elements between rows of one B slot (max_rank) */
+  int64_t b_off;
+  int32_t in_dim;
+  int32_t out_dim;
+} mlora_pool_key;
+
+/* Pool upload: for each staged adapter i < h and each key, copy the bank's A
+ * block into rows [0, rank) of A[key][slots[i]] and its B block into columns
+ * [0, rank) of B[key][slots[i]]; nothing else in the pool changes.  `stage`
+ * is [h, stage_row_stride] on the device; `slots` (int32[h]) and `keys`
+ * (mlora_pool_key[n_keys]) are device arrays, so a captured graph follows
+ * their rewrites.  Slots outside [0, num_slots) are skipped.  `max_numel` is
+ * the largest rank*in_dim or out_dim*rank over the keys (it sizes the grid);
+ * n_keys * h must not exceed 65535.  Data dtype F16, BF16 or F32 (a bit
+ * copy: only the element size matters).
+ * Replaces scatter_stage / _scatter_stage_kernel
+ * (multi_lora/kernels/scatter_bank.py:17-93), called from the pool's upload
+ * (multi_lora/pool.py:199-243). */
+int mlora_pool_scatter(const void* stage, int64_t stage_row_stride, int32_t h, const int32_t* slots,
+                       const mlora_pool_key* keys, int32_t n_keys, int32_t rank, int32_t num_slots,
+                       int64_t max_numel, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,6 +34,7 @@ EXPORTS = (
     "mlora_grouped_workspace_bytes",
     "mlora_apply_grouped",
     "mlora_rmsnorm",
+    "mlora_pool_scatter",
 )
 
 
@@ -69,6 +70,22 @@ class Slice(ctypes.Structure):
 
 SliceArray = Slice * MAX_SLICES
 
+
+class PoolKey(ctypes.Structure):
+    """mlora_pool_key: one module key's slot tensors and bank offsets."""
+
+    _fields_ = [
+        ("a", ctypes.c_void_p),
+        ("a_slot_stride", ctypes.c_int64),
+        ("a_off", ctypes.c_int64),
+        ("b", ctypes.c_void_p),
+        ("b_slot_stride", ctypes.c_int64),
+        ("b_row_stride", ctypes.c_int64),
+        ("b_off", ctypes.c_int64),
+        ("in_dim", ctypes.c_int32),
+        ("out_dim", ctypes.c_int32),
+    ]
+
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
 
@@ -95,6 +112,10 @@ _SIGNATURES = {
     "mlora_rmsnorm": (
         ctypes.c_int,
         [_vp, _i64, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
+    ),
+    "mlora_pool_scatter": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _i32, _vp],
     ),
 }
 

@@ -319,4 +319,32 @@ int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
   return 0;
 }
 
+int mlora_pool_scatter(const void* stage, int64_t stage_row_stride, int32_t h, const int32_t* slots,
+                       const mlora_pool_key* keys, int32_t n_keys, int32_t rank, int32_t num_slots,
+                       int64_t max_numel, int32_t dtype, void* stream) {
+  g_err[0] = '\0';
+  if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
+  if (h < 0 || n_keys < 0 || rank < 1 || num_slots < 0 || max_numel < 0)
+    return fail(kBadArg, "h %d, n_keys %d, rank %d, num_slots %d, max_numel %lld", h, n_keys, rank, num_slots,
+                (long long)max_numel);
+  if (h == 0 || n_keys == 0 || max_numel == 0) return 0;
+  if (stage == nullptr || slots == nullptr || keys == nullptr) return fail(kBadArg, "null stage, slots or keys");
+  if (static_cast<int64_t>(n_keys) * h > 65535)
+    return fail(kBadArg, "n_keys * h = %lld above 65535", static_cast<long long>(n_keys) * h);
+  const int eb = elem_bytes(dtype);
+  mlora::ScatterArgs a{};
+  a.stage = stage;
+  a.stage_stride = stage_row_stride;
+  a.h = h;
+  a.slots = slots;
+  a.keys = keys;
+  a.n_keys = n_keys;
+  a.rank = rank;
+  a.num_slots = num_slots;
+  a.vec = al16(stage) && (stage_row_stride * eb) % 16 == 0;
+  const hipError_t e = mlora::launch_scatter(a, max_numel, eb, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "pool scatter launch");
+  return 0;
+}
+
 }  // extern "C"

@@ -133,6 +133,23 @@ struct RmsArgs {
 
 hipError_t launch_rmsnorm(RmsArgs args, int dtype, hipStream_t stream);
 
+// -------------------------------------------------------------- pool upload
+constexpr int64_t kScatterElems = 8192;  // elements per workgroup and block
+
+struct ScatterArgs {
+  const void* stage;          // [h, stage_stride] staged banks
+  int64_t stage_stride;
+  int h;                      // adapters staged
+  const int32_t* slots;       // [h] destination slot of each staged bank (device)
+  const mlora_pool_key* keys; // [n_keys] per-key layout (device)
+  int n_keys;
+  int rank;
+  int num_slots;
+  int vec;                    // stage and pool 16-byte aligned
+};
+
+hipError_t launch_scatter(const ScatterArgs& args, int64_t max_numel, int elem_bytes, hipStream_t stream);
+
 // Base pointer of slice `s`'s A (or B) for one slot, selected with
 // compile-time indexing so the kernel-argument array is never indexed
 // dynamically.

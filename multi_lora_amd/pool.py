@@ -15,17 +15,23 @@ Upload.  The first time an adapter is loaded its weights are packed once
 into a flat host bank (pinned when the pool is on a GPU): all A blocks, then
 all B blocks, at offsets fixed per rank (the same packing the reference uses,
 pool.py:23-58).  A reload is then one contiguous H2D copy of the bank into a
-device staging row, on a side stream ordered after the compute stream, and a
-device-side scatter of each block into its slot.  The compute stream waits
-for the upload before the next forward.
+device staging row, on a side stream ordered after the compute stream; one
+``mlora_pool_scatter`` launch per staged chunk then copies every key's
+blocks into the slots (the reference's scatter kernel,
+multi_lora/kernels/scatter_bank.py:17-93).  The compute stream waits for the
+upload before the next forward.  A pool on the CPU (host logic and tests)
+copies with torch instead.
 """
 
 from __future__ import annotations
 
 from typing import Dict, Iterable, List, Optional, Tuple
 
+import ctypes
+
 import torch
 
+from . import _ffi
 from .batch_info import BatchLoRAInfo
 from .eviction import EvictionPolicy
 from .weights import AdapterWeights
@@ -56,6 +62,9 @@ class _RankPlan:
             self.b_off[key], self.b_shape[key] = cursor, (out_dim, rank)
             cursor += out_dim * rank
         self.total = cursor
+        self.dims = dims
+        self.device_table: Optional[torch.Tensor] = None  # mlora_pool_key[len(keys)] on the device
+        self.max_numel = max([rank * dims[k][0] for k in keys] + [dims[k][1] * rank for k in keys] + [0])
 
 
 class _GpuBuffers:
@@ -171,13 +180,36 @@ class _GpuBuffers:
                 stage.record_stream(torch.cuda.current_stream(self.device))
             for c0 in range(0, len(group), _BANK_CHUNK):
                 chunk = group[c0 : c0 + _BANK_CHUNK]
+                if self.device.type != "cuda":
+                    for slot, w in chunk:
+                        self._scatter(self._bank_for(w, plan), slot, plan)
+                    continue
                 for i, (slot, w) in enumerate(chunk):
-                    bank = self._bank_for(w, plan)
-                    src = bank
-                    if self.device.type == "cuda":
-                        stage[i].copy_(bank, non_blocking=non_blocking)
-                        src = stage[i]
-                    self._scatter(src, slot, plan)
+                    stage[i].copy_(self._bank_for(w, plan), non_blocking=non_blocking)
+                self._scatter_staged(stage, [slot for slot, _ in chunk], plan)
+
+    def _key_table(self, plan: _RankPlan) -> torch.Tensor:
+        """The plan's mlora_pool_key array on the device, built once per plan."""
+        if plan.device_table is None:
+            arr = (_ffi.PoolKey * len(plan.keys))()
+            for j, key in enumerate(plan.keys):
+                a, b = self.A[key], self.B[key]
+                arr[j] = _ffi.PoolKey(a.data_ptr(), a.stride(0), plan.a_off[key], b.data_ptr(), b.stride(0),
+                                      b.stride(1), plan.b_off[key], a.shape[2], b.shape[1])
+            host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+            plan.device_table = host.to(self.device)
+        return plan.device_table
+
+    def _scatter_staged(self, stage: torch.Tensor, slots: List[int], plan: _RankPlan) -> None:
+        """One launch: staged rows [0, len(slots)) into their slots, every key."""
+        table = self._key_table(plan)
+        slots_dev = torch.tensor(slots, dtype=torch.int32, device=self.device)
+        rc = _ffi.lib().mlora_pool_scatter(
+            stage.data_ptr(), stage.stride(0), len(slots), slots_dev.data_ptr(), table.data_ptr(), len(plan.keys),
+            plan.rank, self.max_loras_per_batch, plan.max_numel, _ffi.dtype_code(self.dtype),
+            _ffi.stream_ptr(self.device),
+        )
+        _ffi.check(rc, "mlora_pool_scatter")
 
     def _scatter(self, flat: torch.Tensor, slot: int, plan: _RankPlan) -> None:
         """Copy one adapter's packed blocks into slot ``slot`` (first ``rank`` rows / columns)."""

@@ -112,3 +112,18 @@ def test_grouped_workspace_sizes():
     assert lib.mlora_grouped_workspace_bytes(4096, 72, 1, 128, 64, bf, 1) == 0               # r_max > 64
     assert lib.mlora_grouped_workspace_bytes(4096, 12, 1, 128, 64, bf, 2) == 0               # r_max % 8
     assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 3) == 0               # bad mode
+
+
+def test_pool_key_struct_layout():
+    """mlora_pool_key as the header lays it out: 7 eight-byte fields, then two int32."""
+    assert ctypes.sizeof(_ffi.PoolKey) == 64
+    assert _ffi.PoolKey.in_dim.offset == 56 and _ffi.PoolKey.out_dim.offset == 60
+    assert _ffi.PoolKey.b.offset == 24 and _ffi.PoolKey.b_off.offset == 48
+
+
+def test_pool_scatter_rejects_bad_arguments():
+    lib = _ffi.lib()
+    assert lib.mlora_pool_scatter(None, 16, 1, None, None, 1, 0, 4, 16, _ffi.MLORA_BF16, None) < 0   # rank 0
+    assert lib.mlora_pool_scatter(None, 16, 1, None, None, 1, 2, 4, 16, 7, None) < 0                 # dtype
+    assert lib.mlora_pool_scatter(None, 16, 1, None, None, 1, 2, 4, 16, _ffi.MLORA_BF16, None) < 0   # null stage
+    assert lib.mlora_pool_scatter(None, 16, 0, None, None, 1, 2, 4, 16, _ffi.MLORA_BF16, None) == 0  # nothing to do

@@ -15,8 +15,9 @@ rules) so callers of the reference can switch without edits:
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import List, Sequence, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 
@@ -45,6 +46,64 @@ class KernelInputMetaData:
     lora_ranks: torch.Tensor
     scalings: torch.Tensor
     max_len: int
+    # Set when the five columns are views of one device buffer with a pinned
+    # host mirror (a GPU table made by write_kernel_input_metadata): a
+    # rewrite is then one asynchronous copy instead of five.
+    packed: Optional["PackedColumns"] = None
+
+
+class PackedColumns:
+    """One device buffer holding the five columns, and a pinned host mirror.
+
+    Layout (each section 64-byte aligned): weight_indices[capacity],
+    seg_lens[capacity], seg_indptr[capacity + 1] (int32), lora_ranks[num_slots]
+    (int32), scalings[num_slots] (the pool dtype).  ``write`` fills the
+    mirror and copies it in one transfer on the current stream; before
+    touching the mirror it waits for the previous transfer to have read it.
+    """
+
+    def __init__(self, capacity: int, num_slots: int, device: torch.device, dtype: torch.dtype) -> None:
+        self.capacity, self.num_slots = capacity, num_slots
+        layout = [("weight_indices", capacity, torch.int32), ("seg_lens", capacity, torch.int32),
+                  ("seg_indptr", capacity + 1, torch.int32), ("lora_ranks", num_slots, torch.int32),
+                  ("scalings", num_slots, dtype)]
+        offs, cur = [], 0
+        for name, n, dt in layout:
+            cur = (cur + 63) // 64 * 64
+            offs.append((name, cur, n, dt))
+            cur += n * torch.empty(0, dtype=dt).element_size()
+        self.dev = torch.zeros(max(cur, 1), dtype=torch.uint8, device=device)
+        self.host = torch.zeros(max(cur, 1), dtype=torch.uint8, pin_memory=True)
+        self.dev_cols: Dict[str, torch.Tensor] = {}
+        self.host_cols: Dict[str, torch.Tensor] = {}
+        host_np = self.host.numpy()
+        self.host_np = {}
+        for name, off, n, dt in offs:
+            es = torch.empty(0, dtype=dt).element_size()
+            self.dev_cols[name] = self.dev[off:off + n * es].view(dt)
+            self.host_cols[name] = self.host[off:off + n * es].view(dt)
+            if dt == torch.int32:
+                self.host_np[name] = host_np[off:off + n * es].view(np.int32)
+        self.event = torch.cuda.Event()
+        self.pending = False
+
+    def write(self, columns: Dict[str, Tuple[list, float]]) -> None:
+        if self.pending:
+            self.event.synchronize()
+        for name, (values, pad) in columns.items():
+            n = len(values)
+            arr = self.host_np.get(name)
+            if arr is not None:  # int32 columns: written through a numpy view of the pinned mirror
+                arr[:n] = values
+                arr[n:] = pad
+                continue
+            col = self.host_cols[name]
+            if n:
+                col[:n].copy_(torch.tensor(values, dtype=col.dtype))  # same conversion as fill_column
+            col[n:].fill_(pad)
+        self.dev.copy_(self.host, non_blocking=True)
+        self.event.record()
+        self.pending = True
 
 
 def segment_lens(bs: int, seq_lens: Sequence[int]) -> Tuple[List[int], List[int]]:
@@ -134,12 +193,38 @@ def write_kernel_input_metadata(
     padded so every column is self-consistent: slot 0, rank 0, length 0,
     ``seg_indptr`` = total rows (monotone), scaling 0.
     ``lora_ranks`` / ``scalings`` always have one entry per pool slot.
+    A table allocated here on a GPU packs its columns into one buffer with a
+    pinned host mirror, so each later rewrite is a single asynchronous copy
+    (the reference issues one pageable copy per column, batch_info.py:153-157).
     """
     rows = len(pool_batch.weight_indices)
     lens, indptr = segment_lens(rows, seq_lens)
     max_len = max(lens) if lens else 0
+    device = torch.device(device)
+    slots = len(pool_batch.lora_ranks)
+    columns = {
+        "weight_indices": (list(pool_batch.weight_indices), 0),
+        "seg_lens": (lens, 0),
+        "seg_indptr": (indptr, indptr[-1]),
+        "lora_ranks": (list(pool_batch.lora_ranks), 0),
+        "scalings": (list(pool_batch.scalings), 0.0),
+    }
 
-    if rows > meta.weight_indices.shape[0]:
+    pk = meta.packed
+    if pk is not None and rows <= pk.capacity and slots == pk.num_slots and meta.scalings.dtype == dtype:
+        pk.write(columns)
+        meta.bs = rows
+        meta.max_len = max_len
+        return meta
+
+    if rows > meta.weight_indices.shape[0] or meta.packed is not None:
+        if device.type == "cuda":
+            pk = PackedColumns(rows, slots, device, dtype)
+            pk.write(columns)
+            c = pk.dev_cols
+            return KernelInputMetaData(bs=rows, seg_lens=c["seg_lens"], seg_indptr=c["seg_indptr"],
+                                       weight_indices=c["weight_indices"], lora_ranks=c["lora_ranks"],
+                                       scalings=c["scalings"], max_len=max_len, packed=pk)
         return KernelInputMetaData(
             bs=rows,
             seg_lens=torch.tensor(lens, dtype=torch.int32, device=device),

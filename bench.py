@@ -234,9 +234,29 @@ def bench_other(args) -> int:
             _, a, b, out = reps[i % n_rep]
             assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=2)
 
+        resid = [torch.randn_like(r[0]) for r in reps]
+        ys = [torch.empty_like(r[0]) for r in reps]
+
+        def add_norm(i):
+            x = reps[i % n_rep][0]
+            _ffi.check(lib.mlora_add_rmsnorm(x.data_ptr(), x.stride(0), resid[i % n_rep].data_ptr(), in_dim,
+                                             w.data_ptr(), _ffi.dtype_code(w.dtype), ys[i % n_rep].data_ptr(),
+                                             in_dim, S, in_dim, eps, _ffi.dtype_code(x.dtype), _ffi.stream_ptr(dev)),
+                       "mlora_add_rmsnorm")
+
+        def add_then_norm(i):
+            x, r = reps[i % n_rep][0], resid[i % n_rep]
+            r.add_(x)
+            _ffi.check(lib.mlora_rmsnorm(r.data_ptr(), r.stride(0), r.stride(0), 1, w.data_ptr(),
+                                         _ffi.dtype_code(w.dtype), ys[i % n_rep].data_ptr(), in_dim, S, in_dim, eps,
+                                         _ffi.dtype_code(x.dtype), _ffi.stream_ptr(dev)), "mlora_rmsnorm")
+
         total_bytes = lora_bytes + norm_bytes
+        add_bytes = 4 * S * in_dim * e + in_dim * e
         parts = {"rmsnorm": (norm, norm_bytes), "grouped_linked (3 slices)": (lora, lora_bytes),
-                 "grouped two-launch schedule (3 slices)": (lora_two, lora_bytes)}
+                 "grouped two-launch schedule (3 slices)": (lora_two, lora_bytes),
+                 "add_rmsnorm fused (schedule comparison)": (add_norm, add_bytes),
+                 "add then rmsnorm, unfused (schedule comparison)": (add_then_norm, add_bytes)}
         path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-grouped, one linked launch)"
     else:
         mids = [torch.empty(S, n * r_max, dtype=host.x.dtype, device=dev) for _ in range(n_rep)]

@@ -163,6 +163,17 @@ int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
                   int64_t y_row_stride, int64_t rows, int32_t hidden, float eps,
                   int32_t dtype, void* stream);
 
+/* Residual add fused with the next RMSNorm of a decoder layer:
+ *   h = round(x + residual); residual <- h; y = round(h * rsqrt(mean(h^2) + eps) * w)
+ * (fp32 math, h rounded to `dtype` as an unfused tensor add stores it).  x, residual
+ * and y are [rows, hidden] with their own row strides; y may be x (in place),
+ * residual must not overlap x or y.  No counterpart is called in the
+ * reference: it is the fusion the reference plans as fused_add_rms_norm
+ * (OPTIMIZATION_TODO.md T22) around multi_lora/kernels/rmsnorm.py:17-48. */
+int mlora_add_rmsnorm(const void* x, int64_t x_row_stride, void* residual, int64_t residual_row_stride,
+                      const void* w, int32_t w_dtype, void* y, int64_t y_row_stride, int64_t rows,
+                      int32_t hidden, float eps, int32_t dtype, void* stream);
+
 /* Layout of one module key in the slot pool and in a staged bank, for
  * mlora_pool_scatter.  A[key] is [num_slots, max_rank, in_dim] and B[key] is
  * [num_slots, out_dim, max_rank] (multi_lora/pool.py:146-155); a bank holds

@@ -35,6 +35,7 @@ EXPORTS = (
     "mlora_apply_grouped",
     "mlora_rmsnorm",
     "mlora_pool_scatter",
+    "mlora_add_rmsnorm",
 )
 
 
@@ -116,6 +117,10 @@ _SIGNATURES = {
     "mlora_pool_scatter": (
         ctypes.c_int,
         [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i64, _i32, _vp],
+    ),
+    "mlora_add_rmsnorm": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
     ),
 }
 

@@ -283,13 +283,19 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   return 0;
 }
 
-int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner, int64_t inner, const void* w,
-                  int32_t w_dtype, void* y, int64_t y_row_stride, int64_t rows, int32_t hidden, float eps,
-                  int32_t dtype, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int rmsnorm_call(const void* x, int64_t x_stride_outer, int64_t x_stride_inner, int64_t inner, void* residual,
+                 int64_t residual_row_stride, const void* w, int32_t w_dtype, void* y, int64_t y_row_stride,
+                 int64_t rows, int32_t hidden, float eps, int32_t dtype, void* stream) {
   g_err[0] = '\0';
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(kBadArg, "bad dtype %d / weight dtype %d", dtype, w_dtype);
   if (hidden <= 0 || rows < 0 || inner < 1) return fail(kBadArg, "hidden %d, rows %lld, inner %lld", hidden, (long long)rows, (long long)inner);
   if (y_row_stride < hidden) return fail(kBadArg, "y row stride %lld < hidden %d", (long long)y_row_stride, hidden);
+  if (residual != nullptr && residual_row_stride < hidden)
+    return fail(kBadArg, "residual row stride %lld < hidden %d", (long long)residual_row_stride, hidden);
   if (rows == 0) return 0;
   if (x == nullptr || w == nullptr || y == nullptr) return fail(kBadArg, "null x, w or y");
   const int vec = vec_elems(dtype);
@@ -312,11 +318,36 @@ int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
   a.nc = 1;
   while (a.nc < 8 && a.nc * tpr < nch) a.nc *= 2;
   a.aligned = al16(x) && al16(y) && hidden % vec == 0 && x_stride_outer % vec == 0 &&
-              x_stride_inner % vec == 0 && y_row_stride % vec == 0;
+              x_stride_inner % vec == 0 && y_row_stride % vec == 0 &&
+              (residual == nullptr || (al16(residual) && residual_row_stride % vec == 0));
   a.w_vec = (w_dtype == dtype) && al16(w) && hidden % vec == 0;
+  a.residual = residual;
+  a.residual_stride = residual_row_stride;
   hipError_t e = mlora::launch_rmsnorm(a, dtype, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlora_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner, int64_t inner, const void* w,
+                  int32_t w_dtype, void* y, int64_t y_row_stride, int64_t rows, int32_t hidden, float eps,
+                  int32_t dtype, void* stream) {
+  return rmsnorm_call(x, x_stride_outer, x_stride_inner, inner, nullptr, 0, w, w_dtype, y, y_row_stride, rows,
+                      hidden, eps, dtype, stream);
+}
+
+int mlora_add_rmsnorm(const void* x, int64_t x_row_stride, void* residual, int64_t residual_row_stride,
+                      const void* w, int32_t w_dtype, void* y, int64_t y_row_stride, int64_t rows, int32_t hidden,
+                      float eps, int32_t dtype, void* stream) {
+  if (residual == nullptr && rows > 0) {
+    g_err[0] = '\0';
+    return fail(kBadArg, "null residual");
+  }
+  return rmsnorm_call(x, x_row_stride, x_row_stride, 1, residual, residual_row_stride, w, w_dtype, y, y_row_stride,
+                      rows, hidden, eps, dtype, stream);
 }
 
 int mlora_pool_scatter(const void* stage, int64_t stage_row_stride, int32_t h, const int32_t* slots,

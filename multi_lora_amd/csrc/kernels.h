@@ -129,6 +129,8 @@ struct RmsArgs {
   int nc;       // 16-byte chunks per thread held in registers (1, 2, 4 or 8)
   int aligned;  // x rows and y rows readable as 16-byte chunks
   int w_vec;    // weight has x's dtype and is readable as 16-byte chunks
+  void* residual;            // non-null: h = x + residual is stored here and normalised
+  int64_t residual_stride;
 };
 
 hipError_t launch_rmsnorm(RmsArgs args, int dtype, hipStream_t stream);

@@ -1,6 +1,9 @@
 // Fused RMSNorm on gfx950: y = round(x * rsqrt(mean(x^2) + eps) * w), fp32
 // math and a single rounding, as the reference kernel computes it
-// (multi_lora/kernels/rmsnorm.py:17-45).  Rows may be addressed with the
+// (multi_lora/kernels/rmsnorm.py:17-45).  With a residual row (ADD) the
+// kernel first forms h = round(x + residual), stores h back to the residual
+// and normalises h: the residual add and the next RMSNorm of a decoder layer
+// in one pass, the fusion the reference plans (OPTIMIZATION_TODO.md T22).  Rows may be addressed with the
 // reference's two-level stride (rmsnorm.py:56-75): row r starts at
 // (r / inner) * stride_outer + (r % inner) * stride_inner.
 //
@@ -36,7 +39,17 @@ __device__ __forceinline__ void weight_chunk(const RmsArgs& a, int c, float (&wf
 
 // NC = 16-byte chunks of the row held per thread (tpr * NC covers the row
 // when the host can make it so; wider rows stream the rest a second time).
-template <class T, int NC, bool AL, bool WV>
+// x + residual rounded to the storage type (what an unfused bf16/fp16 add
+// stores), written back to the residual row when ADD.
+template <class T>
+__device__ __forceinline__ u32x4 add_chunk(const u32x4& x, const u32x4& r) {
+  float f[T::VEC];
+#pragma unroll
+  for (int e = 0; e < T::VEC; ++e) f[e] = chunk_elem<T>(x, e) + chunk_elem<T>(r, e);
+  return pack_chunk<T>(f);
+}
+
+template <class T, int NC, bool AL, bool WV, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -53,6 +66,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   const raw* x = static_cast<const raw*>(a.x);
   const int64_t r = row_ok ? row : 0;
   const raw* xrow = x + (r / a.inner) * a.x_stride_outer + (r % a.inner) * a.x_stride_inner;
+  raw* rrow = ADD ? static_cast<raw*>(a.residual) + r * a.residual_stride : nullptr;
 
   // The row's chunks and the matching weight chunks, all requested at once.
   u32x4 cache[NC];
@@ -61,6 +75,20 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   for (int j = 0; j < NC; ++j) {
     const int c = li + j * tpr;
     cache[j] = load_row_chunk<T, AL>(xrow, c * VEC, (row_ok && c < nch) ? hidden - c * VEC : 0);
+  }
+  if constexpr (ADD) {
+    u32x4 res[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = li + j * tpr;
+      res[j] = load_row_chunk<T, AL>(rrow, c * VEC, (row_ok && c < nch) ? hidden - c * VEC : 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = li + j * tpr;
+      cache[j] = add_chunk<T>(cache[j], res[j]);
+      if (row_ok && c < nch) store_row_chunk<T, AL>(rrow + c * VEC, cache[j], hidden - c * VEC);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NC; ++j) weight_chunk<T, WV>(a, li + j * tpr, wf[j]);
@@ -73,7 +101,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
       ss += v * v;
     }
   for (int c = li + NC * tpr; row_ok && c < nch; c += tpr) {
-    const u32x4 v = load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
+    u32x4 v = load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
+    if constexpr (ADD) {
+      v = add_chunk<T>(v, load_row_chunk<T, AL>(rrow, c * VEC, hidden - c * VEC));
+      store_row_chunk<T, AL>(rrow + c * VEC, v, hidden - c * VEC);
+    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float f = chunk_elem<T>(v, e);
@@ -104,7 +136,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     store_row_chunk<T, AL>(yrow + c * VEC, pack_chunk<T>(f), hidden - c * VEC);
   }
   for (int c = li + NC * tpr; c < nch; c += tpr) {
-    const u32x4 v = load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
+    // Chunks past the cached ones: the sum was stored to the residual row
+    // by this same thread in the first pass.
+    const u32x4 v = ADD ? load_row_chunk<T, AL>(rrow, c * VEC, hidden - c * VEC)
+                        : load_row_chunk<T, AL>(xrow, c * VEC, hidden - c * VEC);
     float w1[VEC];
     weight_chunk<T, WV>(a, c, w1);
     float f[VEC];
@@ -114,18 +149,23 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
   }
 }
 
-template <class T, int NC, bool AL>
+template <class T, int NC, bool AL, bool ADD>
 hipError_t launch_w(const RmsArgs& args, dim3 grid, hipStream_t stream) {
   if (args.w_vec)
-    hipLaunchKernelGGL((rmsnorm_kernel<T, NC, AL, true>), grid, dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NC, AL, true, ADD>), grid, dim3(256), 0, stream, args);
   else
-    hipLaunchKernelGGL((rmsnorm_kernel<T, NC, AL, false>), grid, dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NC, AL, false, ADD>), grid, dim3(256), 0, stream, args);
   return hipGetLastError();
+}
+
+template <class T, int NC, bool AL>
+hipError_t launch_add(const RmsArgs& args, dim3 grid, hipStream_t stream) {
+  return args.residual ? launch_w<T, NC, AL, true>(args, grid, stream) : launch_w<T, NC, AL, false>(args, grid, stream);
 }
 
 template <class T, int NC>
 hipError_t launch_nc(const RmsArgs& args, dim3 grid, hipStream_t stream) {
-  return args.aligned ? launch_w<T, NC, true>(args, grid, stream) : launch_w<T, NC, false>(args, grid, stream);
+  return args.aligned ? launch_add<T, NC, true>(args, grid, stream) : launch_add<T, NC, false>(args, grid, stream);
 }
 
 template <class T>

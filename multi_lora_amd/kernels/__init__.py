@@ -7,7 +7,7 @@ from .lora_ops import (
     sgemm_lora_b_fwd,
     sgemm_lora_b_multi_fwd,
 )
-from .rmsnorm import fuse_rmsnorm, rmsnorm_fwd
+from .rmsnorm import fuse_rmsnorm, fused_add_rmsnorm, rmsnorm_fwd
 
 __all__ = [
     "Workspace",
@@ -17,4 +17,5 @@ __all__ = [
     "sgemm_lora_b_multi_fwd",
     "rmsnorm_fwd",
     "fuse_rmsnorm",
+    "fused_add_rmsnorm",
 ]

@@ -48,6 +48,37 @@ def rmsnorm_fwd(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
     return out.reshape(x.shape)
 
 
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``residual += x`` (rounded to the dtype, in place), then RMSNorm of it.
+
+    The residual add and the following RMSNorm of a decoder layer in one
+    pass, the fusion the reference plans as ``fused_add_rms_norm``
+    (OPTIMIZATION_TODO.md T22).  Returns the normalised rows (a new tensor);
+    ``residual`` holds ``x + residual`` afterwards.
+    """
+    if x.device.type != "cuda":
+        raise RuntimeError(f"x must be on a ROCm GPU (got {x.device}); the HIP path has no CPU fallback")
+    hidden = x.shape[-1]
+    if residual.shape != x.shape or residual.dtype != x.dtype or residual.device != x.device:
+        raise ValueError(f"residual {tuple(residual.shape)} {residual.dtype} must match x {tuple(x.shape)} {x.dtype}")
+    if weight.numel() != hidden:
+        raise ValueError(f"weight has {weight.numel()} entries, hidden size is {hidden}")
+    if not residual.is_contiguous():
+        raise ValueError("residual must be contiguous (it is updated in place)")
+    src = x.contiguous()
+    rows = src.numel() // hidden if hidden else 0
+    out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
+    if rows == 0:
+        return out.reshape(x.shape)
+    w = weight.contiguous()
+    rc = _ffi.lib().mlora_add_rmsnorm(
+        src.data_ptr(), hidden, residual.data_ptr(), hidden, w.data_ptr(), _ffi.dtype_code(w.dtype), out.data_ptr(),
+        hidden, rows, hidden, float(eps), _ffi.dtype_code(x.dtype), _ffi.stream_ptr(x.device),
+    )
+    _ffi.check(rc, "mlora_add_rmsnorm")
+    return out.reshape(x.shape)
+
+
 def fuse_rmsnorm(model: torch.nn.Module) -> int:
     """Route every ``*RMSNorm`` module's forward through ``rmsnorm_fwd``; returns the count.
 

@@ -6,6 +6,10 @@
   (multi_lora/tests/test_fused_rmsnorm.py:19-32): normalise in fp32, round
   to the input dtype, then multiply by the weight in that dtype.
 * ``rmsnorm_f64``  — float64 ground truth.
+* ``add_rmsnorm_ref`` — the residual add and the next RMSNorm of a decoder
+  layer as the unfused modules compute them (the fusion the reference
+  plans, OPTIMIZATION_TODO.md T22): ``h = x + residual`` rounded to the
+  storage dtype (a bf16/fp16 tensor add), then ``rmsnorm_ref(h)``.
 """
 
 from __future__ import annotations
@@ -29,3 +33,9 @@ def rmsnorm_hf(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
 def rmsnorm_f64(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     h = x.detach().cpu().double()
     return h / torch.sqrt((h * h).mean(-1, keepdim=True) + eps) * w.detach().cpu().double()
+
+
+def add_rmsnorm_ref(x: torch.Tensor, residual: torch.Tensor, w: torch.Tensor, eps: float):
+    """Returns (new residual h, normalised y)."""
+    h = (x.detach().cpu().float() + residual.detach().cpu().float()).to(x.dtype)
+    return h, rmsnorm_ref(h, w, eps)

@@ -92,3 +92,43 @@ def test_fuse_patches_all_and_keeps_numerics(dev):
     torch.testing.assert_close(model[0].n2(x2), want2, rtol=2e-2, atol=2e-2)
     assert isinstance(model[0].n1.weight, nn.Parameter)
     assert isinstance(model[0].lin, nn.Linear)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,hidden", [(256, 4096), (33, 100), (7, 14336), (64, 2560)])
+def test_fused_add_rmsnorm(dev, dtype, rows, hidden):
+    """residual <- round(x + residual) bit-exact; y within one unit of the
+    single-rounding RMSNorm of that sum."""
+    from multi_lora_amd.kernels import fused_add_rmsnorm
+    from oracle.rmsnorm_ref import add_rmsnorm_ref
+
+    g = torch.Generator().manual_seed(rows + hidden)
+    x = torch.randn(rows, hidden, generator=g).to(dev, dtype)
+    res = (torch.randn(rows, hidden, generator=g) * 3).to(dev, dtype)
+    w = (torch.randn(hidden, generator=g) * 0.1 + 1).to(dev, dtype)
+    h_ref, y_ref = add_rmsnorm_ref(x, res, w, 1e-5)
+    y = fused_add_rmsnorm(x, res, w, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), h_ref)
+    if dtype == torch.float32:
+        torch.testing.assert_close(y.cpu(), y_ref, atol=1e-5, rtol=1e-5)
+    else:
+        assert_ulp_close(y.cpu(), y_ref, what=f"{dtype} {rows}x{hidden}")
+
+
+def test_fused_add_rmsnorm_in_place_output(dev):
+    """y may overwrite x (vLLM-style in-place use)."""
+    from multi_lora_amd import _ffi
+    from oracle.rmsnorm_ref import add_rmsnorm_ref
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(16, 4096, generator=g).to(dev, torch.bfloat16)
+    res = torch.randn(16, 4096, generator=g).to(dev, torch.bfloat16)
+    w = torch.ones(4096, device=dev, dtype=torch.bfloat16)
+    h_ref, y_ref = add_rmsnorm_ref(x, res, w, 1e-6)
+    rc = _ffi.lib().mlora_add_rmsnorm(x.data_ptr(), 4096, res.data_ptr(), 4096, w.data_ptr(), _ffi.MLORA_BF16,
+                                      x.data_ptr(), 4096, 16, 4096, 1e-6, _ffi.MLORA_BF16, _ffi.stream_ptr(dev))
+    _ffi.check(rc, "mlora_add_rmsnorm")
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), h_ref)
+    assert_ulp_close(x.cpu(), y_ref, what="in place")

@@ -229,3 +229,20 @@ def test_pins_catch_planted_mistakes(mutant):
     want = brute_force(x, a, b, base, lens, slots, ranks, scal)
     got = mutant(x, [a], [b], meta, base)
     assert not torch.allclose(got, want, atol=1e-6)
+
+
+def test_add_rmsnorm_closed_forms():
+    """A zero residual reduces to RMSNorm of x; a residual of -x gives h = 0
+    and y = 0; sums of bf16 values that are exactly representable stay exact."""
+    from oracle.rmsnorm_ref import add_rmsnorm_ref, rmsnorm_ref
+
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(5, 64, generator=g).bfloat16()
+    w = (torch.randn(64, generator=g) * 0.1 + 1).bfloat16()
+    h, y = add_rmsnorm_ref(x, torch.zeros_like(x), w, 1e-5)
+    assert torch.equal(h, x) and torch.equal(y, rmsnorm_ref(x, w, 1e-5))
+    h, y = add_rmsnorm_ref(x, -x, w, 1e-5)
+    assert not h.any() and not y.any()
+    ints = torch.randint(-64, 64, (5, 64), generator=g).bfloat16()
+    h, _ = add_rmsnorm_ref(ints, ints, w, 1e-5)
+    assert torch.equal(h, (2 * ints.float()).bfloat16())

@@ -1,0 +1,189 @@
+"""A minimal Llama-style decoder used as the caller of the LoRA path.
+
+The reference drives its decode step through a Hugging Face model and
+``transformers.StaticCache`` (multi_lora/graph_decode.py:23-111).  Weights
+cannot be downloaded here, so this module provides the model around the
+path: token embedding, ``n_layers`` blocks of [RMSNorm -> q/k/v projections
+-> rotary attention over a static KV cache -> o projection -> residual ->
+RMSNorm -> SiLU-gated MLP -> residual], final RMSNorm and LM head.  Every
+projection is a plain ``nn.Linear`` named like Llama's
+(``layers.{i}.self_attn.q_proj`` ... ``layers.{i}.mlp.down_proj``), so the
+manager wraps them with ``LinearWithLoRA`` exactly as it wraps a Hugging Face
+model, and ``fuse_rmsnorm`` routes the norms through the HIP RMSNorm.
+
+Attention is computed in fp32 from contiguous operands.  The KV cache is
+written in place at ``cache_position`` and read whole under a boolean mask,
+so a decode step touches fixed addresses and can be captured in a HIP graph.
+``forward`` accepts the keyword arguments the reference passes to its model
+(input_ids, attention_mask, position_ids, past_key_values, cache_position,
+use_cache) and returns an object with ``.logits``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from types import SimpleNamespace
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+@dataclass
+class DecoderConfig:
+    vocab_size: int = 512
+    hidden_size: int = 256
+    intermediate_size: int = 512
+    num_hidden_layers: int = 2
+    num_attention_heads: int = 4
+    num_key_value_heads: int = 2
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    @classmethod
+    def llama3_8b(cls) -> "DecoderConfig":
+        return cls(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                   num_attention_heads=32, num_key_value_heads=8, rms_norm_eps=1e-5, rope_theta=500000.0)
+
+
+class StaticKV:
+    """Per-layer K and V buffers ``[batch, kv_heads, max_len, head_dim]``, allocated once."""
+
+    def __init__(self, config: DecoderConfig, batch: int, max_len: int, device, dtype) -> None:
+        shape = (batch, config.num_key_value_heads, max_len, config.head_dim)
+        self.max_len = max_len
+        self.keys: List[torch.Tensor] = [torch.zeros(shape, device=device, dtype=dtype)
+                                         for _ in range(config.num_hidden_layers)]
+        self.values: List[torch.Tensor] = [torch.zeros(shape, device=device, dtype=dtype)
+                                           for _ in range(config.num_hidden_layers)]
+
+
+class DecoderRMSNorm(nn.Module):
+    """``x * rsqrt(mean(x^2) + eps) * w`` (fp32 math, one rounding); replaced by the HIP kernel via fuse_rmsnorm."""
+
+    def __init__(self, hidden: int, eps: float) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden))
+        self.variance_epsilon = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        h = x.float()
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.variance_epsilon) * self.weight.float()
+        return h.to(x.dtype)
+
+
+def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    return x * cos + torch.cat((-x2, x1), dim=-1) * sin
+
+
+class Attention(nn.Module):
+    def __init__(self, c: DecoderConfig) -> None:
+        super().__init__()
+        self.c = c
+        d = c.head_dim
+        self.q_proj = nn.Linear(c.hidden_size, c.num_attention_heads * d, bias=False)
+        self.k_proj = nn.Linear(c.hidden_size, c.num_key_value_heads * d, bias=False)
+        self.v_proj = nn.Linear(c.hidden_size, c.num_key_value_heads * d, bias=False)
+        self.o_proj = nn.Linear(c.num_attention_heads * d, c.hidden_size, bias=False)
+
+    def forward(self, x, cos, sin, mask, kv: Optional[StaticKV], layer: int, cache_position):
+        c = self.c
+        b, t, _ = x.shape
+        h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        q = self.q_proj(x).view(b, t, h, d).transpose(1, 2).float()
+        k = self.k_proj(x).view(b, t, kvh, d).transpose(1, 2).float()
+        v = self.v_proj(x).view(b, t, kvh, d).transpose(1, 2)
+        q, k = _rotate(q, cos, sin), _rotate(k, cos, sin)
+        if kv is not None:
+            kv.keys[layer].index_copy_(2, cache_position, k.to(kv.keys[layer].dtype))
+            kv.values[layer].index_copy_(2, cache_position, v.to(kv.values[layer].dtype))
+            k, v = kv.keys[layer], kv.values[layer]
+        rep = h // kvh
+        keys = k.float().repeat_interleave(rep, dim=1)                       # [b, h, L, d]
+        vals = v.float().repeat_interleave(rep, dim=1)
+        scores = torch.matmul(q, keys.transpose(-1, -2).contiguous()) / math.sqrt(d)   # [b, h, t, L]
+        scores = scores.masked_fill(~mask, float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        out = torch.matmul(probs, vals)                                       # [b, h, t, d]
+        out = out.transpose(1, 2).reshape(b, t, h * d).to(x.dtype)
+        return self.o_proj(out)
+
+
+class MLP(nn.Module):
+    def __init__(self, c: DecoderConfig) -> None:
+        super().__init__()
+        self.gate_proj = nn.Linear(c.hidden_size, c.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(c.hidden_size, c.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(c.intermediate_size, c.hidden_size, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, c: DecoderConfig) -> None:
+        super().__init__()
+        self.input_layernorm = DecoderRMSNorm(c.hidden_size, c.rms_norm_eps)
+        self.self_attn = Attention(c)
+        self.post_attention_layernorm = DecoderRMSNorm(c.hidden_size, c.rms_norm_eps)
+        self.mlp = MLP(c)
+
+    def forward(self, x, cos, sin, mask, kv, layer, cache_position):
+        x = x + self.self_attn(self.input_layernorm(x), cos, sin, mask, kv, layer, cache_position)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+class Decoder(nn.Module):
+    def __init__(self, config: DecoderConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList(Block(config) for _ in range(config.num_hidden_layers))
+        self.norm = DecoderRMSNorm(config.hidden_size, config.rms_norm_eps)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        d = config.head_dim
+        inv = 1.0 / (config.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+        self.register_buffer("inv_freq", inv, persistent=False)
+
+    def forward(self, input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                position_ids: Optional[torch.Tensor] = None, past_key_values: Optional[StaticKV] = None,
+                cache_position: Optional[torch.Tensor] = None, use_cache: bool = True, **_):
+        b, t = input_ids.shape
+        dev = input_ids.device
+        kv = past_key_values if use_cache else None
+        if cache_position is None:
+            cache_position = torch.arange(t, device=dev)
+        if position_ids is None:
+            position_ids = cache_position.view(1, t).expand(b, t)
+        ang = position_ids.float()[..., None] * self.inv_freq            # [b, t, d/2]
+        ang = torch.cat((ang, ang), dim=-1)[:, None]                     # [b, 1, t, d]
+        cos, sin = ang.cos(), ang.sin()
+        length = kv.max_len if kv is not None else t
+        mask = self._mask(attention_mask, b, t, length, cache_position, dev)
+        x = self.embed_tokens(input_ids)
+        for i, layer in enumerate(self.layers):
+            x = layer(x, cos, sin, mask, kv, i, cache_position)
+        return SimpleNamespace(logits=self.lm_head(self.norm(x)))
+
+    @staticmethod
+    def _mask(attention_mask, b, t, length, cache_position, dev) -> torch.Tensor:
+        """Boolean [b, 1, t, length]: a 4-D mask is used as given; a 2-D
+        padding mask over the first positions is combined with causality."""
+        if attention_mask is not None and attention_mask.dim() == 4:
+            return attention_mask.bool()
+        keys = torch.arange(length, device=dev)
+        causal = keys[None, :] <= cache_position[:, None]                # [t, length]
+        mask = causal[None, None].expand(b, 1, t, length)
+        if attention_mask is not None:
+            pad = torch.zeros(b, length, dtype=torch.bool, device=dev)
+            pad[:, : attention_mask.shape[1]] = attention_mask.bool()
+            mask = mask & pad[:, None, None, :]
+        return mask

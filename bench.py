@@ -59,7 +59,116 @@ OTHER_WORKLOADS = {
                   "128 rank-32 adapters",
     "pool_upload": "pool upload scatter, Llama-3-8B 32 layers x 7 projections (224 keys), rank 16, "
                    "4 staged adapters (84 MB each) into an 8-slot pool",
+    "c5_step": "Llama-3-8B 32-layer LoRA step: 7 projections per layer at rank 16 (q|k|v and gate|up fused), "
+               "mixed batch of 2 x 512 prefill + 64 decode tokens, 128-slot pool (10.7 GB), adapters Zipf(1.1) over 512",
 }
+
+
+def bench_c5_step(args) -> int:
+    """Every LoRA call of one 32-layer step (the base GEMMs and attention are
+    not part of the path): per layer q|k|v (3 slices, x read once), o,
+    gate|up (2 slices) and down, on a mixed prefill + decode batch."""
+    import torch
+
+    from multi_lora_amd import HipLoRABackend, synthetic
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    H, I, KV, L, K, R = 4096, 14336, 1024, 32, 128, 16
+    g = torch.Generator().manual_seed(7)
+    zipf = torch.tensor([(i + 1) ** -1.1 for i in range(512)])
+    lens = [512, 512] + [1] * 64
+    picks = torch.multinomial(zipf, len(lens), replacement=True, generator=g).tolist()
+    slot_of = {}
+    seg_slots = [slot_of.setdefault(a, len(slot_of)) for a in picks]   # first come, first slot (as the pool does)
+    used = len(slot_of)
+    ranks = [R] * used + [0] * (K - used)
+    meta = synthetic.make_meta(lens, seg_slots, ranks, [2.0] * K, dev, torch.bfloat16)
+    rows = sum(lens)
+
+    def pool(in_dim, out_dim):
+        a = torch.empty(K, R, in_dim, device=dev, dtype=torch.bfloat16).normal_(0, in_dim ** -0.5)
+        b = torch.empty(K, out_dim, R, device=dev, dtype=torch.bfloat16).normal_(0, 0.02)
+        return a, b
+
+    layers = []
+    for _ in range(L):
+        layers.append({"q": pool(H, H), "k": pool(H, KV), "v": pool(H, KV), "o": pool(H, H),
+                       "gate": pool(H, I), "up": pool(H, I), "down": pool(I, H)})
+    x_h = torch.randn(rows, H, device=dev).bfloat16()
+    x_i = torch.randn(rows, I, device=dev).bfloat16()
+    out_qkv = torch.zeros(rows, H + 2 * KV, device=dev, dtype=torch.bfloat16)
+    out_o = torch.zeros(rows, H, device=dev, dtype=torch.bfloat16)
+    out_gu = torch.zeros(rows, 2 * I, device=dev, dtype=torch.bfloat16)
+    out_down = torch.zeros(rows, H, device=dev, dtype=torch.bfloat16)
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(meta)
+    stream = torch.cuda.current_stream(dev)
+
+    def qkv(i):
+        p = layers[i % L]
+        be.apply_lora_multi(x_h, [p["q"][0], p["k"][0], p["v"][0]], [p["q"][1], p["k"][1], p["v"][1]], out_qkv,
+                            [0, H, H + KV])
+
+    def o(i):
+        be.apply_lora(x_h, layers[i % L]["o"][0], layers[i % L]["o"][1], out_o)
+
+    def gate_up(i):
+        p = layers[i % L]
+        be.apply_lora_multi(x_h, [p["gate"][0], p["up"][0]], [p["gate"][1], p["up"][1]], out_gu, [0, I])
+
+    def down(i):
+        be.apply_lora(x_i, layers[i % L]["down"][0], layers[i % L]["down"][1], out_down)
+
+    def step(i):
+        for fn in (qkv, o, gate_up, down):
+            fn(i)
+
+    e = 2
+    n_used = used
+
+    def call_bytes(in_dim, outs):
+        return rows * in_dim * e + sum(n_used * R * in_dim * e + n_used * od * R * e + 2 * rows * od * e
+                                       for od in outs)
+
+    per_layer = {"q|k|v": call_bytes(H, [H, KV, KV]), "o": call_bytes(H, [H]), "gate|up": call_bytes(H, [I, I]),
+                 "down": call_bytes(I, [H])}
+    step_bytes = L * sum(per_layer.values())
+    for i in range(2 * L):
+        step(i)
+    torch.cuda.synchronize()
+    steps = max(2, min(args.steps // 200, 20))
+    g_step = capture(torch, lambda i: step(i), L)  # one graph = one full step (32 layers)
+    step_ms = time_graph(torch, g_step, steps * L, L, stream) * L
+    kernels = {}
+    for name, fn in (("q|k|v", qkv), ("o", o), ("gate|up", gate_up), ("down", down)):
+        ms = time_graph(torch, capture(torch, fn, L), steps * L, L, stream)
+        kernels[name] = {"us_per_layer": ms * 1e3, "us_per_step": ms * 1e3 * L, "bytes_per_layer": per_layer[name],
+                         "GB/s": per_layer[name] / (ms * 1e-3) / 1e9}
+    dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
+    result = {
+        "metric": "c5 LoRA step latency (all 224 LoRA projections of a 32-layer step)",
+        "value": round(step_ms * 1e3, 1),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 2,
+        "ms_per_step": step_ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": OTHER_WORKLOADS["c5_step"], "rows": rows, "segments": len(lens),
+                   "distinct_adapters": used, "algorithmic_bytes_per_step": step_bytes,
+                   "GB/s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
+                   "timing": "HIP graph of one full step (128 backend calls), replayed"},
+        "kernels": kernels,
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(kernels[dom]["GB/s"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kernels[dom]["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def bench_pool_upload(args) -> int:
@@ -487,6 +596,8 @@ def main() -> int:
         return profile_traffic()
     if args.workload == "pool_upload":
         return bench_pool_upload(args)
+    if args.workload == "c5_step":
+        return bench_c5_step(args)
     if args.workload != "decode_q":
         return bench_other(args)
 

@@ -161,6 +161,50 @@ __device__ __forceinline__ void seg_slot_rank(const SegView& m, int seg, int r_m
   *rank = r;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_sum(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Dense row tiles: tile `tile` of the batch, counting ceil(len / bm) tiles
+// per segment in segment order (len = rows of the segment inside [0, rows)),
+// as (segment, tile within the segment).  Returns false when the batch has
+// fewer tiles.  Every wave computes the same result on its own (no LDS, no
+// barrier); the result is wave-uniform.  Launching about rows / bm + bs
+// workgroups instead of bs * ceil(max_len / bm) keeps a mixed batch (a few
+// long segments among many one-row ones) from dispatching mostly empty
+// workgroups.
+__device__ __forceinline__ bool dense_tile(const SegView& m, int rows, int tile, int bm, int* seg, int* mt) {
+  const int lane = threadIdx.x & 63;
+  int before = 0;
+  for (int c0 = 0; c0 < m.bs; c0 += kWave) {
+    const int i = c0 + lane;
+    int n = 0;
+    if (i < m.bs) {
+      const int s = max(m.indptr[i], 0);
+      const int e = min(m.indptr[i + 1], rows);
+      n = e > s ? (e - s + bm - 1) / bm : 0;
+    }
+    const int incl = wave_incl_sum(n);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (tile < before + total) {
+      const uint64_t hit = __ballot(before + incl > tile);
+      const int l = __builtin_amdgcn_readfirstlane(static_cast<int>(__ffsll(static_cast<unsigned long long>(hit))) - 1);
+      *seg = c0 + l;
+      *mt = tile - before - (__builtin_amdgcn_readlane(incl, l) - __builtin_amdgcn_readlane(n, l));
+      return true;
+    }
+    before += total;
+  }
+  return false;
+}
+
 struct SliceView {
   const void* a;
   int64_t a_slot_stride, a_row_stride;

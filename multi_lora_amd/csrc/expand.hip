@@ -10,7 +10,8 @@
 // every access here is bounded by out_dim, so any output width is safe.
 //
 // Work decomposition (256 threads = 4 wave64s per workgroup):
-//   workgroup = (segment, tile of BM tokens, tile of 256 output columns of one slice)
+//   workgroup = (dense tile of BM tokens of one segment, tile of 256 output
+//               columns of one slice); the n-tile index runs fastest
 //   wave      = 64 output columns (4 MFMA n-blocks) x all BM tokens
 //   MFMA tile = D[n][t] += B[n][k] * mid[t][k]   (16 columns x 16 tokens)
 // The output tile is prefetched into registers before the MFMA loop so its
@@ -45,9 +46,8 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 
   const int bid = blockIdx.x;
   const int nt_g = bid % a.n_tiles;
-  const int tile = bid / a.n_tiles;
-  const int seg = tile / a.m_tiles;
-  const int mt = tile - seg * a.m_tiles;
+  int seg, mt;
+  if (!dense_tile(a.meta, a.rows, bid / a.n_tiles, BM, &seg, &mt)) return;
 
   const int start = max(a.meta.indptr[seg], 0);
   const int end = min(a.meta.indptr[seg + 1], a.rows);
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 
 template <class T, int BM, bool AL>
 hipError_t launch_t(const ExpandArgs& args, hipStream_t stream) {
-  const int64_t blocks = static_cast<int64_t>(args.meta.bs) * args.m_tiles * args.n_tiles;
+  const int64_t blocks = dense_tiles(args.meta.bs, args.m_tiles, args.rows, BM) * args.n_tiles;
   if (blocks <= 0) return hipSuccess;
   hipLaunchKernelGGL((expand_kernel<T, BM, AL>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
   return hipGetLastError();

@@ -8,6 +8,16 @@ namespace mlora {
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Workgroups that cover every dense row tile of bm rows (dense_tile): each
+// segment has ceil(len / bm) tiles and the segments' lengths add up to at
+// most `rows`, so there are at most (rows + bs * (bm - 1)) / bm tiles, and at
+// most bs * m_tiles (m_tiles = ceil(max_len / bm)).
+inline int64_t dense_tiles(int bs, int m_tiles, int rows, int bm) {
+  const int64_t seg_major = static_cast<int64_t>(bs) * m_tiles;
+  const int64_t bound = (static_cast<int64_t>(rows) + static_cast<int64_t>(bs) * (bm - 1)) / bm;
+  return seg_major < bound ? seg_major : bound;
+}
+
 // -------------------------------------------------------------- shrink
 struct ShrinkArgs {
   const void* x;
@@ -21,7 +31,7 @@ struct ShrinkArgs {
   void* mid;
   int64_t mid_stride;
   SegView meta;
-  int m_tiles;      // row tiles per segment
+  int m_tiles;      // row tiles per segment (ceil(max_len / bm)); bounds the grid
   int ks;           // K splits per row tile
   int k_per_split;  // reduction elements per split (multiple of KSTEP)
   float* partials;  // ks > 1: [ks][rows][n_slices * r_max] fp32 split sums

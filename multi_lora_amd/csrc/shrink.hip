@@ -205,9 +205,8 @@ __global__ __launch_bounds__(256) void shrink_rows_kernel(ShrinkArgs a) {
 
   const int bid = blockIdx.x;
   const int kz = bid % a.ks;
-  const int tile = bid / a.ks;
-  const int seg = tile / a.m_tiles;
-  const int mt = tile - seg * a.m_tiles;
+  int seg, mt;
+  if (!dense_tile(a.meta, a.rows, bid / a.ks, BM, &seg, &mt)) return;
 
   const int start = max(a.meta.indptr[seg], 0);
   const int end = min(a.meta.indptr[seg + 1], a.rows);
@@ -341,9 +340,8 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
 
   const int bid = blockIdx.x;
   const int kz = bid % a.ks;
-  const int tile = bid / a.ks;
-  const int seg = tile / a.m_tiles;
-  const int mt = tile - seg * a.m_tiles;
+  int seg, mt;
+  if (!dense_tile(a.meta, a.rows, bid / a.ks, BM, &seg, &mt)) return;
 
   const int start = max(a.meta.indptr[seg], 0);
   const int end = min(a.meta.indptr[seg + 1], a.rows);
@@ -457,11 +455,10 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
 constexpr int kReduceRows = 16;
 
 template <class T>
-__global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int r_tiles) {
+__global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a) {
   using raw = typename T::raw_t;
-  const int tile = blockIdx.x;
-  const int seg = tile / r_tiles;
-  const int mt = tile - seg * r_tiles;
+  int seg, mt;
+  if (!dense_tile(a.meta, a.rows, blockIdx.x, kReduceRows, &seg, &mt)) return;
   const int start = max(a.meta.indptr[seg], 0);
   const int end = min(a.meta.indptr[seg + 1], a.rows);
   const int row0 = start + mt * kReduceRows;
@@ -519,16 +516,18 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a, int r_
   }
 }
 
+// The short kernel (bm 16) runs one workgroup per segment and split; the
+// long kernels and the reduction run over dense row tiles.
 template <class T>
 hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
-  const int64_t tiles = static_cast<int64_t>(args.meta.bs) * p.m_tiles;
+  const int64_t tiles = p.bm == 16 ? static_cast<int64_t>(args.meta.bs) * p.m_tiles
+                                   : dense_tiles(args.meta.bs, p.m_tiles, args.rows, p.bm);
   if (tiles <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * p.ks)), dim3(256), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
-  const int r_tiles = p.m_tiles * (p.bm / kReduceRows);
-  hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(args.meta.bs * int64_t{r_tiles})), dim3(256),
-                     0, stream, args, r_tiles);
+  const int64_t r_tiles = dense_tiles(args.meta.bs, p.m_tiles * (p.bm / kReduceRows), args.rows, kReduceRows);
+  hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(r_tiles)), dim3(256), 0, stream, args);
   return hipGetLastError();
 }
 
@@ -574,7 +573,7 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
   p.bm = (max_len <= 16) ? 16 : 64 * rb;
   p.m_tiles = cdiv(max_len > 0 ? max_len : 1, p.bm);
   const int ksteps = cdiv(in_dim, kstep);
-  const int64_t base = static_cast<int64_t>(bs) * p.m_tiles;
+  const int64_t base = (p.bm == 16) ? static_cast<int64_t>(bs) * p.m_tiles : dense_tiles(bs, p.m_tiles, rows, p.bm);
   int ks = 1;
   if (p.bm == 16) {
     // Decode-shaped rows: enough workgroups to cover the chip twice.

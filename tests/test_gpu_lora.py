@@ -259,3 +259,45 @@ def test_split_k_is_deterministic(dev):
         again = run_hip(wl.x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
         assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
     check_workload(wl)
+
+
+@pytest.mark.parametrize("n_short", [61, 150])
+def test_mixed_long_and_one_row_segments(dev, n_short):
+    """A mixed batch (long prefill segments among many one-row and empty ones,
+    64 segments or more, so the dense tile map scans one full chunk of the
+    segment table or several) through the fused three-slice path: every tile of every
+    segment is computed once, rows of rank-0 and out-of-pool segments stay
+    untouched."""
+    g = torch.Generator().manual_seed(n_short)
+    lens = [1] * n_short
+    for pos, n in ((5, 70), (n_short // 2, 130), (n_short - 1, 200)):
+        lens.insert(pos, n)
+    lens[3] = 0
+    lens[n_short // 3] = 0
+    n_slots = 12
+    slots = torch.randint(0, n_slots, (len(lens),), generator=g).tolist()
+    slots[7], slots[n_short // 2 + 4] = -1, n_slots + 3
+    ranks = [16] * n_slots
+    ranks[2] = 0
+    ranks[5] = 9
+    in_dim, outs, r_max = 1024, [512, 128, 128], 16
+    x = torch.randn(sum(lens), in_dim, generator=g).bfloat16()
+    As = [(torch.randn(n_slots, r_max, in_dim, generator=g) * in_dim ** -0.5).bfloat16() for _ in outs]
+    Bs = [(torch.randn(n_slots, o, r_max, generator=g) * 0.05).bfloat16() for o in outs]
+    base = torch.randn(sum(lens), sum(outs), generator=g).bfloat16()
+    cols = [0, outs[0], outs[0] + outs[1]]
+    scal = [1.0 + 0.25 * i for i in range(n_slots)]
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", torch.bfloat16)
+    assert meta_cpu.bs >= 64 and meta_cpu.max_len > 16  # one full chunk of the table, or several
+    want = apply_f64(x, As, Bs, meta_cpu, base, cols)
+    kmid, kout = apply_kernel_numerics(x, As, Bs, meta_cpu, base, cols)
+    mid, out = run_hip(x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs],
+                       make_meta(lens, slots, ranks, scal, dev, torch.bfloat16), base.to(dev), cols)
+    assert_tol_f64(out, want)
+    assert_ulp_close(out, kout, what="out")
+    assert_ulp_close(mid, kmid, what="mid")
+    st = 0
+    for n, s in zip(lens, slots):
+        if not (0 <= s < n_slots) or ranks[s] == 0:
+            assert torch.equal(out[st:st + n], base[st:st + n])
+        st += n

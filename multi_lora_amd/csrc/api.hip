@@ -53,6 +53,7 @@ int check_meta(const mlora_seg_meta* m) {
   if (!valid_dtype(m->scal_dtype)) return fail(kBadArg, "bad scalings dtype %d", m->scal_dtype);
   if (m->bs > 0 && (m->seg_indptr == nullptr || m->weight_indices == nullptr || m->lora_ranks == nullptr))
     return fail(kBadArg, "null segment table pointer");
+  if (m->bs > 0 && m->num_slots > 0 && m->scalings == nullptr) return fail(kBadArg, "null scalings pointer");
   return 0;
 }
 
@@ -161,7 +162,8 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
   if (r_max <= 0 || num_rows < 0) return fail(kBadArg, "r_max %d, num_rows %d", r_max, num_rows);
   if (mid_row_stride < static_cast<int64_t>(n_slices) * r_max)
     return fail(kBadArg, "mid row stride %lld < n_slices*r_max %d", (long long)mid_row_stride, n_slices * r_max);
-  if (meta->bs == 0 || num_rows == 0) return 0;
+  // No slot in the pool: every segment has rank 0 and the output is untouched.
+  if (meta->bs == 0 || num_rows == 0 || meta->num_slots == 0) return 0;
   if (mid == nullptr || out == nullptr) return fail(kBadArg, "mid or out is null");
 
   const int vec = vec_elems(dtype);

@@ -172,37 +172,77 @@ __device__ __forceinline__ int wave_incl_sum(int v) {
   return v;
 }
 
+// The tile's segment, its tile number within the segment, the segment's
+// clamped row range [start, end) and its slot (weight_indices, unchecked).
+struct TileRef {
+  int seg, mt, start, end, slot;
+};
+
 // Dense row tiles: tile `tile` of the batch, counting ceil(len / bm) tiles
 // per segment in segment order (len = rows of the segment inside [0, rows)),
-// as (segment, tile within the segment).  Returns false when the batch has
-// fewer tiles.  Every wave computes the same result on its own (no LDS, no
-// barrier); the result is wave-uniform.  Launching about rows / bm + bs
-// workgroups instead of bs * ceil(max_len / bm) keeps a mixed batch (a few
-// long segments among many one-row ones) from dispatching mostly empty
-// workgroups.
-__device__ __forceinline__ bool dense_tile(const SegView& m, int rows, int tile, int bm, int* seg, int* mt) {
-  const int lane = threadIdx.x & 63;
-  int before = 0;
-  for (int c0 = 0; c0 < m.bs; c0 += kWave) {
-    const int i = c0 + lane;
-    int n = 0;
-    if (i < m.bs) {
-      const int s = max(m.indptr[i], 0);
-      const int e = min(m.indptr[i + 1], rows);
-      n = e > s ? (e - s + bm - 1) / bm : 0;
-    }
-    const int incl = wave_incl_sum(n);
-    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-    if (tile < before + total) {
-      const uint64_t hit = __ballot(before + incl > tile);
-      const int l = __builtin_amdgcn_readfirstlane(static_cast<int>(__ffsll(static_cast<unsigned long long>(hit))) - 1);
-      *seg = c0 + l;
-      *mt = tile - before - (__builtin_amdgcn_readlane(incl, l) - __builtin_amdgcn_readlane(n, l));
-      return true;
-    }
-    before += total;
+// as a TileRef.  Launching about rows / bm + bs workgroups instead of
+// bs * ceil(max_len / bm) keeps a mixed batch (a few long segments among
+// many one-row ones) from dispatching mostly empty workgroups.
+// The table is scanned 64 segments at a time, one segment per lane: the
+// lane's bounds and slot are loaded together (one round trip per chunk),
+// a wave prefix sum counts the tiles, and a ballot finds the segment.
+// Every wave computes the same result on its own (no LDS, no barrier); the
+// result is wave-uniform.
+struct SegChunk {
+  int s, e, w;  // this lane's segment: clamped bounds and slot
+  int n, incl;  // its tile count and the inclusive prefix over the chunk
+  int total;    // tiles in the chunk
+};
+
+__device__ __forceinline__ SegChunk load_chunk(const SegView& m, int rows, int c0, int bm) {
+  const int i = c0 + (threadIdx.x & 63);
+  SegChunk c{0, 0, 0, 0, 0, 0};
+  if (i < m.bs) {
+    c.s = max(m.indptr[i], 0);
+    c.e = min(m.indptr[i + 1], rows);
+    c.w = m.widx[i];
+    c.n = c.e > c.s ? (c.e - c.s + bm - 1) / bm : 0;
+  }
+  c.incl = wave_incl_sum(c.n);
+  c.total = __builtin_amdgcn_readlane(c.incl, kWave - 1);
+  return c;
+}
+
+// Tile `tile` if it lies in chunk `c` (which starts at segment c0, after
+// `before` tiles); no memory access.
+__device__ __forceinline__ bool pick_tile(const SegChunk& c, int c0, int before, int tile, TileRef* t) {
+  if (tile >= before + c.total) return false;
+  const uint64_t hit = __ballot(before + c.incl > tile);
+  const int l = __builtin_amdgcn_readfirstlane(static_cast<int>(__ffsll(static_cast<unsigned long long>(hit))) - 1);
+  t->seg = c0 + l;
+  t->mt = tile - before - (__builtin_amdgcn_readlane(c.incl, l) - __builtin_amdgcn_readlane(c.n, l));
+  t->start = __builtin_amdgcn_readlane(c.s, l);
+  t->end = __builtin_amdgcn_readlane(c.e, l);
+  t->slot = __builtin_amdgcn_readlane(c.w, l);
+  return true;
+}
+
+// Chunks from segment c0 on (`before` tiles ahead of it); false when the
+// batch has fewer tiles.
+__device__ __forceinline__ bool dense_tile_from(const SegView& m, int rows, int tile, int bm, int c0, int before,
+                                                TileRef* t) {
+  for (; c0 < m.bs; c0 += kWave) {
+    const SegChunk c = load_chunk(m, rows, c0, bm);
+    if (pick_tile(c, c0, before, tile, t)) return true;
+    before += c.total;
   }
   return false;
+}
+
+__device__ __forceinline__ bool dense_tile(const SegView& m, int rows, int tile, int bm, TileRef* t) {
+  return dense_tile_from(m, rows, tile, bm, 0, 0, t);
+}
+
+// Rank of a slot read from the table (slot already loaded): 0 outside the
+// pool, clamped to [0, r_max].
+__device__ __forceinline__ int slot_rank_of(const SegView& m, int slot, int r_max, int rank_mult) {
+  if (slot < 0 || slot >= m.num_slots) return 0;
+  return min(max(m.ranks[slot] * rank_mult, 0), r_max);
 }
 
 struct SliceView {

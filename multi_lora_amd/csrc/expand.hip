@@ -46,15 +46,12 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 
   const int bid = blockIdx.x;
   const int nt_g = bid % a.n_tiles;
-  int seg, mt;
-  if (!dense_tile(a.meta, a.rows, bid / a.n_tiles, BM, &seg, &mt)) return;
-
-  const int start = max(a.meta.indptr[seg], 0);
-  const int end = min(a.meta.indptr[seg + 1], a.rows);
-  const int row0 = start + mt * BM;
-  if (row0 >= end) return;
-  int slot, rank;
-  seg_slot_rank(a.meta, seg, a.r_max, 1, &slot, &rank);
+  TileRef tr;
+  if (!dense_tile(a.meta, a.rows, bid / a.n_tiles, BM, &tr)) return;
+  const int end = tr.end;
+  const int row0 = tr.start + tr.mt * BM;
+  const int slot = tr.slot;
+  const int rank = slot_rank_of(a.meta, slot, a.r_max, 1);
   if (rank == 0) return;
 
   int s = 0;

@@ -205,17 +205,13 @@ __global__ __launch_bounds__(256) void shrink_rows_kernel(ShrinkArgs a) {
 
   const int bid = blockIdx.x;
   const int kz = bid % a.ks;
-  int seg, mt;
-  if (!dense_tile(a.meta, a.rows, bid / a.ks, BM, &seg, &mt)) return;
-
-  const int start = max(a.meta.indptr[seg], 0);
-  const int end = min(a.meta.indptr[seg + 1], a.rows);
-  const int row0 = start + mt * BM;
-  if (row0 >= end) return;
+  TileRef tr;
+  if (!dense_tile(a.meta, a.rows, bid / a.ks, BM, &tr)) return;
+  const int end = tr.end;
+  const int row0 = tr.start + tr.mt * BM;
   const int rows_here = min(BM, end - row0);
-
-  int slot, rank;
-  seg_slot_rank(a.meta, seg, a.r_max, a.rank_mult, &slot, &rank);
+  const int slot = tr.slot;
+  const int rank = slot_rank_of(a.meta, slot, a.r_max, a.rank_mult);
   if (rank == 0) {
     if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, 0);
     return;
@@ -340,17 +336,13 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
 
   const int bid = blockIdx.x;
   const int kz = bid % a.ks;
-  int seg, mt;
-  if (!dense_tile(a.meta, a.rows, bid / a.ks, BM, &seg, &mt)) return;
-
-  const int start = max(a.meta.indptr[seg], 0);
-  const int end = min(a.meta.indptr[seg + 1], a.rows);
-  const int row0 = start + mt * BM;
-  if (row0 >= end) return;
+  TileRef tr;
+  if (!dense_tile(a.meta, a.rows, bid / a.ks, BM, &tr)) return;
+  const int end = tr.end;
+  const int row0 = tr.start + tr.mt * BM;
   const int rows_here = min(BM, end - row0);
-
-  int slot, rank;
-  seg_slot_rank(a.meta, seg, a.r_max, a.rank_mult, &slot, &rank);
+  const int slot = tr.slot;
+  const int rank = slot_rank_of(a.meta, slot, a.r_max, a.rank_mult);
   if (rank == 0) {
     if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, 0);
     return;
@@ -457,15 +449,12 @@ constexpr int kReduceRows = 16;
 template <class T>
 __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a) {
   using raw = typename T::raw_t;
-  int seg, mt;
-  if (!dense_tile(a.meta, a.rows, blockIdx.x, kReduceRows, &seg, &mt)) return;
-  const int start = max(a.meta.indptr[seg], 0);
-  const int end = min(a.meta.indptr[seg + 1], a.rows);
-  const int row0 = start + mt * kReduceRows;
-  if (row0 >= end) return;
+  TileRef tr;
+  if (!dense_tile(a.meta, a.rows, blockIdx.x, kReduceRows, &tr)) return;
+  const int end = tr.end;
+  const int row0 = tr.start + tr.mt * kReduceRows;
   const int rows_here = min(kReduceRows, end - row0);
-  int slot, rank;
-  seg_slot_rank(a.meta, seg, a.r_max, a.rank_mult, &slot, &rank);
+  const int rank = slot_rank_of(a.meta, tr.slot, a.r_max, a.rank_mult);
   if (rank == 0) return;
   const int live = min(((rank + 15) >> 4) * 16, a.r_max);
   const int ncols = a.n_slices * a.r_max;

@@ -285,26 +285,28 @@ __device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, in
   return sum;
 }
 
-template <class T>
+template <class T, int WN>
 struct ExpandLds {
   using raw = typename T::raw_t;
-  raw delta[16 * (kExpandBN + T::VEC)];
+  raw delta[16 * (kExpandBN * WN + T::VEC)];
   raw ytile[16 * (kGroupMaxRank + T::VEC)];
   int rows[kGroupRows];
   int tmp[4];
 };
 
-template <class T, int FMT>
-__device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<T>& lds) {
+// WN: 256-column blocks per item (each wave 64 * WN columns); RS: MFMA
+// K-steps of the expand (r_max <= 32 * RS).
+template <class T, int FMT, int WN, int RS>
+__device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<T, WN>& lds) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   constexpr int KSTEP = T::KSTEP;
-  constexpr int BN = kExpandBN;
+  constexpr int BN = kExpandBN * WN;
+  constexpr int NBW = 4 * WN;  // 16-column blocks per wave
   constexpr int LDS_STRIDE = BN + VEC;
   constexpr int CPR = BN / VEC;
   constexpr int RPT = 16 * CPR / 256;
   constexpr int YS = kGroupMaxRank + VEC;
-  constexpr int RS = kGroupMaxRank / KSTEP;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -323,10 +325,10 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
 
   // B fragments: rows clamped to out_dim, K masked to the rank.
   const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
-  u32x4 bf[RS][4];
+  u32x4 bf[RS][NBW];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const raw* brow = B + static_cast<int64_t>(min(n0 + (wave * 4 + nb) * 16 + r16, out_dim - 1)) * a.slices[s].b_row_stride;
+  for (int nb = 0; nb < NBW; ++nb) {
+    const raw* brow = B + static_cast<int64_t>(min(n0 + (wave * NBW + nb) * 16 + r16, out_dim - 1)) * a.slices[s].b_row_stride;
 #pragma unroll
     for (int ks = 0; ks < RS; ++ks) {
       const int kk = ks * KSTEP + g * VEC;
@@ -380,24 +382,24 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
       }
       __syncthreads();
 
-      f32x4 acc[4];
+      f32x4 acc[NBW];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nb = 0; nb < NBW; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < RS; ++ks) {
         if (ks * KSTEP >= rank) break;
         const int kk = ks * KSTEP + g * VEC;
         const u32x4 yv = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(lds.ytile + r16 * YS + kk) : zero_chunk();
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[nb] = T::mma(acc[nb], bf[ks][nb], yv);
+        for (int nb = 0; nb < NBW; ++nb) acc[nb] = T::mma(acc[nb], bf[ks][nb], yv);
       }
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
+      for (int nb = 0; nb < NBW; ++nb) {
         const f32x4 v = acc[nb];
         uint2 w;
         w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) | (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
         w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) | (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
-        *reinterpret_cast<uint2*>(lds.delta + r16 * LDS_STRIDE + (wave * 4 + nb) * 16 + 4 * g) = w;
+        *reinterpret_cast<uint2*>(lds.delta + r16 * LDS_STRIDE + (wave * NBW + nb) * 16 + 4 * g) = w;
       }
       __syncthreads();
 #pragma unroll
@@ -431,20 +433,20 @@ __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
   shrink_item<T, NBT, FMT>(a, slot, rem / a.kc, rem % a.kc, s_rows, s_tmp, red);
 }
 
-template <class T, int FMT>
-__global__ __launch_bounds__(256, 4) void grouped_expand_kernel(GroupedArgs a) {
-  __shared__ __attribute__((aligned(16))) ExpandLds<T> lds;
+template <class T, int FMT, int WN, int RS>
+__global__ __launch_bounds__(256, WN == 1 ? 4 : 2) void grouped_expand_kernel(GroupedArgs a) {
+  __shared__ __attribute__((aligned(16))) ExpandLds<T, WN> lds;
   const int slot = blockIdx.x / a.n_tiles;
-  expand_item<T, FMT>(a, slot, blockIdx.x - slot * a.n_tiles, lds);
+  expand_item<T, FMT, WN, RS>(a, slot, blockIdx.x - slot * a.n_tiles, lds);
 }
 
 // Shrink items are workgroups [0, num_slots * kc); expand items follow.
 // Four waves per SIMD (at most 128 VGPRs) keep four workgroups resident per
 // CU, so expand items are placed, and run their prologue, while the shrink
 // items still run; with 8 or more A blocks the A fragments alone need more.
-template <class T, int NBT>
-__global__ __launch_bounds__(256, NBT >= 8 ? 1 : 4) void grouped_linked_kernel(GroupedArgs a) {
-  __shared__ __attribute__((aligned(16))) ExpandLds<T> lds;
+template <class T, int NBT, int WN, int RS>
+__global__ __launch_bounds__(256, (NBT >= 8 || WN > 1) ? 2 : 4) void grouped_linked_kernel(GroupedArgs a) {
+  __shared__ __attribute__((aligned(16))) ExpandLds<T, WN> lds;
   __shared__ f32x4 red[3 * NBT][kWave];
   const int per_slot = a.s_groups * a.kc;
   const int ns = a.meta.num_slots * per_slot;
@@ -456,17 +458,17 @@ __global__ __launch_bounds__(256, NBT >= 8 ? 1 : 4) void grouped_linked_kernel(G
   } else {
     const int e = b - ns;
     const int slot = e / a.n_tiles;
-    expand_item<T, kSumLinked>(a, slot, e - slot * a.n_tiles, lds);
+    expand_item<T, kSumLinked, WN, RS>(a, slot, e - slot * a.n_tiles, lds);
   }
 }
 
-template <class T, int NBT>
+template <class T, int NBT, int WN, int RS>
 hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t stream) {
   const int64_t g1 = static_cast<int64_t>(args.meta.num_slots) * args.s_groups * args.kc;
   const int64_t g2 = static_cast<int64_t>(args.meta.num_slots) * args.n_tiles;
   if (g1 <= 0 || g2 <= 0) return hipSuccess;
   if (mode == kGroupLinked) {
-    hipLaunchKernelGGL((grouped_linked_kernel<T, NBT>), dim3(static_cast<unsigned>(g1 + g2)), dim3(256), 0, stream,
+    hipLaunchKernelGGL((grouped_linked_kernel<T, NBT, WN, RS>), dim3(static_cast<unsigned>(g1 + g2)), dim3(256), 0, stream,
                        args);
     return hipGetLastError();
   }
@@ -482,24 +484,31 @@ hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t s
   }
   if (phases & 2) {
     if (args.word64)
-      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumWord0>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
+      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumWord0, WN, RS>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
                          args);
     else
-      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumF32>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
+      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumF32, WN, RS>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
                          args);
     return hipGetLastError();
   }
   return hipSuccess;
 }
 
+template <class T, int WN, int RS>
+hipError_t launch_nbt(const GroupedArgs& args, int nbt, int mode, int phases, hipStream_t stream) {
+  switch (nbt) {
+    case 1: return launch_t<T, 1, WN, RS>(args, mode, phases, stream);
+    case 2: return launch_t<T, 2, WN, RS>(args, mode, phases, stream);
+    default: return launch_t<T, 4, WN, RS>(args, mode, phases, stream);
+  }
+}
+
 template <class T>
 hipError_t launch_dtype(const GroupedArgs& args, int nbt, int mode, int phases, hipStream_t stream) {
-  switch (nbt) {
-    case 1: return launch_t<T, 1>(args, mode, phases, stream);
-    case 2: return launch_t<T, 2>(args, mode, phases, stream);
-    case 4: return launch_t<T, 4>(args, mode, phases, stream);
-    default: return launch_t<T, 4>(args, mode, phases, stream);
-  }
+  const bool rs1 = args.r_max <= T::KSTEP;
+  if (args.expand_wn == 2)
+    return rs1 ? launch_nbt<T, 2, 1>(args, nbt, mode, phases, stream) : launch_nbt<T, 2, 2>(args, nbt, mode, phases, stream);
+  return rs1 ? launch_nbt<T, 1, 1>(args, nbt, mode, phases, stream) : launch_nbt<T, 1, 2>(args, nbt, mode, phases, stream);
 }
 
 }  // namespace

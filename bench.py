@@ -386,6 +386,11 @@ def bench_other(args) -> int:
 
         def lora(i):
             _, a, b, out = reps[i % n_rep]
+            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=0,
+                                 linked_workspace=be.linked_workspace)
+
+        def lora_linked(i):
+            _, a, b, out = reps[i % n_rep]
             assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=1,
                                  linked_workspace=be.linked_workspace)
 
@@ -417,11 +422,13 @@ def bench_other(args) -> int:
 
         total_bytes = lora_bytes + norm_bytes
         add_bytes = 4 * S * in_dim * e + in_dim * e
-        parts = {"rmsnorm": (norm, norm_bytes), "grouped_linked (3 slices)": (lora, lora_bytes),
-                 "grouped two-launch schedule (3 slices)": (lora_two, lora_bytes),
+        parts = {"rmsnorm": (norm, norm_bytes), "grouped (3 slices, the library's schedule)": (lora, lora_bytes),
+                 "grouped linked (schedule comparison)": (lora_linked, lora_bytes),
+                 "grouped two launches, fp32 sums (schedule comparison)": (lora_two, lora_bytes),
                  "add_rmsnorm fused (schedule comparison)": (add_norm, add_bytes),
                  "add then rmsnorm, unfused (schedule comparison)": (add_then_norm, add_bytes)}
-        path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-grouped, one linked launch)"
+        path = ("rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-grouped; the library picks the "
+                "linked launch or two launches by work items per CU: two launches at this shape)")
     else:
         mids = [torch.empty(S, n * r_max, dtype=host.x.dtype, device=dev) for _ in range(n_rep)]
         ws = Workspace()

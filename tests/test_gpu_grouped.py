@@ -273,3 +273,27 @@ def test_hip_graph_replays_match_eager_and_follow_metadata_rewrites(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, eager2)
     assert_linked_clean(be.linked_workspace)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_slices_not_multiples_of_the_expand_tile(dev, mode):
+    """Three slices of 520, 264 and 1000 columns packed into one output row:
+    expand items (256 columns in the single launch, 512 with two launches)
+    straddle no slice boundary and write nothing past a slice's width."""
+    g = torch.Generator().manual_seed(11 + mode)
+    n_slots, rows, in_dim, r_max = 9, 48, 512, 32
+    outs = [520, 264, 1000]
+    slots = torch.randint(0, n_slots, (rows,), generator=g).tolist()
+    ranks = [32, 17, 0, 32, 8, 32, 25, 32, 32]
+    x = torch.randn(rows, in_dim, generator=g).bfloat16()
+    As = [(torch.randn(n_slots, r_max, in_dim, generator=g) * in_dim ** -0.5).bfloat16() for _ in outs]
+    Bs = [(torch.randn(n_slots, o, r_max, generator=g) * 0.05).bfloat16() for o in outs]
+    base = torch.randn(rows, sum(outs), generator=g).bfloat16()
+    cols = [0, outs[0], outs[0] + outs[1]]
+    meta = make_meta([1] * rows, slots, ranks, [1.25] * n_slots, dev, torch.bfloat16)
+    wl = synthetic.LoRAWorkload("slices", x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs], base.to(dev),
+                                meta, cols, [1] * rows, slots, ranks, [1.25] * n_slots)
+    got = check(wl, mode=mode)
+    for t, s in enumerate(slots):
+        if ranks[s] == 0:
+            assert torch.equal(got[t], base[t])

@@ -301,3 +301,35 @@ def test_mixed_long_and_one_row_segments(dev, n_short):
         if not (0 <= s < n_slots) or ranks[s] == 0:
             assert torch.equal(out[st:st + n], base[st:st + n])
         st += n
+
+
+@pytest.mark.parametrize("n_slices,r_max,ranks", [
+    (1, 16, [16, 9, 0, 16]),     # one A block per stage (padded to two)
+    (2, 16, [16, 5, 0, 12]),     # two blocks
+    (3, 16, [16, 16, 0, 7]),     # three blocks, compiled as four
+    (2, 64, [64, 40, 0, 17]),    # eight blocks
+])
+def test_streamed_lds_shrink_block_counts(dev, n_slices, r_max, ranks):
+    """Long segments with K a multiple of 64 take the shrink that streams x
+    and A straight into LDS; every block count it compiles, with the K
+    reduction split over workgroups, ranks below r_max, a rank-0 slot and
+    tiles shorter than 64 rows."""
+    g = torch.Generator().manual_seed(n_slices * 100 + r_max)
+    in_dim, outs = 8192, [256] * n_slices
+    lens = [70, 3, 130, 64, 20]
+    slots = [0, 2, 1, 3, 0]
+    n_slots = len(ranks)
+    x = torch.randn(sum(lens), in_dim, generator=g).bfloat16()
+    As = [(torch.randn(n_slots, r_max, in_dim, generator=g) * in_dim ** -0.5).bfloat16() for _ in outs]
+    Bs = [(torch.randn(n_slots, o, r_max, generator=g) * 0.05).bfloat16() for o in outs]
+    base = torch.randn(sum(lens), sum(outs), generator=g).bfloat16()
+    cols = [256 * s for s in range(n_slices)]
+    scal = [0.5, 1.0, 1.5, 2.0]
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", torch.bfloat16)
+    want = apply_f64(x, As, Bs, meta_cpu, base, cols)
+    kmid, kout = apply_kernel_numerics(x, As, Bs, meta_cpu, base, cols)
+    mid, out = run_hip(x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs],
+                       make_meta(lens, slots, ranks, scal, dev, torch.bfloat16), base.to(dev), cols)
+    assert_tol_f64(out, want)
+    assert_ulp_close(out, kout, what="out")
+    assert_ulp_close(mid, kmid, what="mid")

@@ -537,12 +537,28 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   const int kend = min(a.in_dim, kbeg + a.k_per_split);
   const int nst = (kend - kbeg) / kDmaKt;  // the plan makes the split a multiple of kDmaKt
 
+  // x instructions of this wave that hold rows of the segment (8 rows
+  // each): the others would only fetch the clamped last row again, so they
+  // are skipped and their LDS rows, whose products are discarded, left as
+  // they are.  The count is the same for every stage.
+  const int xi_live = min(max((rows_here - wave * XI * 8 + 7) / 8, 0), XI);
   auto issue = [&](int st) {
     unsigned char* base = lds + (st % kDmaStages) * STAGE_BYTES;
     const int k0 = kbeg + st * kDmaKt;
 #pragma unroll
     for (int i = 0; i < L; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid_t*)(src[i] + k0), (lvoid_t*)(base + lds_off[i]), 16, 0, 0);
+      if (i >= XI || i < xi_live)
+        __builtin_amdgcn_global_load_lds((gvoid_t*)(src[i] + k0), (lvoid_t*)(base + lds_off[i]), 16, 0, 0);
+  };
+  // This wave's loads per stage, for the vmcnt of a stage still in flight.
+  auto wait_one_stage_ahead = [&]() {
+    static_assert(XI == 2, "one case per live x instruction count");
+    if (xi_live == 2)
+      wait_vmcnt<(kDmaStages - 2) * (AI + 2)>();
+    else if (xi_live == 1)
+      wait_vmcnt<(kDmaStages - 2) * (AI + 1)>();
+    else
+      wait_vmcnt<(kDmaStages - 2) * AI>();
   };
 
   f32x4 acc[NBT];
@@ -554,7 +570,7 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
     if (st < nst) issue(st);
   for (int st = 0; st < nst; ++st) {
     if (st + kDmaStages - 2 < nst)
-      wait_vmcnt<(kDmaStages - 2) * L>();
+      wait_one_stage_ahead();
     else
       wait_vmcnt<0>();
     // A bare barrier: a fenced one would also wait for the stages still in

@@ -57,6 +57,10 @@ constexpr int kExpandBN = 256;  // output columns per tile
 // registers a lane, so four workgroups fit on a CU and their output tiles
 // are in flight together.
 constexpr int kExpandLongBM = 32;
+// Token rows per tile of the streamed expand (output tile staged in LDS by
+// direct-to-LDS loads, no prefetch registers), used when segments average
+// at least this many rows.
+constexpr int kExpandStreamBM = 64;
 
 struct ExpandArgs {
   const void* mid;

@@ -333,3 +333,39 @@ def test_streamed_lds_shrink_block_counts(dev, n_slices, r_max, ranks):
     assert_tol_f64(out, want)
     assert_ulp_close(out, kout, what="out")
     assert_ulp_close(mid, kmid, what="mid")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_streamed_expand_long_segments(dev, dtype):
+    """Segments of 64 rows or more on average take the expand that stages the
+    output tile in LDS (64-row tiles): slices of 1000 and 264 columns (partial
+    column tiles) at an offset inside a wider output row, a rank-0 slot,
+    ranks below r_max and segment lengths that are not multiples of 64."""
+    g = torch.Generator().manual_seed(77)
+    in_dim, r_max = 512, 32
+    outs = [1000, 264]
+    lens = [150, 65, 200, 63, 130]
+    slots = [1, 0, 3, 2, 1]
+    ranks = [32, 0, 20, 9]
+    n_slots = len(ranks)
+    assert sum(lens) >= 64 * len(lens)
+    x = torch.randn(sum(lens), in_dim, generator=g).to(dtype)
+    As = [(torch.randn(n_slots, r_max, in_dim, generator=g) * in_dim ** -0.5).to(dtype) for _ in outs]
+    Bs = [(torch.randn(n_slots, o, r_max, generator=g) * 0.05).to(dtype) for o in outs]
+    wide = torch.randn(sum(lens), 1400, generator=g).to(dtype)
+    cols = [8, 8 + outs[0]]
+    scal = [1.5, 1.0, 0.5, 2.0]
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", dtype)
+    want = apply_f64(x, As, Bs, meta_cpu, wide, cols)
+    kmid, kout = apply_kernel_numerics(x, As, Bs, meta_cpu, wide, cols)
+    mid, out = run_hip(x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs],
+                       make_meta(lens, slots, ranks, scal, dev, dtype), wide.to(dev), cols)
+    assert_tol_f64(out, want)
+    assert_ulp_close(out, kout, what="out")
+    assert_ulp_close(mid, kmid, what="mid")
+    assert torch.equal(out[:, :8], wide[:, :8]) and torch.equal(out[:, 8 + sum(outs):], wide[:, 8 + sum(outs):])
+    st = 0
+    for n, slot in zip(lens, slots):
+        if ranks[slot] == 0:  # rank-0 slot: its segments' rows are untouched
+            assert torch.equal(out[st:st + n], wide[st:st + n])
+        st += n

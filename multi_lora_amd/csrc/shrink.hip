@@ -537,28 +537,34 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   const int kend = min(a.in_dim, kbeg + a.k_per_split);
   const int nst = (kend - kbeg) / kDmaKt;  // the plan makes the split a multiple of kDmaKt
 
-  // x instructions of this wave that hold rows of the segment (8 rows
-  // each): the others would only fetch the clamped last row again, so they
-  // are skipped and their LDS rows, whose products are discarded, left as
-  // they are.  The count is the same for every stage.
+  // Instructions of this wave that hold live rows (8 rows each): x rows of
+  // the segment and A rows of the live rank blocks.  The others would only
+  // fetch a clamped row again; they are skipped and their LDS rows, whose
+  // products are discarded, left as they are.  The counts are the same for
+  // every stage.
   const int xi_live = min(max((rows_here - wave * XI * 8 + 7) / 8, 0), XI);
+  const int ai_live = min(max((nbt * 16 - wave * AI * 8 + 7) / 8, 0), AI);
   auto issue = [&](int st) {
     unsigned char* base = lds + (st % kDmaStages) * STAGE_BYTES;
     const int k0 = kbeg + st * kDmaKt;
 #pragma unroll
     for (int i = 0; i < L; ++i)
-      if (i >= XI || i < xi_live)
+      if (i < XI ? i < xi_live : i - XI < ai_live)
         __builtin_amdgcn_global_load_lds((gvoid_t*)(src[i] + k0), (lvoid_t*)(base + lds_off[i]), 16, 0, 0);
   };
-  // This wave's loads per stage, for the vmcnt of a stage still in flight.
+  // vmcnt allowing one stage of this wave's loads still in flight.
+  const int live = xi_live + ai_live;
   auto wait_one_stage_ahead = [&]() {
-    static_assert(XI == 2, "one case per live x instruction count");
-    if (xi_live == 2)
-      wait_vmcnt<(kDmaStages - 2) * (AI + 2)>();
-    else if (xi_live == 1)
-      wait_vmcnt<(kDmaStages - 2) * (AI + 1)>();
-    else
-      wait_vmcnt<(kDmaStages - 2) * AI>();
+    static_assert(L <= 6 && kDmaStages == 3, "one case per live load count");
+    switch (live) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<1>(); break;
+      case 2: wait_vmcnt<2>(); break;
+      case 3: wait_vmcnt<3>(); break;
+      case 4: wait_vmcnt<4>(); break;
+      case 5: wait_vmcnt<5>(); break;
+      default: wait_vmcnt<6>(); break;
+    }
   };
 
   f32x4 acc[NBT];

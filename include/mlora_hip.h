@@ -39,7 +39,11 @@ enum mlora_dtype { MLORA_F32 = 0, MLORA_F16 = 1, MLORA_BF16 = 2 };
  * A slot outside [0, num_slots) is treated as rank 0 (the segment is skipped),
  * a rank above the tensor's r_max is clamped to r_max, and segment bounds are
  * clamped to [0, num_rows) of the call, so an inconsistent table can produce
- * wrong rows but never an access outside the caller's tensors. */
+ * wrong rows but never an access outside the caller's tensors.  Segments are
+ * expected not to overlap: the segment kernels launch as many row tiles as
+ * non-overlapping segments of num_rows rows in all can have, and tiles
+ * beyond that (possible only when segments overlap) are not computed.
+ * max_len bounds the segment lengths the same way. */
 typedef struct mlora_seg_meta {
   const int32_t* seg_indptr;
   const int32_t* weight_indices;

@@ -6,7 +6,7 @@
 // fp32 accumulation over k < rank, multiply by the slot's scaling, round the
 // delta to the storage type, add the existing output in fp32 and round again.
 // Rank-0 segments return before touching `out`.  Unlike the reference's tiled
-// form (whose store mask omits the column bound, sgemm_lora_b.py:362-364),
+// form (whose output mask omits the column bound, sgemm_lora_b.py:88-90),
 // every access here is bounded by out_dim, so any output width is safe.
 //
 // Work decomposition (256 threads = 4 wave64s per workgroup):
@@ -14,11 +14,14 @@
 //               columns of one slice); the n-tile index runs fastest
 //   wave      = 64 output columns (4 MFMA n-blocks) x all BM tokens
 //   MFMA tile = D[n][t] += B[n][k] * mid[t][k]   (16 columns x 16 tokens)
-// The output tile is prefetched into registers before the MFMA loop so its
-// HBM latency overlaps the B/mid reads; the rounded deltas go through LDS so
-// the read-modify-write of `out` is done with row-contiguous 16-byte chunks.
-// All loads are unconditional (rows clamped, chunks masked), so they issue
-// back to back.
+// expand_kernel (32-row tiles for mixed batches, 16 for decode-shaped ones,
+// any dtype): the output tile is prefetched into registers before the MFMA
+// loop so its HBM latency overlaps the B/mid reads; the rounded deltas go
+// through LDS so the read-modify-write of `out` is done with row-contiguous
+// 16-byte chunks.  expand_dma_kernel (64-row tiles when segments are long):
+// the output tile is streamed into LDS instead and updated there.  All loads
+// are unconditional (rows clamped, chunks masked), so they issue back to
+// back.
 #include "kernels.h"
 #include "loads.h"
 

@@ -369,3 +369,37 @@ def test_streamed_expand_long_segments(dev, dtype):
         if ranks[slot] == 0:  # rank-0 slot: its segments' rows are untouched
             assert torch.equal(out[st:st + n], wide[st:st + n])
         st += n
+
+
+@pytest.mark.parametrize("part", ["qkv", "down"])
+def test_c5_mixed_batch_full_shape(dev, part):
+    """The 32-layer step's batch at its real shape: 2 x 512 prefill rows and
+    64 one-row decode segments (1088 rows, 66 segments) through the fused
+    q|k|v (4096 -> 4096/1024/1024) or the down projection (14336 -> 4096),
+    rank 16 in a 128-slot pool with adapters drawn Zipf(1.1) over 512."""
+    g = torch.Generator().manual_seed(4)
+    lens = [512, 512] + [1] * 64
+    zipf = torch.tensor([(i + 1) ** -1.1 for i in range(512)])
+    picks = torch.multinomial(zipf, len(lens), replacement=True, generator=g).tolist()
+    first = {}
+    slots = [first.setdefault(p, len(first)) for p in picks]
+    n_slots, r = 128, 16
+    ranks = [r] * len(first) + [0] * (n_slots - len(first))
+    in_dim, outs = (4096, [4096, 1024, 1024]) if part == "qkv" else (14336, [4096])
+    used = sorted(set(slots))
+    x = torch.randn(sum(lens), in_dim, generator=g).bfloat16()
+    As, Bs = [], []
+    for o in outs:
+        a = torch.zeros(n_slots, r, in_dim, dtype=torch.bfloat16)
+        b = torch.zeros(n_slots, o, r, dtype=torch.bfloat16)
+        a[used] = (torch.randn(len(used), r, in_dim, generator=g) * in_dim ** -0.5).bfloat16()
+        b[used] = (torch.randn(len(used), o, r, generator=g) * 0.02).bfloat16()
+        As.append(a)
+        Bs.append(b)
+    base = torch.randn(sum(lens), sum(outs), generator=g).bfloat16()
+    cols = [sum(outs[:i]) for i in range(len(outs))]
+    meta_cpu = make_meta(lens, slots, ranks, [2.0] * n_slots, "cpu", torch.bfloat16)
+    want = apply_f64(x, As, Bs, meta_cpu, base, cols)
+    mid, out = run_hip(x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs],
+                       make_meta(lens, slots, ranks, [2.0] * n_slots, dev, torch.bfloat16), base.to(dev), cols)
+    assert_tol_f64(out, want, f"c5 {part}")

@@ -555,15 +555,16 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   // vmcnt allowing one stage of this wave's loads still in flight.
   const int live = xi_live + ai_live;
   auto wait_one_stage_ahead = [&]() {
-    static_assert(L <= 6 && kDmaStages == 3, "one case per live load count");
+    static_assert(L <= 6, "one case per live load count");
+    constexpr int A = kDmaStages - 2;  // stages still in flight
     switch (live) {
       case 0: wait_vmcnt<0>(); break;
-      case 1: wait_vmcnt<1>(); break;
-      case 2: wait_vmcnt<2>(); break;
-      case 3: wait_vmcnt<3>(); break;
-      case 4: wait_vmcnt<4>(); break;
-      case 5: wait_vmcnt<5>(); break;
-      default: wait_vmcnt<6>(); break;
+      case 1: wait_vmcnt<A * 1>(); break;
+      case 2: wait_vmcnt<A * 2>(); break;
+      case 3: wait_vmcnt<A * 3>(); break;
+      case 4: wait_vmcnt<A * 4>(); break;
+      case 5: wait_vmcnt<A * 5>(); break;
+      default: wait_vmcnt<A * 6>(); break;
     }
   };
 

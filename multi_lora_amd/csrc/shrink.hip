@@ -445,21 +445,25 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
   if (kz == 0) zero_mid_cols<T>(a, row0, rows_here, nb_act * 16);
 }
 
-// Long segments, 16-bit types, aligned rows, K split in multiples of
-// kDmaKt: x and A stages go from HBM straight to LDS (global_load_lds_dwordx4:
-// lane l of a wave instruction fills LDS bytes [16 l, 16 l + 16) above the
-// instruction's base), kDmaStages stages in flight, so loads hold no VGPRs
-// and occupancy is set by LDS alone.  A stage is 64 x rows and NAL A rows of
-// kDmaKt elements (128 bytes, 8 chunks of 16 bytes); rows are not padded:
+// Long segments, 16-bit types, aligned rows, K split in multiples of the
+// stage width KT: x and A stages go from HBM straight to LDS
+// (global_load_lds_dwordx4: lane l of a wave instruction fills LDS bytes
+// [16 l, 16 l + 16) above the instruction's base), kDmaStages stages in
+// flight, so loads hold no VGPRs and occupancy is set by LDS alone.  A stage
+// is 64 x rows and NAL A rows of KT elements (2 KT bytes, KT / 8 chunks of 16
+// bytes); rows are not padded:
 // the chunk c of LDS row r holds source chunk c ^ dma_swz(r), which makes the
 // MFMA fragment reads (16 rows, one chunk each) hit 16 different bank groups.
 // Per stage: wait for this wave's loads of the stage (vmcnt), one barrier
 // (all waves' loads landed, the buffer of stage st - 1 is free), request
 // stage st + kDmaStages - 1 into that buffer, MFMAs from LDS.
-constexpr int kDmaKt = 64;
+constexpr int kDmaKt = 64;  // reduction elements per stage
 constexpr int kDmaStages = 3;
 
-__device__ __forceinline__ int dma_swz(int r) { return (r >> 1) & 7; }
+// Swizzle of LDS row r for rows of CPR 16-byte chunks: the 16 rows of one
+// MFMA fragment read land on 16 different 16-byte bank groups.
+template <int CPR>
+__device__ __forceinline__ int dma_swz(int r) { return (r / (16 / CPR)) & (CPR - 1); }
 
 // s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9
 // encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
@@ -472,19 +476,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
 
-template <class T, int NBT>
+template <class T, int NBT, int KT>
 __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   using raw = typename T::raw_t;
   static_assert(sizeof(raw) == 2, "16-bit types only");
   constexpr int BM = 64;
   constexpr int NAL = 16 * (NBT < 2 ? 2 : NBT);  // A rows loaded per stage (a whole instruction per wave)
   constexpr int ROWS = BM + NAL;
-  constexpr int ROW_BYTES = kDmaKt * 2;           // 128
+  constexpr int ROW_BYTES = KT * 2;               // 128 or 64
+  constexpr int CPR = KT / 8;                     // 16-byte chunks per row per stage
+  constexpr int RPI = 64 / CPR;                   // rows per wave instruction
   constexpr int STAGE_BYTES = ROWS * ROW_BYTES;
-  constexpr int XI = BM * 8 / 256;                // x instructions per wave per stage (2)
-  constexpr int AI = NAL * 8 / 256;               // A instructions per wave per stage
+  constexpr int XI = BM * CPR / 256;              // x instructions per wave per stage
+  constexpr int AI = NAL * CPR / 256;             // A instructions per wave per stage
   constexpr int L = XI + AI;                      // loads per wave per stage
-  static_assert((BM * 8) % 256 == 0 && (NAL * 8) % 256 == 0, "whole instructions per wave");
+  static_assert((BM * CPR) % 256 == 0 && (NAL * CPR) % 256 == 0, "whole instructions per wave");
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kDmaStages * STAGE_BYTES];
 
   const int tid = threadIdx.x;
@@ -510,43 +516,43 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   const int nbt = a.n_slices * nb_act;
 
   // Source of this lane's chunk in each of its load instructions: LDS row r
-  // (stage-local), LDS chunk lane % 8, source chunk (lane % 8) ^ dma_swz(r).
-  const int c8 = lane & 7;
+  // (stage-local), LDS chunk lane % CPR, source chunk (lane % CPR) ^ swz(r).
+  const int c8 = lane & (CPR - 1);
   const raw* src[L];
   int lds_off[L];  // byte offset of the instruction's first chunk within a stage
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int first = (wave * XI + i) * 64;       // chunk index within the x region
-    const int r = (first + lane) >> 3;            // x row of the tile, 0..63
+    const int r = (first + lane) / CPR;           // x row of the tile, 0..63
     src[i] = static_cast<const raw*>(a.x) + static_cast<int64_t>(min(row0 + r, end - 1)) * a.x_stride +
-             ((c8 ^ dma_swz(r)) << 3);
+             ((c8 ^ dma_swz<CPR>(r)) << 3);
     lds_off[i] = first * 16;
   }
 #pragma unroll
   for (int i = 0; i < AI; ++i) {
     const int first = (wave * AI + i) * 64;       // chunk index within the A region
-    const int ra = (first + lane) >> 3;           // A row of the stage, 0..NAL-1
+    const int ra = (first + lane) / CPR;          // A row of the stage, 0..NAL-1
     const int j = min(ra >> 4, nbt - 1);
     const int s = j / nb_act;
     const raw* arow = slice_a<raw>(a.slices, s, slot, min((j - s * nb_act) * 16 + (ra & 15), rank - 1));
-    src[XI + i] = arow + ((c8 ^ dma_swz(BM + ra)) << 3);
+    src[XI + i] = arow + ((c8 ^ dma_swz<CPR>(BM + ra)) << 3);
     lds_off[XI + i] = BM * ROW_BYTES + first * 16;
   }
 
   const int kbeg = kz * a.k_per_split;
   const int kend = min(a.in_dim, kbeg + a.k_per_split);
-  const int nst = (kend - kbeg) / kDmaKt;  // the plan makes the split a multiple of kDmaKt
+  const int nst = (kend - kbeg) / KT;  // the dispatch makes the split a multiple of KT
 
   // Instructions of this wave that hold live rows (8 rows each): x rows of
   // the segment and A rows of the live rank blocks.  The others would only
   // fetch a clamped row again; they are skipped and their LDS rows, whose
   // products are discarded, left as they are.  The counts are the same for
   // every stage.
-  const int xi_live = min(max((rows_here - wave * XI * 8 + 7) / 8, 0), XI);
-  const int ai_live = min(max((nbt * 16 - wave * AI * 8 + 7) / 8, 0), AI);
+  const int xi_live = min(max((rows_here - wave * XI * RPI + RPI - 1) / RPI, 0), XI);
+  const int ai_live = min(max((nbt * 16 - wave * AI * RPI + RPI - 1) / RPI, 0), AI);
   auto issue = [&](int st) {
     unsigned char* base = lds + (st % kDmaStages) * STAGE_BYTES;
-    const int k0 = kbeg + st * kDmaKt;
+    const int k0 = kbeg + st * KT;
 #pragma unroll
     for (int i = 0; i < L; ++i)
       if (i < XI ? i < xi_live : i - XI < ai_live)
@@ -587,14 +593,14 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
     if (st + kDmaStages - 1 < nst) issue(st + kDmaStages - 1);
     const unsigned char* base = lds + (st % kDmaStages) * STAGE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < kDmaKt / 32; ++ks) {
+    for (int ks = 0; ks < KT / 32; ++ks) {
       const int c = ks * 4 + g;
       const int xr = wave * 16 + r16;
-      const u32x4 xf = *reinterpret_cast<const u32x4*>(base + xr * ROW_BYTES + ((c ^ dma_swz(xr)) << 4));
+      const u32x4 xf = *reinterpret_cast<const u32x4*>(base + xr * ROW_BYTES + ((c ^ dma_swz<CPR>(xr)) << 4));
 #pragma unroll
       for (int j = 0; j < NBT; ++j) {
         const int ar = BM + j * 16 + r16;
-        const u32x4 af = *reinterpret_cast<const u32x4*>(base + ar * ROW_BYTES + ((c ^ dma_swz(ar)) << 4));
+        const u32x4 af = *reinterpret_cast<const u32x4*>(base + ar * ROW_BYTES + ((c ^ dma_swz<CPR>(ar)) << 4));
         acc[j] = T::mma(acc[j], af, xf);
       }
     }
@@ -715,8 +721,12 @@ hipError_t launch_nbt_al(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_
   if constexpr (AL && sizeof(typename T::raw_t) == 2 && NBT <= 8) {
     // Direct-to-LDS stages when every split is a whole number of them
     // (measured at prefill gate|up 25.3 vs 33.7 us, down 39.5 vs 43.5 us).
-    if (args.in_dim % kDmaKt == 0 && p.k_per_split % kDmaKt == 0)
-      return launch_with<T>(shrink_dma_kernel<T, NBT>, p, args, stream);
+    // 64-element stages for every block count: with eight A blocks, 32-element
+    // stages (36 KB of LDS, twice the occupancy) measured slower at prefill
+    // gate|up, 30.8 vs 26 us.
+    constexpr int KT = kDmaKt;
+    if (args.in_dim % KT == 0 && p.k_per_split % KT == 0)
+      return launch_with<T>(shrink_dma_kernel<T, NBT, KT>, p, args, stream);
     return launch_with<T>(shrink_lds_kernel<T, NBT, RB>, p, args, stream);
   }
   return launch_with<T>(shrink_rows_kernel<T, NBT, RB, AL>, p, args, stream);

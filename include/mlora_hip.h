@@ -115,6 +115,27 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
                  int32_t n_slices, int32_t r_max, void* out, int64_t out_row_stride,
                  const mlora_seg_meta* meta, int32_t dtype, void* stream);
 
+/* Bytes of workspace mlora_apply_segments needs: a mid region
+ * [num_rows, n_slices * r_max] of `dtype` (256-byte aligned), then the split
+ * sums of mlora_shrink_workspace_bytes.  0 for an invalid shape. */
+size_t mlora_apply_segments_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
+                                            int32_t bs, int32_t max_len, int32_t dtype);
+
+/* Segment shrink then expand in one call, with the same results as
+ * mlora_shrink followed by mlora_expand element for element; the rank-r
+ * intermediate lives in the workspace instead of a caller `mid`.  When the
+ * shrink's K reduction is split over workgroups (16-bit data, r_max <= 64,
+ * segments not all long) the expand adds the split sums up itself, in split
+ * order with the same rounding, and no reduce launch or mid round trip
+ * happens.  Replaces LoRABackend.apply_lora (multi_lora/backend/base.py:60-89)
+ * for batches the grouped path does not take (prefill and mixed batches).
+ * The workspace is scratch for this call only (no initialisation needed);
+ * calls that overlap in time need separate workspaces. */
+int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                         const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                         int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace mlora_apply_grouped needs for this shape and `mode`;
  * 0 when the shape is not eligible (or mode is not 0..2).  mode 2 (two
  * launches): fp32 sums of each 256-wide K chunk for every row and slice.

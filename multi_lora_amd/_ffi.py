@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MLORA_F32, MLORA_F16, MLORA_BF16 = 0, 1, 2
 MAX_SLICES = 4
@@ -29,6 +29,8 @@ EXPORTS = (
     "mlora_abi_version",
     "mlora_last_error",
     "mlora_shrink_workspace_bytes",
+    "mlora_apply_segments_workspace_bytes",
+    "mlora_apply_segments",
     "mlora_shrink",
     "mlora_expand",
     "mlora_grouped_workspace_bytes",
@@ -95,6 +97,12 @@ _SIGNATURES = {
     "mlora_abi_version": (ctypes.c_int, []),
     "mlora_last_error": (ctypes.c_char_p, []),
     "mlora_shrink_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "mlora_apply_segments_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "mlora_apply_segments": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _i32, ctypes.POINTER(Slice), _i32, _i32, _vp, _i64, ctypes.POINTER(SegMeta), _i32, _vp,
+         _sz, _vp],
+    ),
     "mlora_grouped_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "mlora_apply_grouped": (
         ctypes.c_int,

@@ -14,7 +14,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from ..kernels.lora_ops import GROUPED_MAX_LEN, LinkedWorkspace, Workspace, apply_grouped, expand, shrink
+from ..kernels.lora_ops import GROUPED_MAX_LEN, LinkedWorkspace, Workspace, apply_grouped, apply_segments, expand, shrink
 from .base import LoRABackend
 
 
@@ -55,7 +55,7 @@ class HipLoRABackend(LoRABackend):
 
         Decode-shaped batches (every segment at most 16 rows) take the
         slot-grouped path, which reads each referenced adapter once per call;
-        other batches run the segment shrink and expand.
+        other batches run the segment shrink and expand in one library call.
         """
         return self.apply_lora_multi(x, [a_stack], [b_stack], base_output, [0])
 
@@ -89,8 +89,4 @@ class HipLoRABackend(LoRABackend):
             linked_workspace=self.linked_workspace,
         ):
             return base_output
-        n = len(a_stacks)
-        r_max = a_stacks[0].shape[1]
-        mid = self.mid_buffer(x.shape[0], n * r_max, x)
-        shrink(x, a_stacks, meta, mid, workspace=self.workspace)
-        return expand(mid, b_stacks, meta, base_output, col_offsets)
+        return apply_segments(x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace)

@@ -82,27 +82,19 @@ mlora::SliceView slice_view(const mlora_slice& s) {
   return v;
 }
 
-}  // namespace
-
-extern "C" {
-
-int mlora_abi_version(void) { return 2; }
-
-const char* mlora_last_error(void) { return g_err; }
-
-size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows, int32_t bs,
-                                    int32_t max_len, int32_t dtype) {
-  if (!valid_dtype(dtype)) return 0;
-  mlora::ShrinkPlan p;
-  if (!mlora::plan_shrink(in_dim, r_max, n_slices, num_rows, bs, max_len, dtype, num_cus(), &p)) return 0;
-  return p.ws_bytes;
+// Bytes of the mid region at the start of a segment workspace (256-byte
+// aligned, so the split sums after it are too).
+size_t mid_region_bytes(int32_t rows, int32_t n_slices, int32_t r_max, int32_t dtype) {
+  const size_t b = static_cast<size_t>(rows) * n_slices * r_max * elem_bytes(dtype);
+  return (b + 255) / 256 * 256;
 }
 
-int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim, const mlora_slice* slices,
-                 int32_t n_slices, int32_t r_max, int32_t rank_mult, void* mid, int64_t mid_row_stride,
-                 const mlora_seg_meta* meta, int32_t dtype, void* workspace, size_t workspace_bytes,
-                 void* stream) {
-  g_err[0] = '\0';
+// Shrink; with skip_reduce the split sums stay in the workspace for the
+// expand (no reduce launch).
+int shrink_impl(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim, const mlora_slice* slices,
+                int32_t n_slices, int32_t r_max, int32_t rank_mult, void* mid, int64_t mid_row_stride,
+                const mlora_seg_meta* meta, int32_t dtype, void* workspace, size_t workspace_bytes, bool skip_reduce,
+                void* stream) {
   if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
   if (int rc = check_meta(meta)) return rc;
   if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
@@ -146,15 +138,17 @@ int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t 
   args.mid_stride = mid_row_stride;
   args.meta = seg_view(meta);
   args.partials = static_cast<float*>(workspace);
+  args.skip_reduce = skip_reduce ? 1 : 0;
   hipError_t e = mlora::launch_shrink(plan, args, dtype, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "shrink launch");
   return 0;
 }
 
-int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices, int32_t n_slices,
-                 int32_t r_max, void* out, int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype,
-                 void* stream) {
-  g_err[0] = '\0';
+// Expand; with partials (ks > 1) y is added up from the shrink's split sums
+// instead of read from mid.
+int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices, int32_t n_slices,
+                int32_t r_max, void* out, int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype,
+                const float* partials, int ks, void* stream) {
   if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
   if (int rc = check_meta(meta)) return rc;
   if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
@@ -197,9 +191,93 @@ int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, cons
   args.meta = seg_view(meta);
   args.m_tiles = mlora::cdiv(meta->max_len > 0 ? meta->max_len : 1, bm);
   args.n_tiles = tiles;
+  args.partials = partials;
+  args.ks = ks;
   hipError_t e = mlora::launch_expand(bm, args, dtype, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "expand launch");
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlora_abi_version(void) { return 3; }
+
+const char* mlora_last_error(void) { return g_err; }
+
+size_t mlora_shrink_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows, int32_t bs,
+                                    int32_t max_len, int32_t dtype) {
+  if (!valid_dtype(dtype)) return 0;
+  mlora::ShrinkPlan p;
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, num_rows, bs, max_len, dtype, num_cus(), &p)) return 0;
+  return p.ws_bytes;
+}
+
+int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim, const mlora_slice* slices,
+                 int32_t n_slices, int32_t r_max, int32_t rank_mult, void* mid, int64_t mid_row_stride,
+                 const mlora_seg_meta* meta, int32_t dtype, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_err[0] = '\0';
+  return shrink_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, rank_mult, mid, mid_row_stride, meta,
+                     dtype, workspace, workspace_bytes, false, stream);
+}
+
+int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices, int32_t n_slices,
+                 int32_t r_max, void* out, int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype,
+                 void* stream) {
+  g_err[0] = '\0';
+  return expand_impl(mid, mid_row_stride, num_rows, slices, n_slices, r_max, out, out_row_stride, meta, dtype, nullptr,
+                     0, stream);
+}
+
+size_t mlora_apply_segments_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
+                                            int32_t bs, int32_t max_len, int32_t dtype) {
+  if (!valid_dtype(dtype) || num_rows < 0 || r_max <= 0 || n_slices < 1) return 0;
+  mlora::ShrinkPlan p;
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, num_rows, bs, max_len, dtype, num_cus(), &p)) return 0;
+  return mid_region_bytes(num_rows, n_slices, r_max, dtype) + p.ws_bytes;
+}
+
+int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                         const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                         int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
+  if (int rc = check_meta(meta)) return rc;
+  if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
+  if (in_dim <= 0 || r_max <= 0 || num_rows < 0) return fail(kBadArg, "in_dim %d, r_max %d, num_rows %d", in_dim, r_max, num_rows);
+  if (meta->bs == 0 || num_rows == 0) return 0;
+  mlora::ShrinkPlan plan;
+  if (!mlora::plan_shrink(in_dim, r_max, n_slices, num_rows, meta->bs, meta->max_len, dtype, num_cus(), &plan))
+    return fail(kUnsupported, "shrink shape unsupported: %d slices x r_max %d exceeds 16 blocks of 16 rows",
+                n_slices, r_max);
+  const size_t mid_bytes = mid_region_bytes(num_rows, n_slices, r_max, dtype);
+  if (workspace == nullptr || workspace_bytes < mid_bytes + plan.ws_bytes)
+    return fail(kWorkspace, "segment workspace too small: need %zu bytes, got %zu", mid_bytes + plan.ws_bytes,
+                workspace_bytes);
+  // The expand adds up the split sums itself (no reduce launch, no mid)
+  // when K is split, the data is 16-bit, the rank fits its y tile, the batch
+  // is not one of long segments (those take the streamed expand, which reads
+  // mid), and the output is at most kFuseMaxTiles column tiles wide: every
+  // column tile of a row tile adds the same sums again, which costs more
+  // than the reduce launch it saves on wide outputs (measured per layer at
+  // the 32-layer step: o 20.5 vs 21.8 us, down 32.2 vs 32.9, but q|k|v 31.3
+  // vs 29.8 and gate|up 82.1 vs 64.7).
+  int col_tiles = 0;
+  for (int s = 0; s < n_slices && slices != nullptr; ++s) col_tiles += mlora::cdiv(slices[s].out_dim, mlora::kExpandBN);
+  const bool long_segments =
+      meta->max_len > 16 && static_cast<int64_t>(num_rows) >= static_cast<int64_t>(mlora::kExpandStreamBM) * meta->bs;
+  const bool fused = plan.ks > 1 && dtype != MLORA_F32 && r_max <= mlora::kFuseMaxRank && r_max % 4 == 0 &&
+                     !long_segments && col_tiles <= mlora::kFuseMaxTiles;
+  char* ws = static_cast<char*>(workspace);
+  const int64_t mid_stride = static_cast<int64_t>(n_slices) * r_max;
+  int rc = shrink_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, 1, ws, mid_stride, meta, dtype,
+                       ws + mid_bytes, plan.ws_bytes, fused, stream);
+  if (rc != 0) return rc;
+  return expand_impl(ws, mid_stride, num_rows, slices, n_slices, r_max, out, out_row_stride, meta, dtype,
+                     fused ? reinterpret_cast<const float*>(ws + mid_bytes) : nullptr, fused ? plan.ks : 0, stream);
 }
 
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,

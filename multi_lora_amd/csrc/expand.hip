@@ -29,7 +29,9 @@ namespace mlora {
 
 namespace {
 
-template <class T, int BM, bool AL>
+// FUSED: y is added up from the shrink's split sums (a separate instance, so
+// the common one keeps its registers and occupancy).
+template <class T, int BM, bool AL, bool FUSED>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -39,7 +41,9 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   constexpr int LDS_STRIDE = BN + VEC;      // padded row, keeps 16-byte alignment
   constexpr int CPR = BN / VEC;             // chunks per tile row
   constexpr int RPT = BM * CPR / 256;       // chunks per thread in the RMW
+  constexpr int YS = kFuseMaxRank + VEC;    // y tile row (split sums added here)
   __shared__ __attribute__((aligned(16))) raw delta[BM * LDS_STRIDE];
+  __shared__ __attribute__((aligned(16))) raw ytile[FUSED ? BM * YS : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -95,12 +99,48 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Split sums: the workgroup adds up the tile's y (four columns a thread,
+  // sixteen split terms in split order with zeros past ks, as the split
+  // reduce does) and rounds it into LDS; columns at and past the rank are 0.
+  if constexpr (FUSED) {
+    static_assert(sizeof(raw) == 2, "split sums are taken for 16-bit types");
+    {
+      const int ncols = a.n_slices * a.r_max;
+      const int quads = a.r_max / 4;
+      const int64_t zq = static_cast<int64_t>(a.rows) * ncols / 4;
+      for (int q = tid; q < BM * quads; q += 256) {
+        const int row = q / quads;
+        const int c4 = (q - row * quads) * 4;
+        const int t = min(row0 + row, end - 1);
+        const f32x4* p = reinterpret_cast<const f32x4*>(a.partials + static_cast<int64_t>(t) * ncols + s * a.r_max + c4);
+        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int z0 = 0; z0 < 16; z0 += 8) {
+          f32x4 v[8];
+#pragma unroll
+          for (int z = 0; z < 8; ++z) v[z] = (z0 + z < a.ks) ? p[(z0 + z) * zq] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int z = 0; z < 8; ++z) sum += v[z];
+        }
+        raw* y = ytile + row * YS + c4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = T::from_f32(c4 + e < rank ? sum[e] : 0.f);
+      }
+      __syncthreads();
+    }
+  }
+
   for (int k0 = 0; k0 < rank; k0 += KSTEP) {
     const int kk = k0 + g * VEC;
     const int valid = rank - kk;
     u32x4 yv[TB];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) yv[tb] = load_row_chunk<T, AL>(mrow[tb], kk, valid);
+    for (int tb = 0; tb < TB; ++tb) {
+      if constexpr (FUSED)
+        yv[tb] = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(ytile + (tb * 16 + r16) * YS + kk) : zero_chunk();
+      else
+        yv[tb] = load_row_chunk<T, AL>(mrow[tb], kk, valid);
+    }
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const u32x4 bv = load_row_chunk<T, AL>(brow[nb], kk, valid);
@@ -289,7 +329,14 @@ template <class T, int BM, bool AL>
 hipError_t launch_t(const ExpandArgs& args, hipStream_t stream) {
   const int64_t blocks = dense_tiles(args.meta.bs, args.m_tiles, args.rows, BM) * args.n_tiles;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((expand_kernel<T, BM, AL>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
+  if constexpr (sizeof(typename T::raw_t) == 2) {
+    if (args.ks > 1) {
+      hipLaunchKernelGGL((expand_kernel<T, BM, AL, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                         args);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((expand_kernel<T, BM, AL, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
   return hipGetLastError();
 }
 
@@ -318,7 +365,7 @@ hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipSt
   // (measured at prefill gate|up 113.9 vs 126.7 us, down 21.1 vs 21.7 us).
   // Mixed batches, whose tiles are mostly one-row decode segments, keep the
   // 32-row tiles.
-  if (aligned && bm == kExpandLongBM && (dtype == MLORA_BF16 || dtype == MLORA_F16) &&
+  if (aligned && bm == kExpandLongBM && (dtype == MLORA_BF16 || dtype == MLORA_F16) && args.ks <= 1 &&
       static_cast<int64_t>(args.rows) >= static_cast<int64_t>(kExpandStreamBM) * args.meta.bs)
     return dtype == MLORA_BF16 ? launch_streamed<BF16>(args, stream) : launch_streamed<F16>(args, stream);
   switch (dtype) {

@@ -35,6 +35,7 @@ struct ShrinkArgs {
   int ks;           // K splits per row tile
   int k_per_split;  // reduction elements per split (multiple of KSTEP)
   float* partials;  // ks > 1: [ks][rows][n_slices * r_max] fp32 split sums
+  int skip_reduce;  // ks > 1: leave the split sums for the expand (no reduce launch)
 };
 
 struct ShrinkPlan {
@@ -75,7 +76,16 @@ struct ExpandArgs {
   int m_tiles;
   int n_tiles;                     // n-tiles over all slices
   int tile_base[kMaxSlices + 1];   // first n-tile of each slice
+  // ks > 1: y is not read from `mid` but added up here from the shrink's
+  // fp32 split sums [ks][rows][n_slices * r_max], in split order, and
+  // rounded once (the values the split reduce would have written to mid).
+  const float* partials;
+  int ks;
 };
+// Largest r_max, and widest output in 256-column tiles, for which the
+// expand takes split sums.
+constexpr int kFuseMaxRank = 64;
+constexpr int kFuseMaxTiles = 16;
 
 hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream);
 

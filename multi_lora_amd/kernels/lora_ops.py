@@ -276,6 +276,48 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
     return True
 
 
+def apply_segments(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],
+                   meta: KernelInputMetaData, out: torch.Tensor, out_cols: Sequence[int],
+                   workspace: Optional[Workspace] = None) -> torch.Tensor:
+    """Segment shrink then expand into ``out`` (in place), one library call.
+
+    Same results as ``shrink`` followed by ``expand`` element for element;
+    the rank-r intermediate lives in the workspace, and where the shrink's
+    reduction is split over workgroups the expand adds the split sums up
+    itself (no reduce launch).
+    """
+    _require_gpu(x, "x")
+    dev = x.device
+    n = len(a_stacks)
+    if len(b_stacks) != n or not 1 <= n <= _ffi.MAX_SLICES:
+        raise ValueError(f"need matching A and B stacks (1..{_ffi.MAX_SLICES} slices)")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D [S, in] tensor with contiguous rows")
+    if out.dim() != 2 or out.stride(1) != 1 or out.dtype != x.dtype or out.device != dev or out.shape[0] < x.shape[0]:
+        raise ValueError("output must be a 2-D row-contiguous tensor covering x's rows, with x's dtype and device")
+    in_dim, r_max = x.shape[1], a_stacks[0].shape[1]
+    for i, (a, b) in enumerate(zip(a_stacks, b_stacks)):
+        _check_stack(a, f"A[{i}]", x.dtype, dev)
+        _check_stack(b, f"B[{i}]", x.dtype, dev)
+        if a.shape[1] != r_max or a.shape[2] != in_dim or b.shape[2] != r_max:
+            raise ValueError(f"slice {i}: A {tuple(a.shape)} / B {tuple(b.shape)} do not match r_max={r_max}, in={in_dim}")
+        if out_cols[i] < 0 or out_cols[i] + b.shape[1] > out.shape[1]:
+            raise ValueError(f"slice {i}: columns outside the output")
+    m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
+    lib = _ffi.lib()
+    dt = _ffi.dtype_code(x.dtype)
+    need = lib.mlora_apply_segments_workspace_bytes(in_dim, r_max, n, x.shape[0], m.bs, m.max_len, dt)
+    ws_ptr, ws_bytes = (workspace or _default_workspace(dev)).get(need, dev)
+    sl = _slices(a_stacks, b_stacks, out_cols)
+    rc = lib.mlora_apply_segments(
+        x.data_ptr(), x.stride(0), x.shape[0], in_dim, sl, n, r_max, out.data_ptr(), out.stride(0), ctypes.byref(m),
+        dt, ws_ptr, ws_bytes, _ffi.stream_ptr(dev),
+    )
+    _ffi.check(rc, "mlora_apply_segments")
+    del keep
+    return out
+
+
 def sgemm_lora_a_fwd(x: torch.Tensor, weights: torch.Tensor, kernel_input_metadata: KernelInputMetaData,
                      output: torch.Tensor, stack_num: int = 1) -> torch.Tensor:
     """LoRA A segment GEMM: ``output[:S, :r_max]`` = per-segment ``x @ A[slot, :r].T``.

@@ -73,27 +73,37 @@ __device__ __forceinline__ SegEntry load_seg(const SegView& m, int seg) {
   return SegEntry{seg < m.bs ? w : -1, m.indptr[sc], m.indptr[sc + 1]};
 }
 
+// One 256-segment block of the slot's row list: entry `e` of this thread;
+// `total` rows of the slot precede the block.
+__device__ __forceinline__ void slot_rows_block(const SegEntry& e, int rows, int slot, int w0, int* list, int* tmp,
+                                                int* total) {
+  int st = 0, len = 0;
+  if (e.slot == slot) {
+    st = max(e.p0, 0);
+    len = max(min(e.p1, rows) - st, 0);
+  }
+  int sum;
+  const int off = block_exclusive_scan<4>(len, tmp, &sum) + *total;
+  const int lo = max(w0 - off, 0);
+  const int hi = min(w0 + kGroupRows - off, len);
+  for (int i = lo; i < hi; ++i) list[off + i - w0] = st + i;
+  *total += sum;
+}
+
 // Rows owned by `slot` in ascending order.  Positions [w0, w0 + kGroupRows)
 // of that list go to `list`; returns the full count.  `first` is this
 // thread's entry of the first 256 segments, loaded at kernel start so the
-// table read overlaps the other first loads.  All threads call it.
+// table read overlaps the other first loads.  All threads call it.  The
+// first block is kept out of the loop over further blocks: a path that
+// joins the loop's freshly loaded entries would make the compiler wait for
+// every load in flight (the caller's A or B fragments included) before the
+// scan, instead of for `first` alone.
 __device__ int slot_rows(const SegView& m, const SegEntry& first, int rows, int slot, int w0, int* list, int* tmp) {
   int total = 0;
-  for (int base = 0; base < m.bs; base += 256) {
-    const SegEntry e = (base == 0) ? first : load_seg(m, base + threadIdx.x);
-    int st = 0, len = 0;
-    if (e.slot == slot) {
-      st = max(e.p0, 0);
-      len = max(min(e.p1, rows) - st, 0);
-    }
-    int sum;
-    const int off = block_exclusive_scan<4>(len, tmp, &sum) + total;
-    const int lo = max(w0 - off, 0);
-    const int hi = min(w0 + kGroupRows - off, len);
-    for (int i = lo; i < hi; ++i) list[off + i - w0] = st + i;
-    total += sum;
-  }
-  __syncthreads();
+  slot_rows_block(first, rows, slot, w0, list, tmp, &total);
+  for (int base = 256; base < m.bs; base += 256)
+    slot_rows_block(load_seg(m, base + threadIdx.x), rows, slot, w0, list, tmp, &total);
+  lds_barrier();
   return total;
 }
 
@@ -115,6 +125,20 @@ __device__ __forceinline__ uint32_t launch_tag() {
 
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
   return (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
+}
+
+// An empty asm that takes the registers of `r` in and out: instructions
+// that use them cannot move above it, and neither can the wait for their
+// loads.  It costs no instruction.
+template <class V, int A>
+__device__ __forceinline__ void fence_regs(V (&r)[A]) {
+#pragma unroll
+  for (int i = 0; i < A; ++i) asm volatile("" : "+v"(r[i]));
+}
+template <class V, int A, int B>
+__device__ __forceinline__ void fence_regs(V (&r)[A][B]) {
+#pragma unroll
+  for (int i = 0; i < A; ++i) fence_regs(r[i]);
 }
 
 // Linked-schedule workspace: [error word | pad to 256 B][tagged sums
@@ -153,7 +177,9 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
   const int nbt = ((a.s_groups == 1) ? a.n_slices : 1) * nb_act;
   const int kbeg = c * a.k_chunk;
 
-  // This wave's A fragments for the chunk, kept for every row tile.
+  // This wave's A fragments for the chunk, kept for every row tile.  They
+  // are loaded unmasked and masked to in_dim where the MFMA uses them, so no
+  // instruction between here and the x loads needs their data.
   u32x4 af[kGroupSteps][NBT];
 #pragma unroll
   for (int j = 0; j < NBT; ++j) {
@@ -163,7 +189,7 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
 #pragma unroll
     for (int sp = 0; sp < kGroupSteps; ++sp) {
       const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
-      af[sp][j] = load_row_chunk<T, true>(arow, kk, a.in_dim - kk);
+      af[sp][j] = ld_chunk(arow + (kk < a.in_dim ? kk : 0));
     }
   }
 
@@ -177,20 +203,30 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
       f32x4 acc[NBT];
 #pragma unroll
       for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // Both x chunks are requested before the first MFMA waits for data.
+      u32x4 xv[kGroupSteps];
 #pragma unroll
       for (int sp = 0; sp < kGroupSteps; ++sp) {
         const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
-        const u32x4 xv = load_row_chunk<T, true>(xrow, kk, a.in_dim - kk);
+        xv[sp] = load_row_chunk<T, true>(xrow, kk, a.in_dim - kk);
+      }
+      // The A fragments are masked only after this point (their mask needs
+      // their data); an empty asm that rewrites them keeps the compiler from
+      // hoisting the mask, and with it a wait for A, above the x loads.
+      fence_regs(af);
+#pragma unroll
+      for (int sp = 0; sp < kGroupSteps; ++sp) {
+        const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
 #pragma unroll
         for (int j = 0; j < NBT; ++j)
-          if (j < nbt) acc[j] = T::mma(acc[j], af[sp][j], xv);
+          if (j < nbt) acc[j] = T::mma(acc[j], af[sp][j] & keep_mask<T>(a.in_dim - kk), xv[sp]);
       }
       if (wave > 0) {
 #pragma unroll
         for (int j = 0; j < NBT; ++j)
           if (j < nbt) red[(wave - 1) * NBT + j][lane] = acc[j];
       }
-      __syncthreads();
+      lds_barrier();
       if (wave == 0) {
         // One wave's sums at a time keeps the register peak at two sets.
 #pragma unroll 1
@@ -224,7 +260,7 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
           }
         }
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
 }
@@ -254,6 +290,8 @@ template <int FMT>
 __device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, int64_t zstride) {
   float sum = 0.f;
   for (int z0 = 0; z0 < a.kc; z0 += kPollBatch) {
+    // Every word of the batch is requested before any is used: indices past
+    // the last chunk read the last chunk again (in bounds) and count as 0.
     float v[kPollBatch];
     if constexpr (FMT == kSumLinked) {
       const LinkedView lv = linked_view(a);
@@ -262,22 +300,25 @@ __device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, in
       uint64_t w[kPollBatch];
 #pragma unroll
       for (int u = 0; u < kPollBatch; ++u)
-        w[u] = (z0 + u < a.kc) ? __hip_atomic_load(p + (z0 + u) * zstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                               : tagged(tag, 0.f);
+        w[u] = __hip_atomic_load(p + min(z0 + u, a.kc - 1) * zstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int u = 0; u < kPollBatch; ++u)
-        if (static_cast<uint32_t>(w[u] >> 32) != tag) w[u] = wait_word(lv, p + (z0 + u) * zstride, tag);
+        if (z0 + u < a.kc && static_cast<uint32_t>(w[u] >> 32) != tag) w[u] = wait_word(lv, p + (z0 + u) * zstride, tag);
 #pragma unroll
-      for (int u = 0; u < kPollBatch; ++u) v[u] = __uint_as_float(static_cast<uint32_t>(w[u]));
+      for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? __uint_as_float(static_cast<uint32_t>(w[u])) : 0.f;
     } else if constexpr (FMT == kSumWord0) {
       const uint64_t* p = linked_view(a).sums + idx;
+      uint64_t w[kPollBatch];
 #pragma unroll
-      for (int u = 0; u < kPollBatch; ++u)
-        v[u] = (z0 + u < a.kc) ? __uint_as_float(static_cast<uint32_t>(p[(z0 + u) * zstride])) : 0.f;
+      for (int u = 0; u < kPollBatch; ++u) w[u] = p[min(z0 + u, a.kc - 1) * zstride];
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? __uint_as_float(static_cast<uint32_t>(w[u])) : 0.f;
     } else {
       const float* p = a.partials + idx;
 #pragma unroll
-      for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? p[(z0 + u) * zstride] : 0.f;
+      for (int u = 0; u < kPollBatch; ++u) v[u] = p[min(z0 + u, a.kc - 1) * zstride];
+#pragma unroll
+      for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? v[u] : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < kPollBatch; ++u) sum += v[u];
@@ -323,7 +364,9 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
   const int n0 = (nt_g - a.tile_base[s]) * BN;
   const int out_dim = a.slices[s].out_dim;
 
-  // B fragments: rows clamped to out_dim, K masked to the rank.
+  // B fragments: rows clamped to out_dim; loaded unmasked and masked to the
+  // rank where the MFMA uses them, so no instruction between here and the
+  // output-row loads needs their data.
   const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
   u32x4 bf[RS][NBW];
 #pragma unroll
@@ -332,7 +375,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
 #pragma unroll
     for (int ks = 0; ks < RS; ++ks) {
       const int kk = ks * KSTEP + g * VEC;
-      bf[ks][nb] = load_row_chunk<T, true>(brow, kk, rank - kk);
+      bf[ks][nb] = ld_chunk(brow + (kk < rank ? kk : 0));
     }
   }
 
@@ -355,6 +398,9 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
         const int t = lds.rows[min(tt + row, cnt - 1)];
         ov[i] = load_row_chunk<T, true>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
       }
+      // The B fragments are masked only after this point (see the A
+      // fragments in shrink_item).
+      fence_regs(bf);
       const int rows_here = min(16, cnt - tt);
       if constexpr (FMT == kSumLinked) {
         // Light polling first: one lane per K chunk waits for the word its
@@ -368,7 +414,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
           const uint32_t tag = launch_tag();
           for (int z = lane; z < a.kc; z += kWave) wait_word(lv, lv.sums + z * zstride + sidx, tag);
         }
-        __syncthreads();
+        lds_barrier();
       }
       // y = in-order sum of the K-chunk sums, rounded like the reference's
       // mid; zero at and past the rank.  One (row, column) per thread.
@@ -380,7 +426,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
           v = chunk_sum<FMT>(a, static_cast<int64_t>(lds.rows[tt + yr]) * ncols + s * a.r_max + yc, zstride);
         lds.ytile[yr * YS + yc] = T::from_f32(yc < rank ? v : 0.f);
       }
-      __syncthreads();
+      lds_barrier();
 
       f32x4 acc[NBW];
 #pragma unroll
@@ -391,7 +437,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
         const int kk = ks * KSTEP + g * VEC;
         const u32x4 yv = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(lds.ytile + r16 * YS + kk) : zero_chunk();
 #pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) acc[nb] = T::mma(acc[nb], bf[ks][nb], yv);
+        for (int nb = 0; nb < NBW; ++nb) acc[nb] = T::mma(acc[nb], bf[ks][nb] & keep_mask<T>(rank - kk), yv);
       }
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
@@ -401,7 +447,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
         w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) | (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
         *reinterpret_cast<uint2*>(lds.delta + r16 * LDS_STRIDE + (wave * NBW + nb) * 16 + 4 * g) = w;
       }
-      __syncthreads();
+      lds_barrier();
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         const int cidx = tid + i * 256;
@@ -416,10 +462,12 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
           st_chunk(out + static_cast<int64_t>(lds.rows[tt + row]) * a.out_stride + n, pack_chunk<T>(f));
         }
       }
-      __syncthreads();
+      // The output rows are used above only under a condition; this use on
+      // every path lets the next tile start without a wait for their loads.
+      fence_regs(ov);
+      lds_barrier();
     }
   }
-
 }
 
 template <class T, int NBT, int FMT>

@@ -73,8 +73,19 @@ __device__ __forceinline__ void store_row_chunk(typename T::raw_t* p, u32x4 v, i
   }
 }
 
+// Workgroup barrier that orders LDS accesses only: the fences are scoped to
+// the local address space, so the wait before s_barrier is lgkmcnt(0) and
+// global loads and stores still in flight stay in flight.  __syncthreads()
+// would also wait for vmcnt(0), i.e. for every outstanding global access.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Exclusive prefix sum of `v` over a workgroup of NW wave64s; `*total` gets
-// the sum.  `tmp` is NW ints of LDS.  Every thread of the workgroup must call it.
+// the sum.  `tmp` is NW ints of LDS.  Every thread of the workgroup must call
+// it.  Loads the caller has in flight are not waited for.
 template <int NW>
 __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63;
@@ -86,7 +97,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
     if (lane >= off) x += y;
   }
   if (lane == kWave - 1) tmp[wave] = x;
-  __syncthreads();
+  lds_barrier();
   int before = 0, all = 0;
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
@@ -94,7 +105,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int* total)
     before += (w < wave) ? t : 0;
     all += t;
   }
-  __syncthreads();
+  lds_barrier();
   *total = all;
   return before + x - v;
 }

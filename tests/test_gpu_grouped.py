@@ -94,6 +94,34 @@ def test_single_launch_ranks_and_odd_k(dev, rank, r_max):
         check(wl, mode=mode)
 
 
+@pytest.mark.parametrize("n_slots", [200, 300])
+def test_live_slots_scattered_over_the_pool(dev, n_slots):
+    """Work items are numbered over the slots with a non-zero rank.  Live
+    slots spread over several 64-slot chunks of the rank table (200 slots),
+    and a pool too large for that numbering (300: numbered by slot); segments
+    of rank-0 and out-of-pool slots keep the residual bit for bit."""
+    g = torch.Generator().manual_seed(n_slots)
+    live = [3, 64, 65, 127, 150, 199] + ([255, 256, 299] if n_slots > 256 else [])
+    ranks = [0] * n_slots
+    for i, s in enumerate(live):
+        ranks[s] = 16 if i % 2 == 0 else 8
+    rows, in_dim, out_dim = 72, 512, 768
+    slots = [live[int(i)] for i in torch.randint(0, len(live), (rows,), generator=g)]
+    slots[4], slots[9], slots[17] = 0, n_slots, -1  # rank 0, past the pool, negative
+    x = torch.randn(rows, in_dim, generator=g).bfloat16()
+    a = (torch.randn(n_slots, 16, in_dim, generator=g) * in_dim ** -0.5).bfloat16()
+    b = (torch.randn(n_slots, out_dim, 16, generator=g) * 0.05).bfloat16()
+    base = torch.randn(rows, out_dim, generator=g).bfloat16()
+    scal = [0.5 + 0.01 * i for i in range(n_slots)]
+    meta = make_meta([1] * rows, slots, ranks, scal, dev, torch.bfloat16)
+    wl = synthetic.LoRAWorkload("live_slots", x.to(dev), [a.to(dev)], [b.to(dev)], base.to(dev), meta, [0],
+                                [1] * rows, slots, ranks, scal)
+    for mode in (1, 2):
+        got = check(wl, mode=mode)
+        for r in (4, 9, 17):
+            assert torch.equal(got[r], base[r])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_grouped_matches_segment_kernels(dev, dtype):
     wl = synthetic.decode_q(device=dev, dtype=dtype, tokens=96, in_dim=2048, out=1536, n_slots=24, n_adapters=11,
@@ -169,7 +197,7 @@ def test_auto_mode_switches_schedules_on_one_workspace(dev):
         cm = cpu_meta(wl.meta)
         xs, As, Bs = wl.x.cpu(), [a.cpu() for a in wl.a_stacks], [b.cpu() for b in wl.b_stacks]
         assert_ulp_close(got, apply_kernel_numerics(xs, As, Bs, cm, wl.base.cpu(), wl.col_offsets)[1], what=wl.name)
-    assert _ffi.ABI_VERSION == 2
+    assert _ffi.lib().mlora_abi_version() == _ffi.ABI_VERSION
 
 
 def test_linked_repeated_calls_are_bit_identical(dev):

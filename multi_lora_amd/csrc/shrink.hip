@@ -769,19 +769,39 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
   if (p.bm == 16) {
     // Decode-shaped rows: enough workgroups to cover the chip twice.
     while (ks < 16 && base * ks < 2LL * num_cus && cdiv(ksteps, ks * 2) >= 16) ks *= 2;
+    const int steps_per_split = cdiv(ksteps, ks);
+    p.k_per_split = steps_per_split * kstep;
   } else {
-    // Long segments: up to three workgroups per CU, at least 512 reduction
-    // elements per split, and split sums (written and read back as fp32,
-    // 8 bytes per column and split) costing at most half the x bytes.
+    // Long segments.  Each split is a whole number of `unit` elements (the
+    // streamed kernel's 64-element stage when it will run, else one K-step).
+    // The split count is sized by the batch's rows counted in full 64-row
+    // tiles: about 1.7 workgroups of full tiles per CU, at most 12 splits.
+    // Measured on prefill gate|up / down (4073 rows: 6 splits, 25.3 / 37.5 us
+    // with the reduce, against 30 / 46 us at 8) and on the 32-layer step's
+    // mixed batch (1088 rows: 8 splits at K 4096, 12 at K 14336); neither
+    // full occupancy nor a wave count predicted these.  Splits keep at least
+    // 512 reduction elements, and split sums (written and read back as fp32,
+    // 8 bytes per column and split) cost at most the x bytes (at gate|up, six
+    // splits move 0.75 of the x bytes in sums and still beat four).
+    const bool streamed = dtype != MLORA_F32 && p.nbt <= 8 && in_dim % kDmaKt == 0;
+    const int unit = streamed ? kDmaKt : kstep;
+    const int units = cdiv(in_dim, unit);
     const int ncols = n_slices * r_max;
     const int64_t x_row_bytes = static_cast<int64_t>(in_dim) * (dtype == MLORA_F32 ? 4 : 2);
-    while (ks < 16 && base * ks < 3LL * num_cus && cdiv(ksteps, ks * 2) * kstep >= 512 &&
-           static_cast<int64_t>(ks * 2) * ncols * 8 <= x_row_bytes / 2)
-      ks *= 2;
+    const double full_tiles = rows > 64 ? rows / 64.0 : 1.0;
+    int want = static_cast<int>(1.7 * num_cus / full_tiles);
+    want = want < 1 ? 1 : (want > 12 ? 12 : want);
+    int per = cdiv(units, want);
+    for (; want > 1; --want) {
+      per = cdiv(units, want);
+      const int n = cdiv(units, per);
+      if (per * unit >= 512 && static_cast<int64_t>(n) * ncols * 8 <= x_row_bytes) break;
+    }
+    if (want == 1) per = units;
+    const int best_units = per;
+    p.k_per_split = best_units * unit;
   }
-  const int steps_per_split = cdiv(ksteps, ks);
-  p.k_per_split = steps_per_split * kstep;
-  p.ks = cdiv(ksteps, steps_per_split);
+  p.ks = cdiv(in_dim, p.k_per_split);
   p.ws_bytes = (p.ks > 1) ? static_cast<size_t>(p.ks) * rows * n_slices * r_max * sizeof(float) : 0;
   *plan = p;
   return true;

@@ -352,6 +352,13 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   }
   args.partials = static_cast<float*>(workspace);
   args.word64 = (mode == mlora::kGroupAuto && m == mlora::kGroupTwo) ? 1 : 0;
+  // The plan's chunks are the single launch's; two launches take chunks
+  // kGroupStepsTwo / kGroupStepsLinked times wider (fewer sums, so the
+  // workspace planned above is large enough).
+  if (m == mlora::kGroupTwo) {
+    k_chunk = k_chunk / mlora::kGroupStepsLinked * mlora::kGroupStepsTwo;
+    kc = mlora::cdiv(in_dim, k_chunk);
+  }
   args.kc = kc;
   args.k_chunk = k_chunk;
   args.s_groups = s_groups;

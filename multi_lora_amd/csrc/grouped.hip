@@ -8,7 +8,8 @@
 // rows come out in ascending order) and reads that slot's A / B chunk once
 // for all of them.  No planning pass and no host-side state are involved.
 //
-//   shrink item  (slot, 256-wide K chunk): the 4 waves take 2 K-steps each,
+//   shrink item  (slot, K chunk: 256 wide in the single launch, 512 with two
+//                launches): the 4 waves take 2 or 4 K-steps each,
 //                A fragments stay in registers while the slot's rows go by
 //                16 at a time; the four wave sums are added in LDS and the
 //                chunk's fp32 sums are published per (chunk, row, column).
@@ -154,8 +155,9 @@ __device__ __forceinline__ LinkedView linked_view(const GroupedArgs& a) {
 }
 
 // Shrink item (slot, slice group sg, K chunk c).  With a.s_groups == 1 the
-// item covers every slice; otherwise slice sg only.
-template <class T, int NBT, int FMT>
+// item covers every slice; otherwise slice sg only.  SP: K-steps per wave
+// (a.k_chunk = 4 * SP * KSTEP).
+template <class T, int NBT, int FMT, int SP>
 __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* s_rows, int* s_tmp,
                             f32x4 (*red)[kWave]) {
   using raw = typename T::raw_t;
@@ -180,14 +182,14 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
   // This wave's A fragments for the chunk, kept for every row tile.  They
   // are loaded unmasked and masked to in_dim where the MFMA uses them, so no
   // instruction between here and the x loads needs their data.
-  u32x4 af[kGroupSteps][NBT];
+  u32x4 af[SP][NBT];
 #pragma unroll
   for (int j = 0; j < NBT; ++j) {
     const int jj = j < nbt ? j : 0;
     const int sl = jj / nb_act;  // slice within the item
     const raw* arow = slice_a<raw>(a.slices, s_first + sl, slot, min((jj - sl * nb_act) * 16 + r16, rank - 1));
 #pragma unroll
-    for (int sp = 0; sp < kGroupSteps; ++sp) {
+    for (int sp = 0; sp < SP; ++sp) {
       const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
       af[sp][j] = ld_chunk(arow + (kk < a.in_dim ? kk : 0));
     }
@@ -204,9 +206,9 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
 #pragma unroll
       for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
       // Both x chunks are requested before the first MFMA waits for data.
-      u32x4 xv[kGroupSteps];
+      u32x4 xv[SP];
 #pragma unroll
-      for (int sp = 0; sp < kGroupSteps; ++sp) {
+      for (int sp = 0; sp < SP; ++sp) {
         const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
         xv[sp] = load_row_chunk<T, true>(xrow, kk, a.in_dim - kk);
       }
@@ -215,7 +217,7 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
       // hoisting the mask, and with it a wait for A, above the x loads.
       fence_regs(af);
 #pragma unroll
-      for (int sp = 0; sp < kGroupSteps; ++sp) {
+      for (int sp = 0; sp < SP; ++sp) {
         const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
 #pragma unroll
         for (int j = 0; j < NBT; ++j)
@@ -470,7 +472,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
   }
 }
 
-template <class T, int NBT, int FMT>
+template <class T, int NBT, int FMT, int SP>
 __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
   __shared__ int s_rows[kGroupRows];
   __shared__ int s_tmp[4];
@@ -478,7 +480,7 @@ __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
   const int per_slot = a.s_groups * a.kc;
   const int slot = blockIdx.x / per_slot;
   const int rem = blockIdx.x - slot * per_slot;
-  shrink_item<T, NBT, FMT>(a, slot, rem / a.kc, rem % a.kc, s_rows, s_tmp, red);
+  shrink_item<T, NBT, FMT, SP>(a, slot, rem / a.kc, rem % a.kc, s_rows, s_tmp, red);
 }
 
 template <class T, int FMT, int WN, int RS>
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(256, (NBT >= 8 || WN > 1) ? 2 : 4) void grouped_lin
   if (b < ns) {
     const int slot = b / per_slot;
     const int rem = b - slot * per_slot;
-    shrink_item<T, NBT, kSumLinked>(a, slot, rem / a.kc, rem % a.kc, lds.rows, lds.tmp, red);
+    shrink_item<T, NBT, kSumLinked, kGroupStepsLinked>(a, slot, rem / a.kc, rem % a.kc, lds.rows, lds.tmp, red);
   } else {
     const int e = b - ns;
     const int slot = e / a.n_tiles;
@@ -522,11 +524,11 @@ hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t s
   }
   if (phases & 1) {
     if (args.word64)
-      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumWord0>), dim3(static_cast<unsigned>(g1)), dim3(256), 0,
-                         stream, args);
+      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumWord0, kGroupStepsTwo>), dim3(static_cast<unsigned>(g1)),
+                         dim3(256), 0, stream, args);
     else
-      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumF32>), dim3(static_cast<unsigned>(g1)), dim3(256), 0,
-                         stream, args);
+      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumF32, kGroupStepsTwo>), dim3(static_cast<unsigned>(g1)),
+                         dim3(256), 0, stream, args);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -574,7 +576,7 @@ bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int*
   int b = 1;
   while (b < item_blocks) b *= 2;
   *nbt = b;
-  *k_chunk = 4 * kGroupSteps * BF16::KSTEP;
+  *k_chunk = 4 * kGroupStepsLinked * BF16::KSTEP;
   *kc = cdiv(in_dim, *k_chunk);
   const size_t words = static_cast<size_t>(*kc) * rows * n_slices * r_max;
   *linked_bytes = kLinkedHeader + words * sizeof(uint64_t);

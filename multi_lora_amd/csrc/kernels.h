@@ -95,7 +95,12 @@ hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipSt
 // once per chunk.  Shrink items leave fp32 K-chunk sums in the workspace;
 // expand items add them in chunk order and apply the expand.
 constexpr int kGroupRows = 256;  // rows gathered per pass
-constexpr int kGroupSteps = 2;   // K-steps per wave per chunk (chunk = 4 waves x 2 steps)
+// K-steps per wave per K chunk (chunk = 4 waves x steps x 32): 256-wide
+// chunks in the single launch, 512-wide with two launches (measured: decode
+// q_proj linked 8.4 vs 8.7 us with 512; q|k|v at 128 rank-32 adapters, two
+// launches with 64-bit sums, 42.4 vs 45.4 us with 256).
+constexpr int kGroupStepsLinked = 2;
+constexpr int kGroupStepsTwo = 4;
 constexpr int kGroupAuto = 0;    // mode: the library picks one of the two below
 constexpr int kGroupLinked = 1;  // mode: one launch, sums passed as tagged words
 constexpr int kGroupTwo = 2;     // mode: two launches, sums passed as plain fp32

@@ -54,6 +54,11 @@
 
 namespace mlora {
 
+// The launch's dispatch id (its AQL packet index on the hardware queue),
+// through the LLVM intrinsic; declared outside the anonymous namespace so the
+// bodiless declaration has external linkage.
+__device__ uint64_t hw_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
 namespace {
 
 // How shrink items pass their K-chunk sums to expand items.
@@ -112,8 +117,6 @@ __device__ __forceinline__ int slot_rank(const GroupedArgs& a, int slot) {
   const int r = (slot < a.meta.num_slots) ? a.meta.ranks[slot] : 0;
   return max(min(r, a.r_max), 0);
 }
-
-__device__ uint64_t hw_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
 
 // This launch's tag: odd (a zero-filled workspace never matches), equal for
 // every workgroup of the launch, different for launches on one queue fewer

@@ -111,7 +111,6 @@ __global__ __launch_bounds__(256) void shrink_kernel(ShrinkArgs a) {
   const int kbeg = kz * a.k_per_split;
   const int kend = min(a.in_dim, kbeg + a.k_per_split);
   const int nfull = (kend - kbeg) / KSTEP;
-#pragma unroll 4
   for (int i = wk; i < nfull; i += WK) {
     const int kk = kbeg + i * KSTEP + g * VEC;
     const u32x4 xv = load_row_chunk<T, AL>(xrow, kk, VEC);
@@ -152,7 +151,7 @@ __global__ __launch_bounds__(256) void shrink_kernel(ShrinkArgs a) {
     float* prow = a.partials + (static_cast<int64_t>(kz) * a.rows + t) * ncols;
 #pragma unroll
     for (int j = 0; j < NBT; ++j) {
-      if (j >= nbt) break;
+      if (j >= nbt) continue;
       const int s = j / nb_act;
       const int n = (j - s * nb_act) * 16 + 4 * g;
       const int col = s * a.r_max + n;
@@ -288,7 +287,7 @@ __global__ __launch_bounds__(256) void shrink_rows_kernel(ShrinkArgs a) {
     float* prow = a.partials + (static_cast<int64_t>(kz) * a.rows + t) * ncols;
 #pragma unroll
     for (int j = 0; j < NBT; ++j) {
-      if (j >= nbt) break;
+      if (j >= nbt) continue;
       const int s = j / nb_act;
       const int n = (j - s * nb_act) * 16 + 4 * g;
       const int col = s * a.r_max + n;

@@ -43,7 +43,19 @@ enum mlora_dtype { MLORA_F32 = 0, MLORA_F16 = 1, MLORA_BF16 = 2 };
  * expected not to overlap: the segment kernels launch as many row tiles as
  * non-overlapping segments of num_rows rows in all can have, and tiles
  * beyond that (possible only when segments overlap) are not computed.
- * max_len bounds the segment lengths the same way. */
+ * max_len bounds the segment lengths the same way.
+ *
+ * Optional host-side summary of the table (no counterpart in the reference's
+ * KernelInputMetaData; -1 in all three when not known):
+ *   long_segs    segments of more than 16 rows (after clamping to the call's
+ *                rows), and long_rows the rows they hold;
+ *   short_slots  distinct slots in [0, num_slots) among the segments of 1 to
+ *                16 rows.
+ * With it, a batch mixing long and short segments gets its expand as one
+ * launch sized to the work: tiles over the long segments, and slot-grouped
+ * items that read each adapter's B once for all of its short rows (pools of
+ * up to 2048 slots, 16-bit data, r_max <= 64).  The kernels recount both
+ * from the table, so a wrong summary costs time, never results. */
 typedef struct mlora_seg_meta {
   const int32_t* seg_indptr;
   const int32_t* weight_indices;
@@ -53,6 +65,9 @@ typedef struct mlora_seg_meta {
   int32_t max_len;
   int32_t num_slots;
   int32_t scal_dtype;
+  int32_t long_segs;
+  int32_t long_rows;
+  int32_t short_slots;
 } mlora_seg_meta;
 
 /* One LoRA slice of a (possibly fused) projection.

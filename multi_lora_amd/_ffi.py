@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MLORA_F32, MLORA_F16, MLORA_BF16 = 0, 1, 2
 MAX_SLICES = 4
@@ -41,6 +41,11 @@ EXPORTS = (
 )
 
 
+# Segments of at most this many rows are short in the table summary
+# (mlora_seg_meta.long_segs / long_rows / short_slots).
+SHORT_SEG_ROWS = 16
+
+
 class SegMeta(ctypes.Structure):
     """struct mlora_seg_meta."""
 
@@ -53,6 +58,9 @@ class SegMeta(ctypes.Structure):
         ("max_len", ctypes.c_int32),
         ("num_slots", ctypes.c_int32),
         ("scal_dtype", ctypes.c_int32),
+        ("long_segs", ctypes.c_int32),
+        ("long_rows", ctypes.c_int32),
+        ("short_slots", ctypes.c_int32),
     ]
 
 

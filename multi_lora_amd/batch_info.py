@@ -14,11 +14,15 @@ rules) so callers of the reference can switch without edits:
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
+
+# Segments of at most this many rows count as short (decode-like) in the
+# table summary; the library's mixed-batch expand uses the same bound.
+SHORT_SEG_ROWS = 16
 
 
 @dataclass
@@ -50,6 +54,33 @@ class KernelInputMetaData:
     # host mirror (a GPU table made by write_kernel_input_metadata): a
     # rewrite is then one asynchronous copy instead of five.
     packed: Optional["PackedColumns"] = None
+    # Host copies of the segment lengths and slots (set by
+    # write_kernel_input_metadata; None when unknown).  They give the
+    # library a summary of the table (table_summary) with which a batch
+    # mixing long and short segments gets one expand launch sized to it.
+    host_lens: Optional[List[int]] = None
+    host_slots: Optional[List[int]] = None
+    _summaries: Dict[int, Tuple[int, int, int]] = field(default_factory=dict, repr=False, compare=False)
+
+    def table_summary(self, num_slots: int) -> Tuple[int, int, int]:
+        """(long_segs, long_rows, short_slots) for a pool of ``num_slots``
+        slots, or (-1, -1, -1) without host copies: segments of more than 16
+        rows and the rows they hold, and the distinct in-pool slots among the
+        segments of 1 to 16 rows."""
+        if self.host_lens is None or self.host_slots is None:
+            return (-1, -1, -1)
+        got = self._summaries.get(num_slots)
+        if got is None:
+            long_lens = [n for n in self.host_lens if n > SHORT_SEG_ROWS]
+            short = {w for n, w in zip(self.host_lens, self.host_slots)
+                     if 1 <= n <= SHORT_SEG_ROWS and 0 <= w < num_slots}
+            got = self._summaries[num_slots] = (len(long_lens), sum(long_lens), len(short))
+        return got
+
+    def set_host_copies(self, lens: Sequence[int], slots: Sequence[int]) -> None:
+        self.host_lens = list(lens)
+        self.host_slots = list(slots)
+        self._summaries.clear()
 
 
 class PackedColumns:
@@ -215,6 +246,7 @@ def write_kernel_input_metadata(
         pk.write(columns)
         meta.bs = rows
         meta.max_len = max_len
+        meta.set_host_copies(lens, pool_batch.weight_indices)
         return meta
 
     if rows > meta.weight_indices.shape[0] or meta.packed is not None:
@@ -222,18 +254,21 @@ def write_kernel_input_metadata(
             pk = PackedColumns(rows, slots, device, dtype)
             pk.write(columns)
             c = pk.dev_cols
-            return KernelInputMetaData(bs=rows, seg_lens=c["seg_lens"], seg_indptr=c["seg_indptr"],
-                                       weight_indices=c["weight_indices"], lora_ranks=c["lora_ranks"],
-                                       scalings=c["scalings"], max_len=max_len, packed=pk)
-        return KernelInputMetaData(
-            bs=rows,
-            seg_lens=torch.tensor(lens, dtype=torch.int32, device=device),
-            seg_indptr=torch.tensor(indptr, dtype=torch.int32, device=device),
-            weight_indices=torch.tensor(pool_batch.weight_indices, dtype=torch.int32, device=device),
-            lora_ranks=torch.tensor(pool_batch.lora_ranks, dtype=torch.int32, device=device),
-            scalings=torch.tensor(pool_batch.scalings, dtype=dtype, device=device),
-            max_len=max_len,
-        )
+            fresh = KernelInputMetaData(bs=rows, seg_lens=c["seg_lens"], seg_indptr=c["seg_indptr"],
+                                        weight_indices=c["weight_indices"], lora_ranks=c["lora_ranks"],
+                                        scalings=c["scalings"], max_len=max_len, packed=pk)
+        else:
+            fresh = KernelInputMetaData(
+                bs=rows,
+                seg_lens=torch.tensor(lens, dtype=torch.int32, device=device),
+                seg_indptr=torch.tensor(indptr, dtype=torch.int32, device=device),
+                weight_indices=torch.tensor(pool_batch.weight_indices, dtype=torch.int32, device=device),
+                lora_ranks=torch.tensor(pool_batch.lora_ranks, dtype=torch.int32, device=device),
+                scalings=torch.tensor(pool_batch.scalings, dtype=dtype, device=device),
+                max_len=max_len,
+            )
+        fresh.set_host_copies(lens, pool_batch.weight_indices)
+        return fresh
 
     fill_column(meta.weight_indices, pool_batch.weight_indices, 0)
     fill_column(meta.lora_ranks, pool_batch.lora_ranks, 0)
@@ -242,4 +277,5 @@ def write_kernel_input_metadata(
     fill_column(meta.scalings, pool_batch.scalings, 0.0)
     meta.bs = rows
     meta.max_len = max_len
+    meta.set_host_copies(lens, pool_batch.weight_indices)
     return meta

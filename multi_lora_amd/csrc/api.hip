@@ -2,6 +2,7 @@
 // Each entry point validates its arguments on the host, picks a launch
 // shape, and launches on the caller's stream.  Nothing here allocates,
 // frees or synchronises.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -51,6 +52,8 @@ int check_meta(const mlora_seg_meta* m) {
   if (m->bs < 0 || m->max_len < 0 || m->num_slots < 0)
     return fail(kBadArg, "negative bs/max_len/num_slots (%d/%d/%d)", m->bs, m->max_len, m->num_slots);
   if (!valid_dtype(m->scal_dtype)) return fail(kBadArg, "bad scalings dtype %d", m->scal_dtype);
+  if (m->long_segs < -1 || m->long_rows < -1 || m->short_slots < -1)
+    return fail(kBadArg, "table summary below -1 (%d/%d/%d)", m->long_segs, m->long_rows, m->short_slots);
   if (m->bs > 0 && (m->seg_indptr == nullptr || m->weight_indices == nullptr || m->lora_ranks == nullptr))
     return fail(kBadArg, "null segment table pointer");
   if (m->bs > 0 && m->num_slots > 0 && m->scalings == nullptr) return fail(kBadArg, "null scalings pointer");
@@ -181,6 +184,13 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
   args.tile_base[n_slices] = tiles;
 
   const int bm = (dtype == MLORA_F32 || meta->max_len <= 16) ? 16 : mlora::kExpandLongBM;
+  // A batch mixing long and short segments, with the host's summary of the
+  // table: one launch of tiles over the long segments and slot-grouped items
+  // over the short ones.  Batches long on average keep the streamed tiles.
+  const bool mixed = bm == mlora::kExpandLongBM && aligned && (dtype == MLORA_BF16 || dtype == MLORA_F16) &&
+                     meta->long_segs >= 0 && meta->long_rows >= 0 && meta->short_slots > 0 &&
+                     meta->num_slots <= mlora::kMixedMaxSlots && r_max <= mlora::kGroupMaxRank && r_max % 8 == 0 &&
+                     static_cast<int64_t>(num_rows) < static_cast<int64_t>(mlora::kExpandStreamBM) * meta->bs;
   args.mid = mid;
   args.mid_stride = mid_row_stride;
   args.rows = num_rows;
@@ -193,7 +203,19 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
   args.n_tiles = tiles;
   args.partials = partials;
   args.ks = ks;
-  hipError_t e = mlora::launch_expand(bm, args, dtype, aligned, static_cast<hipStream_t>(stream));
+  hipError_t e;
+  if (mixed) {
+    // Tiles of 32 rows over the long segments: at most (rows + 31 * segs) / 32.
+    // At least one unit, which loops over every long tile should the summary
+    // have none (max_len > 16 says there is one).
+    const int64_t long_units = std::max<int64_t>(
+        1, (static_cast<int64_t>(meta->long_rows) + static_cast<int64_t>(mlora::kExpandLongBM - 1) * meta->long_segs) /
+               mlora::kExpandLongBM);
+    e = mlora::launch_mixed(args, dtype, static_cast<int>(long_units), meta->short_slots,
+                            static_cast<hipStream_t>(stream));
+  } else {
+    e = mlora::launch_expand(bm, args, dtype, aligned, static_cast<hipStream_t>(stream));
+  }
   if (e != hipSuccess) return hip_fail(e, "expand launch");
   return 0;
 }
@@ -202,7 +224,7 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
 
 extern "C" {
 
-int mlora_abi_version(void) { return 3; }
+int mlora_abi_version(void) { return 4; }
 
 const char* mlora_last_error(void) { return g_err; }
 

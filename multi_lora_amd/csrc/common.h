@@ -194,14 +194,16 @@ struct SegChunk {
   int total;    // tiles in the chunk
 };
 
-__device__ __forceinline__ SegChunk load_chunk(const SegView& m, int rows, int c0, int bm) {
+// Segments of at most `short_max` rows count no tiles (-1: every segment
+// counts).
+__device__ __forceinline__ SegChunk load_chunk(const SegView& m, int rows, int c0, int bm, int short_max = -1) {
   const int i = c0 + (threadIdx.x & 63);
   SegChunk c{0, 0, 0, 0, 0, 0};
   if (i < m.bs) {
     c.s = max(m.indptr[i], 0);
     c.e = min(m.indptr[i + 1], rows);
     c.w = m.widx[i];
-    c.n = c.e > c.s ? (c.e - c.s + bm - 1) / bm : 0;
+    c.n = c.e - c.s > short_max && c.e > c.s ? (c.e - c.s + bm - 1) / bm : 0;
   }
   c.incl = wave_incl_sum(c.n);
   c.total = __builtin_amdgcn_readlane(c.incl, kWave - 1);
@@ -236,6 +238,21 @@ __device__ __forceinline__ bool dense_tile_from(const SegView& m, int rows, int 
 
 __device__ __forceinline__ bool dense_tile(const SegView& m, int rows, int tile, int bm, TileRef* t) {
   return dense_tile_from(m, rows, tile, bm, 0, 0, t);
+}
+
+// Dense tiles over the segments of more than `short_max` rows only.  Scans
+// the whole table and returns the number of such tiles; *found tells
+// whether tile `tile` exists (then *t holds it).
+__device__ __forceinline__ int long_tile(const SegView& m, int rows, int tile, int bm, int short_max, TileRef* t,
+                                         bool* found) {
+  int before = 0;
+  *found = false;
+  for (int c0 = 0; c0 < m.bs; c0 += kWave) {
+    const SegChunk c = load_chunk(m, rows, c0, bm, short_max);
+    if (!*found && pick_tile(c, c0, before, tile, t)) *found = true;
+    before += c.total;
+  }
+  return before;
 }
 
 // Rank of a slot read from the table (slot already loaded): 0 outside the

@@ -22,6 +22,7 @@
 // the output tile is streamed into LDS instead and updated there.  All loads
 // are unconditional (rows clamped, chunks masked), so they issue back to
 // back.
+#include "expand_tile.h"
 #include "kernels.h"
 #include "loads.h"
 
@@ -33,160 +34,11 @@ namespace {
 // the common one keeps its registers and occupancy).
 template <class T, int BM, bool AL, bool FUSED>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
-  using raw = typename T::raw_t;
-  constexpr int VEC = T::VEC;
-  constexpr int KSTEP = T::KSTEP;
-  constexpr int BN = kExpandBN;
-  constexpr int TB = BM / 16;
-  constexpr int LDS_STRIDE = BN + VEC;      // padded row, keeps 16-byte alignment
-  constexpr int CPR = BN / VEC;             // chunks per tile row
-  constexpr int RPT = BM * CPR / 256;       // chunks per thread in the RMW
-  constexpr int YS = kFuseMaxRank + VEC;    // y tile row (split sums added here)
-  __shared__ __attribute__((aligned(16))) raw delta[BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) raw ytile[FUSED ? BM * YS : 1];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int r16 = lane & 15;
-  const int g = lane >> 4;
-
+  __shared__ __attribute__((aligned(16))) ExpandTileLds<T, BM, FUSED> lds;
   const int bid = blockIdx.x;
-  const int nt_g = bid % a.n_tiles;
   TileRef tr;
   if (!dense_tile(a.meta, a.rows, bid / a.n_tiles, BM, &tr)) return;
-  const int end = tr.end;
-  const int row0 = tr.start + tr.mt * BM;
-  const int slot = tr.slot;
-  const int rank = slot_rank_of(a.meta, slot, a.r_max, 1);
-  if (rank == 0) return;
-
-  int s = 0;
-  while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
-  const int n0 = (nt_g - a.tile_base[s]) * BN;
-  const int out_dim = a.slices[s].out_dim;
-  const float scale = load_scaling(a.meta.scalings, slot, a.meta.scal_dtype);
-
-  raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
-
-  // Prefetch this thread's share of the output tile (rows clamped to the
-  // segment; chunks past out_dim read the row start and are masked).
-  u32x4 ov[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int c = tid + i * 256;
-    const int row = c / CPR;
-    const int n = n0 + (c - row * CPR) * VEC;
-    const int t = min(row0 + row, end - 1);
-    ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
-  }
-
-  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
-  const int64_t brs = a.slices[s].b_row_stride;
-  const raw* brow[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-    brow[nb] = B + static_cast<int64_t>(min(n0 + (wave * 4 + nb) * 16 + r16, out_dim - 1)) * brs;
-  const raw* mrow[TB];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
-    mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
-               static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
-
-  f32x4 acc[4][TB];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Split sums: the workgroup adds up the tile's y (four columns a thread,
-  // sixteen split terms in split order with zeros past ks, as the split
-  // reduce does) and rounds it into LDS; columns at and past the rank are 0.
-  if constexpr (FUSED) {
-    static_assert(sizeof(raw) == 2, "split sums are taken for 16-bit types");
-    {
-      const int ncols = a.n_slices * a.r_max;
-      const int quads = a.r_max / 4;
-      const int64_t zq = static_cast<int64_t>(a.rows) * ncols / 4;
-      for (int q = tid; q < BM * quads; q += 256) {
-        const int row = q / quads;
-        const int c4 = (q - row * quads) * 4;
-        const int t = min(row0 + row, end - 1);
-        const f32x4* p = reinterpret_cast<const f32x4*>(a.partials + static_cast<int64_t>(t) * ncols + s * a.r_max + c4);
-        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int z0 = 0; z0 < 16; z0 += 8) {
-          f32x4 v[8];
-#pragma unroll
-          for (int z = 0; z < 8; ++z) v[z] = (z0 + z < a.ks) ? p[(z0 + z) * zq] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int z = 0; z < 8; ++z) sum += v[z];
-        }
-        raw* y = ytile + row * YS + c4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = T::from_f32(c4 + e < rank ? sum[e] : 0.f);
-      }
-      __syncthreads();
-    }
-  }
-
-  for (int k0 = 0; k0 < rank; k0 += KSTEP) {
-    const int kk = k0 + g * VEC;
-    const int valid = rank - kk;
-    u32x4 yv[TB];
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      if constexpr (FUSED)
-        yv[tb] = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(ytile + (tb * 16 + r16) * YS + kk) : zero_chunk();
-      else
-        yv[tb] = load_row_chunk<T, AL>(mrow[tb], kk, valid);
-    }
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const u32x4 bv = load_row_chunk<T, AL>(brow[nb], kk, valid);
-#pragma unroll
-      for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = T::mma(acc[nb][tb], bv, yv[tb]);
-    }
-  }
-
-  // Scaled, rounded deltas -> LDS as [token][column].
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int nl = (wave * 4 + nb) * 16 + 4 * g;
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int tl = tb * 16 + r16;
-      const f32x4 v = acc[nb][tb];
-      raw* p = delta + tl * LDS_STRIDE + nl;
-      if constexpr (sizeof(raw) == 2) {
-        uint2 w;
-        w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) |
-              (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
-        w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) |
-              (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
-        *reinterpret_cast<uint2*>(p) = w;
-      } else {
-        *reinterpret_cast<f32x4*>(p) = v * scale;
-      }
-    }
-  }
-  __syncthreads();
-
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int c = tid + i * 256;
-    const int row = c / CPR;
-    const int cc = c - row * CPR;
-    const int n = n0 + cc * VEC;
-    const int t = row0 + row;
-    if (t < end && n < out_dim) {
-      const u32x4 d = *reinterpret_cast<const u32x4*>(delta + row * LDS_STRIDE + cc * VEC);
-      float f[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(ov[i], e) + chunk_elem<T>(d, e);
-      store_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n);
-    }
-  }
+  expand_tile<T, BM, AL, FUSED>(a, tr, bid % a.n_tiles, lds);
 }
 
 typedef __attribute__((address_space(1))) void gvoid_t;

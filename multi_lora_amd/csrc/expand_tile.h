@@ -1,0 +1,186 @@
+// Tiled segment expand body shared by expand_kernel (expand.hip) and the
+// mixed-batch expand (grouped.hip): one workgroup's (row tile, 256-column
+// tile) of
+//   out[t, out_col_s + n] += round(scaling[slot] * sum_{k<rank} y[t, k] * B_s[slot, n, k])
+// with y read from `mid`, or (FUSED) added up from the shrink's split sums.
+//   wave      = 64 output columns (4 MFMA n-blocks) x all BM tokens
+//   MFMA tile = D[n][t] += B[n][k] * y[t][k]   (16 columns x 16 tokens)
+// The output tile is prefetched into registers before the MFMA loop so its
+// HBM latency overlaps the B / y reads; the rounded deltas go through LDS
+// so the read-modify-write of `out` is done with row-contiguous 16-byte
+// chunks.  All loads are unconditional (rows clamped, chunks masked).
+#pragma once
+
+#include "kernels.h"
+#include "loads.h"
+
+namespace mlora {
+
+// Per-workgroup LDS of expand_tile.
+template <class T, int BM, bool FUSED>
+struct ExpandTileLds {
+  using raw = typename T::raw_t;
+  static constexpr int LDS_STRIDE = kExpandBN + T::VEC;  // padded row, keeps 16-byte alignment
+  static constexpr int YS = kFuseMaxRank + T::VEC;       // y tile row (split sums added here)
+  raw delta[BM * LDS_STRIDE];
+  raw ytile[FUSED ? BM * YS : 1];
+};
+
+// Tile `tr` (rows [tr.start + tr.mt * BM, ...) of one segment), column tile
+// nt_g of the call's slices.  Every thread of the workgroup calls it.
+template <class T, int BM, bool AL, bool FUSED>
+__device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& tr, int nt_g,
+                                            ExpandTileLds<T, BM, FUSED>& lds) {
+  using raw = typename T::raw_t;
+  constexpr int VEC = T::VEC;
+  constexpr int KSTEP = T::KSTEP;
+  constexpr int BN = kExpandBN;
+  constexpr int TB = BM / 16;
+  constexpr int LDS_STRIDE = ExpandTileLds<T, BM, FUSED>::LDS_STRIDE;
+  constexpr int CPR = BN / VEC;             // chunks per tile row
+  constexpr int RPT = BM * CPR / 256;       // chunks per thread in the RMW
+  constexpr int YS = ExpandTileLds<T, BM, FUSED>::YS;
+  raw* delta = lds.delta;
+  raw* ytile = lds.ytile;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int end = tr.end;
+  const int row0 = tr.start + tr.mt * BM;
+  const int slot = tr.slot;
+  const int rank = slot_rank_of(a.meta, slot, a.r_max, 1);
+  if (rank == 0) return;
+
+  int s = 0;
+  while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
+  const int n0 = (nt_g - a.tile_base[s]) * BN;
+  const int out_dim = a.slices[s].out_dim;
+  const float scale = load_scaling(a.meta.scalings, slot, a.meta.scal_dtype);
+
+  raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
+
+  // Prefetch this thread's share of the output tile (rows clamped to the
+  // segment; chunks past out_dim read the row start and are masked).
+  u32x4 ov[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / CPR;
+    const int n = n0 + (c - row * CPR) * VEC;
+    const int t = min(row0 + row, end - 1);
+    ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
+  }
+
+  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
+  const int64_t brs = a.slices[s].b_row_stride;
+  const raw* brow[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+    brow[nb] = B + static_cast<int64_t>(min(n0 + (wave * 4 + nb) * 16 + r16, out_dim - 1)) * brs;
+  const raw* mrow[TB];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+    mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
+               static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
+
+  f32x4 acc[4][TB];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Split sums: the workgroup adds up the tile's y (four columns a thread,
+  // sixteen split terms in split order with zeros past ks, as the split
+  // reduce does) and rounds it into LDS; columns at and past the rank are 0.
+  if constexpr (FUSED) {
+    static_assert(sizeof(raw) == 2, "split sums are taken for 16-bit types");
+    {
+      const int ncols = a.n_slices * a.r_max;
+      const int quads = a.r_max / 4;
+      const int64_t zq = static_cast<int64_t>(a.rows) * ncols / 4;
+      for (int q = tid; q < BM * quads; q += 256) {
+        const int row = q / quads;
+        const int c4 = (q - row * quads) * 4;
+        const int t = min(row0 + row, end - 1);
+        const f32x4* p = reinterpret_cast<const f32x4*>(a.partials + static_cast<int64_t>(t) * ncols + s * a.r_max + c4);
+        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int z0 = 0; z0 < 16; z0 += 8) {
+          f32x4 v[8];
+#pragma unroll
+          for (int z = 0; z < 8; ++z) v[z] = (z0 + z < a.ks) ? p[(z0 + z) * zq] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int z = 0; z < 8; ++z) sum += v[z];
+        }
+        raw* y = ytile + row * YS + c4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = T::from_f32(c4 + e < rank ? sum[e] : 0.f);
+      }
+      __syncthreads();
+    }
+  }
+
+  for (int k0 = 0; k0 < rank; k0 += KSTEP) {
+    const int kk = k0 + g * VEC;
+    const int valid = rank - kk;
+    u32x4 yv[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      if constexpr (FUSED)
+        yv[tb] = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(ytile + (tb * 16 + r16) * YS + kk) : zero_chunk();
+      else
+        yv[tb] = load_row_chunk<T, AL>(mrow[tb], kk, valid);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const u32x4 bv = load_row_chunk<T, AL>(brow[nb], kk, valid);
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = T::mma(acc[nb][tb], bv, yv[tb]);
+    }
+  }
+
+  // Scaled, rounded deltas -> LDS as [token][column].
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int nl = (wave * 4 + nb) * 16 + 4 * g;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int tl = tb * 16 + r16;
+      const f32x4 v = acc[nb][tb];
+      raw* p = delta + tl * LDS_STRIDE + nl;
+      if constexpr (sizeof(raw) == 2) {
+        uint2 w;
+        w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) |
+              (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
+        w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) |
+              (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
+        *reinterpret_cast<uint2*>(p) = w;
+      } else {
+        *reinterpret_cast<f32x4*>(p) = v * scale;
+      }
+    }
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / CPR;
+    const int cc = c - row * CPR;
+    const int n = n0 + cc * VEC;
+    const int t = row0 + row;
+    if (t < end && n < out_dim) {
+      const u32x4 d = *reinterpret_cast<const u32x4*>(delta + row * LDS_STRIDE + cc * VEC);
+      float f[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(ov[i], e) + chunk_elem<T>(d, e);
+      store_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n);
+    }
+  }
+}
+
+}  // namespace mlora

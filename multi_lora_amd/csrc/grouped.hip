@@ -49,6 +49,7 @@
 //                 error word reports it.
 // Arithmetic per row is the same as the segment kernels' (fp32 sums, two
 // roundings); only the split of the K reduction differs.
+#include "expand_tile.h"
 #include "kernels.h"
 #include "loads.h"
 
@@ -65,6 +66,7 @@ namespace {
 constexpr int kSumF32 = 0;     // two launches: fp32 words
 constexpr int kSumWord0 = 1;   // two launches on a single-launch workspace: 64-bit words tagged 0
 constexpr int kSumLinked = 2;  // one launch: 64-bit words tagged with the launch, polled
+constexpr int kSumMid = 3;     // mixed-batch expand: y read from `mid` (already summed and rounded)
 constexpr int kSpinLimit = 1 << 20;   // polls before an expand item gives up
 constexpr int kPollBatch = 16;        // K-chunk words requested together
 
@@ -80,13 +82,15 @@ __device__ __forceinline__ SegEntry load_seg(const SegView& m, int seg) {
 }
 
 // One 256-segment block of the slot's row list: entry `e` of this thread;
-// `total` rows of the slot precede the block.
+// `total` rows of the slot precede the block.  short_only: segments of more
+// than kShortSegRows rows are left out.
 __device__ __forceinline__ void slot_rows_block(const SegEntry& e, int rows, int slot, int w0, int* list, int* tmp,
-                                                int* total) {
+                                                int* total, bool short_only) {
   int st = 0, len = 0;
   if (e.slot == slot) {
     st = max(e.p0, 0);
     len = max(min(e.p1, rows) - st, 0);
+    if (short_only && len > kShortSegRows) len = 0;
   }
   int sum;
   const int off = block_exclusive_scan<4>(len, tmp, &sum) + *total;
@@ -104,11 +108,12 @@ __device__ __forceinline__ void slot_rows_block(const SegEntry& e, int rows, int
 // joins the loop's freshly loaded entries would make the compiler wait for
 // every load in flight (the caller's A or B fragments included) before the
 // scan, instead of for `first` alone.
-__device__ int slot_rows(const SegView& m, const SegEntry& first, int rows, int slot, int w0, int* list, int* tmp) {
+__device__ int slot_rows(const SegView& m, const SegEntry& first, int rows, int slot, int w0, int* list, int* tmp,
+                         bool short_only) {
   int total = 0;
-  slot_rows_block(first, rows, slot, w0, list, tmp, &total);
+  slot_rows_block(first, rows, slot, w0, list, tmp, &total, short_only);
   for (int base = 256; base < m.bs; base += 256)
-    slot_rows_block(load_seg(m, base + threadIdx.x), rows, slot, w0, list, tmp, &total);
+    slot_rows_block(load_seg(m, base + threadIdx.x), rows, slot, w0, list, tmp, &total, short_only);
   lds_barrier();
   return total;
 }
@@ -199,9 +204,9 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
   }
 
   const int ncols = a.n_slices * a.r_max;
-  int total = slot_rows(a.meta, first, a.rows, slot, 0, s_rows, s_tmp);
+  int total = slot_rows(a.meta, first, a.rows, slot, 0, s_rows, s_tmp, false);
   for (int w0 = 0; w0 < total; w0 += kGroupRows) {
-    if (w0 > 0) total = slot_rows(a.meta, first, a.rows, slot, w0, s_rows, s_tmp);
+    if (w0 > 0) total = slot_rows(a.meta, first, a.rows, slot, w0, s_rows, s_tmp, false);
     const int cnt = min(kGroupRows, total - w0);
     for (int tt = 0; tt < cnt; tt += 16) {
       const raw* xrow = static_cast<const raw*>(a.x) + static_cast<int64_t>(s_rows[min(tt + r16, cnt - 1)]) * a.x_stride;
@@ -389,9 +394,9 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
   const int64_t zstride = static_cast<int64_t>(a.rows) * ncols;
   // Columns the shrink items publish: whole 16-column blocks up to the rank.
   const int live = min(((rank + 15) >> 4) * 16, a.r_max);
-  int total = slot_rows(a.meta, first, a.rows, slot, 0, lds.rows, lds.tmp);
+  int total = slot_rows(a.meta, first, a.rows, slot, 0, lds.rows, lds.tmp, a.short_only != 0);
   for (int w0 = 0; w0 < total; w0 += kGroupRows) {
-    if (w0 > 0) total = slot_rows(a.meta, first, a.rows, slot, w0, lds.rows, lds.tmp);
+    if (w0 > 0) total = slot_rows(a.meta, first, a.rows, slot, w0, lds.rows, lds.tmp, a.short_only != 0);
     const int cnt = min(kGroupRows, total - w0);
     for (int tt = 0; tt < cnt; tt += 16) {
       u32x4 ov[RPT];
@@ -427,8 +432,13 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
         const int yr = idx / a.r_max;
         const int yc = idx - yr * a.r_max;
         float v = 0.f;
-        if (yr < rows_here && yc < live)
-          v = chunk_sum<FMT>(a, static_cast<int64_t>(lds.rows[tt + yr]) * ncols + s * a.r_max + yc, zstride);
+        if (yr < rows_here && yc < live) {
+          if constexpr (FMT == kSumMid)
+            v = T::to_f32(static_cast<const raw*>(a.mid)[static_cast<int64_t>(lds.rows[tt + yr]) * a.mid_stride +
+                                                         s * a.r_max + yc]);
+          else
+            v = chunk_sum<FMT>(a, static_cast<int64_t>(lds.rows[tt + yr]) * ncols + s * a.r_max + yc, zstride);
+        }
         lds.ytile[yr * YS + yc] = T::from_f32(yc < rank ? v : 0.f);
       }
       lds_barrier();
@@ -564,6 +574,110 @@ hipError_t launch_dtype(const GroupedArgs& args, int nbt, int mode, int phases, 
   return rs1 ? launch_nbt<T, 1, 1>(args, nbt, mode, phases, stream) : launch_nbt<T, 1, 2>(args, nbt, mode, phases, stream);
 }
 
+// ---------------------------------------------------------------- mixed batches
+// Distinct slots of the short segments (1..kShortSegRows rows after clamping
+// to the call's rows, slot in [0, num_slots)), as a bitmap over the pool in
+// LDS, with each word's exclusive count of set bits in `offs`; returns how
+// many there are.  Every thread calls it.
+__device__ int short_slot_map(const GroupedArgs& a, unsigned* bits, int* offs, int* tmp) {
+  const int nwords = (a.meta.num_slots + 31) >> 5;
+  for (int i = threadIdx.x; i < nwords; i += 256) bits[i] = 0u;
+  lds_barrier();
+  for (int base = 0; base < a.meta.bs; base += 256) {
+    const int seg = base + threadIdx.x;
+    if (seg < a.meta.bs) {
+      const int p0 = max(a.meta.indptr[seg], 0);
+      const int len = min(a.meta.indptr[seg + 1], a.rows) - p0;
+      const int w = a.meta.widx[seg];
+      if (len >= 1 && len <= kShortSegRows && w >= 0 && w < a.meta.num_slots)
+        atomicOr(&bits[w >> 5], 1u << (w & 31));
+    }
+  }
+  lds_barrier();
+  const int cnt = threadIdx.x < nwords ? __popc(bits[threadIdx.x]) : 0;
+  int total;
+  const int off = block_exclusive_scan<4>(cnt, tmp, &total);
+  if (threadIdx.x < nwords) offs[threadIdx.x] = off;
+  lds_barrier();
+  return total;
+}
+
+// Slot number k (< the map's count) of the map, in increasing slot order.
+// Every thread calls it; the result is uniform.
+__device__ int short_slot(const unsigned* bits, const int* offs, int nwords, int k, int* out) {
+  const int w = threadIdx.x;
+  if (w < nwords) {
+    unsigned b = bits[w];
+    const int c = __popc(b);
+    if (k >= offs[w] && k < offs[w] + c) {
+      for (int i = offs[w]; i < k; ++i) b &= b - 1u;  // drop the lower set bits
+      *out = w * 32 + __ffs(static_cast<int>(b)) - 1;
+    }
+  }
+  lds_barrier();
+  const int slot = *out;
+  lds_barrier();
+  return slot;
+}
+
+// One launch over a mixed batch: slot-grouped items for the short segments,
+// then tiled units for the long ones (see launch_mixed).  FUSED: y from
+// the shrink's split sums (ea.partials, ea.ks splits), else from mid.
+template <class T, bool FUSED, int RS>
+__global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, GroupedArgs ga, int long_units,
+                                                              int short_units) {
+  __shared__ __attribute__((aligned(16))) ExpandTileLds<T, kExpandLongBM, FUSED> tl;
+  __shared__ __attribute__((aligned(16))) ExpandLds<T, 1> gl;
+  __shared__ unsigned bits[kMixedMaxSlots / 32];
+  __shared__ int offs[kMixedMaxSlots / 32];
+  __shared__ int pick;
+  const int nt = ea.n_tiles;
+  const int b = blockIdx.x;
+  if (b < short_units * nt) {
+    const int j = b / nt;
+    const int nt_g = b - j * nt;
+    const int n_short = short_slot_map(ga, bits, offs, gl.tmp);
+    const int nwords = (ga.meta.num_slots + 31) >> 5;
+    // More short slots than the launch has units for (a summary from an
+    // earlier table, e.g. in a replayed graph): this unit also takes slots
+    // j + short_units, j + 2 short_units, ...  These units come first in the
+    // grid, so such extra work overlaps the long tiles'.
+    for (int k = j; k < n_short; k += short_units) {
+      const int slot = short_slot(bits, offs, nwords, k, &pick);
+      expand_item<T, FUSED ? kSumF32 : kSumMid, 1, RS>(ga, slot, nt_g, gl);
+      __syncthreads();
+    }
+    return;
+  }
+  const int u = (b - short_units * nt) / nt;
+  const int nt_g = (b - short_units * nt) - u * nt;
+  TileRef tr;
+  bool found;
+  const int total = long_tile(ea.meta, ea.rows, u, kExpandLongBM, kShortSegRows, &tr, &found);
+  if (found) expand_tile<T, kExpandLongBM, true, FUSED>(ea, tr, nt_g, tl);
+  // More long tiles than the launch has units for: this unit also takes
+  // tiles u + long_units, u + 2 long_units, ...
+  for (int t = u + long_units; t < total; t += long_units) {
+    __syncthreads();
+    long_tile(ea.meta, ea.rows, t, kExpandLongBM, kShortSegRows, &tr, &found);
+    if (found) expand_tile<T, kExpandLongBM, true, FUSED>(ea, tr, nt_g, tl);
+  }
+}
+
+template <class T, bool FUSED>
+hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int long_units, int short_units,
+                          hipStream_t stream) {
+  const int64_t blocks = static_cast<int64_t>(long_units + short_units) * ea.n_tiles;
+  if (blocks <= 0) return hipSuccess;
+  if (ga.r_max <= T::KSTEP)
+    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       ea, ga, long_units, short_units);
+  else
+    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       ea, ga, long_units, short_units);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
@@ -590,6 +704,31 @@ bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int*
 hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int mode, int phases, hipStream_t stream) {
   if (dtype == MLORA_BF16) return launch_dtype<BF16>(args, nbt, mode, phases, stream);
   return launch_dtype<F16>(args, nbt, mode, phases, stream);
+}
+
+hipError_t launch_mixed(const ExpandArgs& args, int dtype, int long_units, int short_units, hipStream_t stream) {
+  GroupedArgs ga{};
+  ga.rows = args.rows;
+  for (int s = 0; s < kMaxSlices; ++s) ga.slices[s] = args.slices[s];
+  ga.n_slices = args.n_slices;
+  ga.r_max = args.r_max;
+  ga.out = args.out;
+  ga.out_stride = args.out_stride;
+  ga.meta = args.meta;
+  ga.partials = const_cast<float*>(args.partials);
+  ga.kc = args.ks > 1 ? args.ks : 1;
+  ga.n_tiles = args.n_tiles;
+  for (int s = 0; s <= kMaxSlices; ++s) ga.tile_base[s] = args.tile_base[s];
+  ga.expand_wn = 1;
+  ga.short_only = 1;
+  ga.mid = args.mid;
+  ga.mid_stride = args.mid_stride;
+  const bool fused = args.ks > 1 && args.partials != nullptr;
+  if (dtype == MLORA_BF16)
+    return fused ? launch_mixed_t<BF16, true>(args, ga, long_units, short_units, stream)
+                 : launch_mixed_t<BF16, false>(args, ga, long_units, short_units, stream);
+  return fused ? launch_mixed_t<F16, true>(args, ga, long_units, short_units, stream)
+               : launch_mixed_t<F16, false>(args, ga, long_units, short_units, stream);
 }
 
 }  // namespace mlora

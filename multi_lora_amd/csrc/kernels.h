@@ -130,10 +130,32 @@ struct GroupedArgs {
   int n_tiles;       // expand items per slot (column tiles over all slices)
   int tile_base[kMaxSlices + 1];
   int expand_wn;     // 256-column blocks per expand item (1 or 2)
+  // Mixed-batch expand (launch_mixed): expand items take the rows of the
+  // slot's short segments only (at most kShortSegRows rows), and y from
+  // `mid` (or, with split sums, from `partials` with kc = the split count).
+  int short_only;
+  const void* mid;
+  int64_t mid_stride;
 };
 
 // Largest r_max (per slice) the grouped path handles.
 constexpr int kGroupMaxRank = 64;
+
+// ------------------------------------------------------ mixed-batch expand
+// Segments of at most this many rows are "short" (decode-like) in a mixed
+// batch; the host summary in mlora_seg_meta uses the same bound.
+constexpr int kShortSegRows = 16;
+// Pools of up to this many slots (a bitmap of 32-bit words in LDS).
+constexpr int kMixedMaxSlots = 2048;
+// One launch for a batch mixing long and short segments: units
+// [0, short_units * n_tiles) are slot-grouped items (distinct slot of the
+// short segments, in slot order; 256-column tile), which read each adapter's
+// B tile once for all of that slot's short rows; the next
+// long_units * n_tiles are (32-row tile of a long segment, 256-column tile),
+// as expand_kernel's.  The kernel recounts both from the table: a count
+// given too small is covered by looping, one too large leaves units that
+// exit.
+hipError_t launch_mixed(const ExpandArgs& args, int dtype, int long_units, int short_units, hipStream_t stream);
 
 // Shape check and plan.  Workspaces: linked_bytes for the single launch
 // (header + tagged words, also used by the auto mode whichever schedule it

@@ -113,6 +113,9 @@ def seg_meta(meta: KernelInputMetaData, device: torch.device, num_slots: int) ->
         raise ValueError(f"metadata holds {widx.numel()} segments / {indptr.numel()} offsets for bs={bs}")
     if scal.numel() < ranks.numel():
         raise ValueError(f"scalings ({scal.numel()}) shorter than lora_ranks ({ranks.numel()})")
+    n_slots = min(ranks.numel(), int(num_slots))
+    summary = getattr(meta, "table_summary", None)
+    long_segs, long_rows, short_slots = summary(n_slots) if summary is not None else (-1, -1, -1)
     m = _ffi.SegMeta(
         indptr.data_ptr(),
         widx.data_ptr(),
@@ -120,8 +123,11 @@ def seg_meta(meta: KernelInputMetaData, device: torch.device, num_slots: int) ->
         scal.data_ptr(),
         bs,
         int(meta.max_len),
-        min(ranks.numel(), int(num_slots)),
+        n_slots,
         _ffi.dtype_code(scal.dtype),
+        long_segs,
+        long_rows,
+        short_slots,
     )
     return m, [indptr, widx, ranks, scal]
 

@@ -52,12 +52,14 @@ class LoRAWorkload:
 
 
 def make_meta(seg_lens: List[int], seg_slots: List[int], slot_ranks: List[int], scalings: List[float],
-              device, scal_dtype: torch.dtype) -> KernelInputMetaData:
+              device, scal_dtype: torch.dtype, host_copies: bool = True) -> KernelInputMetaData:
+    """A segment table on ``device``; ``host_copies`` keeps the host lists for
+    the table summary, as write_kernel_input_metadata does."""
     indptr = [0]
     for n in seg_lens:
         indptr.append(indptr[-1] + n)
     dev = torch.device(device)
-    return KernelInputMetaData(
+    meta = KernelInputMetaData(
         bs=len(seg_lens),
         seg_lens=torch.tensor(seg_lens, dtype=torch.int32, device=dev),
         seg_indptr=torch.tensor(indptr, dtype=torch.int32, device=dev),
@@ -66,6 +68,9 @@ def make_meta(seg_lens: List[int], seg_slots: List[int], slot_ranks: List[int], 
         scalings=torch.tensor(scalings, dtype=scal_dtype, device=dev),
         max_len=max(seg_lens) if seg_lens else 0,
     )
+    if host_copies:
+        meta.set_host_copies(seg_lens, seg_slots)
+    return meta
 
 
 def _normal(g: torch.Generator, shape, std: float, mean: float = 0.0) -> torch.Tensor:

@@ -90,3 +90,97 @@ def test_backend_mixed_batch_uses_one_call_and_replays_in_a_graph(dev):
         torch.cuda.synchronize()
         _, want = run_hip(xd, Ad, Bd, meta, base.to(dev), cols)
         assert torch.equal(out.cpu(), want), f"replay {rep}"
+
+
+def zipf_slots(g, n, n_adapters, n_slots):
+    """Slots of n requests drawn Zipf(1.1) over n_adapters adapters, the
+    adapters placed in pool slots in order of first appearance."""
+    zipf = torch.tensor([(i + 1) ** -1.1 for i in range(n_adapters)])
+    picks = torch.multinomial(zipf, n, replacement=True, generator=g).tolist()
+    first = {}
+    return [first.setdefault(p, len(first)) % n_slots for p in picks]
+
+
+MIXED_CASES = [
+    # name, lens, slots (None: Zipf), ranks, in_dim, outs, r_max, dtype
+    # wide outputs: the expand reads mid; two long segments and 64 one-row ones
+    ("wide_mid", [512, 512] + [1] * 64, None, [16] * 48 + [0] * 16, 1024, [4096, 1024, 1024], 16, torch.bfloat16),
+    # narrow output with split K: the expand adds the split sums
+    ("narrow_split", [300, 90] + [1] * 40, None, [16] * 40, 4096, [1024], 16, torch.bfloat16),
+    # r_max 64, ranks below it (stale tails), fp16, short segments of 2..16 rows
+    ("r64_f16", [200, 40, 3, 16, 7, 1, 2, 17, 9, 1, 5, 0, 12],
+     [0, 1, 2, 3, 2, 0, 1, 4, 3, 2, 5, 1, 0], [64, 40, 16, 33, 64, 8], 2048, [768, 512], 64, torch.float16),
+    # rank-0, out-of-pool and empty short segments next to live ones
+    ("odd_slots", [100, 1, 1, 4, 1, 0, 3, 1, 33], [0, 9, -1, 1, 2, 1, 1, 3, 2], [16, 16, 0, 16], 1024, [512], 16,
+     torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("name,lens,slots,ranks,in_dim,outs,r_max,dtype", MIXED_CASES)
+def test_mixed_batch_expand_equals_tiled(dev, name, lens, slots, ranks, in_dim, outs, r_max, dtype):
+    """With the host summary, a batch mixing long and short segments takes
+    the one-launch mixed expand (slot-grouped items for the short segments);
+    without it, every segment is tiled.  Results are equal bit for bit, also
+    when the summary is wrong (too small: units loop; too large: units exit),
+    and match the oracle."""
+    g = torch.Generator().manual_seed(len(name))
+    if slots is None:
+        slots = [0] * 2 + zipf_slots(g, len(lens) - 2, 512, len(ranks))
+    x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, len(name))
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+
+    def run(meta):
+        out = base.to(dev).clone()
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=Workspace())
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    tiled = run(make_meta(lens, slots, ranks, scal, dev, dtype, host_copies=False))
+    hinted = make_meta(lens, slots, ranks, scal, dev, dtype)
+    long_segs, long_rows, short_slots = hinted.table_summary(len(ranks))
+    assert long_segs > 0 and short_slots > 0, "the case must mix long and short segments"
+    assert torch.equal(run(hinted), tiled), f"{name}: mixed expand differs from the tiled one"
+    for wrong in ((1, 1, 1), (long_segs, long_rows, max(1, short_slots // 3)), (long_segs + 5, long_rows + 900,
+                                                                               short_slots + 7)):
+        bad = make_meta(lens, slots, ranks, scal, dev, dtype)
+        bad.table_summary = lambda n, w=wrong: w
+        assert torch.equal(run(bad), tiled), f"{name}: summary {wrong} changed the result"
+    assert_tol_f64(tiled, apply_f64(x, As, Bs, meta_cpu, base, cols), name)
+
+
+def test_mixed_batch_expand_in_a_replayed_graph_follows_table_rewrites(dev):
+    """A captured mixed expand keeps the launch size of its capture; after an
+    in-place rewrite that gives the short segments more distinct slots, the
+    replay still equals the tiled result (the kernel recounts and loops)."""
+    g = torch.Generator().manual_seed(77)
+    lens = [256, 200] + [1] * 48
+    ranks = [16] * 64
+    slots0 = [0, 1] + [2 + (i % 4) for i in range(48)]          # 4 distinct short slots at capture
+    slots1 = [0, 1] + zipf_slots(g, 48, 64, 64)                   # many more after the rewrite
+    x, As, Bs, base, cols, _, scal = case(dev, lens, slots0, ranks, 2048, [4096, 1024], 16, torch.bfloat16, 3)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    meta = make_meta(lens, slots0, ranks, scal, dev, torch.bfloat16)
+    assert meta.table_summary(64)[2] == 4
+    out = base.to(dev).clone()
+    ws = Workspace()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)
+    for rep, slots in enumerate((slots0, slots1, slots1, slots0)):
+        meta.weight_indices.copy_(torch.tensor(slots, dtype=torch.int32))
+        meta.set_host_copies(lens, slots)
+        out.copy_(base.to(dev))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = base.to(dev).clone()
+        apply_segments(xd, Ad, Bd, make_meta(lens, slots, ranks, scal, dev, torch.bfloat16, host_copies=False), want,
+                       cols, workspace=Workspace())
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want.cpu()), f"replay {rep}"

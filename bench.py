@@ -424,7 +424,7 @@ def bench_other(args) -> int:
         add_bytes = 4 * S * in_dim * e + in_dim * e
         parts = {"rmsnorm": (norm, norm_bytes), "grouped (3 slices, the library's schedule)": (lora, lora_bytes),
                  "grouped linked (schedule comparison)": (lora_linked, lora_bytes),
-                 "grouped two launches, fp32 sums (schedule comparison)": (lora_two, lora_bytes),
+                 "grouped two launches, mode 2 on its own workspace (schedule comparison)": (lora_two, lora_bytes),
                  "add_rmsnorm fused (schedule comparison)": (add_norm, add_bytes),
                  "add then rmsnorm, unfused (schedule comparison)": (add_then_norm, add_bytes)}
         path = ("rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-grouped; the library picks the "

@@ -154,9 +154,10 @@ int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, 
 /* Bytes of workspace mlora_apply_grouped needs for this shape and `mode`;
  * 0 when the shape is not eligible (or mode is not 0..2).  mode 2 (two
  * launches): fp32 sums of each 256-wide K chunk for every row and slice.
- * modes 1 and 0: a 256-byte header (error word) and the same sums as 64-bit
- * tagged words.  `num_slots` is accepted for layouts that depend on it; none
- * does now. */
+ * mode 1: a 256-byte header (error word) and the same sums as 64-bit tagged
+ * words.  mode 0: mode 1's layout, then (at the next 256-byte boundary) mode
+ * 2's, for the calls it runs as two launches.  `num_slots` is accepted for
+ * layouts that depend on it; none does now. */
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
                                      int32_t num_slots, int32_t dtype, int32_t mode);
 
@@ -173,8 +174,8 @@ size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_sl
  * dispatch id on its hardware queue);
  * 0 = the library's choice per call: the single launch while all work items
  * fit on the chip at once (num_slots * items per slot <= 16 per CU), else
- * two launches that pass their sums as words tagged 0 in the same workspace
- * (single-launch tags are odd, so neither schedule mistakes the other's).
+ * two launches whose fp32 sums go to the region after the tagged words, so
+ * neither schedule ever reads the other's sums.
  * The workspace of modes 0 and 1 must be zero-filled before its first use,
  * passed to nothing but calls of the same mode afterwards, and used from one
  * stream only (give each stream its own); it is never cleared between calls.

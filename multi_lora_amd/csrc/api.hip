@@ -222,6 +222,21 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
 
 }  // namespace
 
+namespace {
+
+// Workspace of mlora_apply_grouped: mode 2 the fp32 sums; mode 1 the linked
+// header and words; mode 0 the linked region, then (256-byte aligned) an
+// fp32 region for the calls it runs as two launches.
+size_t auto_plain_offset(size_t linked) { return (linked + 255) / 256 * 256; }
+
+size_t grouped_ws_bytes(int mode, size_t linked, size_t plain) {
+  if (mode == mlora::kGroupTwo) return plain;
+  if (mode == mlora::kGroupLinked) return linked;
+  return auto_plain_offset(linked) + plain;
+}
+
+}  // namespace
+
 extern "C" {
 
 int mlora_abi_version(void) { return 4; }
@@ -310,7 +325,7 @@ size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_sl
   if (mode < 0 || mode > 2) return 0;
   if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &s_groups, &linked, &plain))
     return 0;
-  return (mode == mlora::kGroupTwo) ? plain : linked;
+  return grouped_ws_bytes(mode, linked, plain);
 }
 
 int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
@@ -335,7 +350,7 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &s_groups, &linked, &plain))
     return fail(kUnsupported, "grouped path needs bf16/fp16, r_max <= %d and a multiple of 8, in_dim a multiple of 8",
                 mlora::kGroupMaxRank);
-  const size_t ws = (mode == mlora::kGroupTwo) ? plain : linked;
+  const size_t ws = grouped_ws_bytes(mode, linked, plain);
   if (workspace == nullptr || workspace_bytes < ws)
     return fail(kWorkspace, "grouped workspace too small: need %zu bytes, got %zu", ws, workspace_bytes);
   const int vec = vec_elems(dtype);
@@ -372,8 +387,11 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
     const int64_t items = static_cast<int64_t>(meta->num_slots) * (s_groups * kc + tiles);
     m = (items <= static_cast<int64_t>(mlora::kLinkedItemsPerCu) * num_cus()) ? mlora::kGroupLinked : mlora::kGroupTwo;
   }
+  // Mode 0's two launches use the fp32 region after the linked words, so a
+  // later single launch on this workspace never reads their sums as words.
   args.partials = static_cast<float*>(workspace);
-  args.word64 = (mode == mlora::kGroupAuto && m == mlora::kGroupTwo) ? 1 : 0;
+  if (mode == mlora::kGroupAuto && m == mlora::kGroupTwo)
+    args.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + auto_plain_offset(linked));
   // The plan's chunks are the single launch's; two launches take chunks
   // kGroupStepsTwo / kGroupStepsLinked times wider (fewer sums, so the
   // workspace planned above is large enough).

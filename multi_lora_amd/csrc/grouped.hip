@@ -64,7 +64,6 @@ namespace {
 
 // How shrink items pass their K-chunk sums to expand items.
 constexpr int kSumF32 = 0;     // two launches: fp32 words
-constexpr int kSumWord0 = 1;   // two launches on a single-launch workspace: 64-bit words tagged 0
 constexpr int kSumLinked = 2;  // one launch: 64-bit words tagged with the launch, polled
 constexpr int kSumMid = 3;     // mixed-batch expand: y read from `mid` (already summed and rounded)
 constexpr int kSpinLimit = 1 << 20;   // polls before an expand item gives up
@@ -259,11 +258,6 @@ __device__ void shrink_item(const GroupedArgs& a, int slot, int sg, int c, int* 
 #pragma unroll
               for (int q = 0; q < 4; ++q)
                 __hip_atomic_store(p + q, tagged(tag, acc[j][q]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else if constexpr (FMT == kSumWord0) {
-              // Tag 0 is even: no single launch's (odd) tag ever matches it.
-              uint64_t* p = linked_view(a).sums + rowoff + s * a.r_max + n;
-#pragma unroll
-              for (int q = 0; q < 4; ++q) p[q] = tagged(0u, acc[j][q]);
             } else {
               *reinterpret_cast<f32x4*>(a.partials + rowoff + s * a.r_max + n) = acc[j];
             }
@@ -314,13 +308,6 @@ __device__ __forceinline__ float chunk_sum(const GroupedArgs& a, int64_t idx, in
 #pragma unroll
       for (int u = 0; u < kPollBatch; ++u)
         if (z0 + u < a.kc && static_cast<uint32_t>(w[u] >> 32) != tag) w[u] = wait_word(lv, p + (z0 + u) * zstride, tag);
-#pragma unroll
-      for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? __uint_as_float(static_cast<uint32_t>(w[u])) : 0.f;
-    } else if constexpr (FMT == kSumWord0) {
-      const uint64_t* p = linked_view(a).sums + idx;
-      uint64_t w[kPollBatch];
-#pragma unroll
-      for (int u = 0; u < kPollBatch; ++u) w[u] = p[min(z0 + u, a.kc - 1) * zstride];
 #pragma unroll
       for (int u = 0; u < kPollBatch; ++u) v[u] = (z0 + u < a.kc) ? __uint_as_float(static_cast<uint32_t>(w[u])) : 0.f;
     } else {
@@ -536,22 +523,14 @@ hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t s
     return hipGetLastError();
   }
   if (phases & 1) {
-    if (args.word64)
-      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumWord0, kGroupStepsTwo>), dim3(static_cast<unsigned>(g1)),
-                         dim3(256), 0, stream, args);
-    else
-      hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumF32, kGroupStepsTwo>), dim3(static_cast<unsigned>(g1)),
-                         dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((grouped_shrink_kernel<T, NBT, kSumF32, kGroupStepsTwo>), dim3(static_cast<unsigned>(g1)), dim3(256), 0,
+                       stream, args);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (phases & 2) {
-    if (args.word64)
-      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumWord0, WN, RS>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
-                         args);
-    else
-      hipLaunchKernelGGL((grouped_expand_kernel<T, kSumF32, WN, RS>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
-                         args);
+    hipLaunchKernelGGL((grouped_expand_kernel<T, kSumF32, WN, RS>), dim3(static_cast<unsigned>(g2)), dim3(256), 0, stream,
+                       args);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -126,7 +126,6 @@ struct GroupedArgs {
   int kc;            // K chunks
   int k_chunk;       // reduction elements per chunk
   int s_groups;      // shrink items per (slot, chunk): 1 (all slices) or n_slices (one each)
-  int word64;        // two launches: sums as tag-0 words of a single-launch workspace
   int n_tiles;       // expand items per slot (column tiles over all slices)
   int tile_base[kMaxSlices + 1];
   int expand_wn;     // 256-column blocks per expand item (1 or 2)

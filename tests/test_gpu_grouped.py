@@ -182,7 +182,7 @@ def test_linked_workspace_reused_across_shapes(dev):
 
 def test_auto_mode_switches_schedules_on_one_workspace(dev):
     """Mode 0 takes the single launch for small batches and two launches for
-    large ones (words tagged 0 in the same workspace); alternating between
+    large ones (fp32 sums in the region after the tagged words); alternating between
     them, with shapes changing, every call still matches the oracle."""
     from multi_lora_amd import _ffi
 

@@ -96,7 +96,8 @@ def test_errors_map_to_reference_exception_types():
 def test_grouped_workspace_sizes():
     """Workspace sizes are host arithmetic: K chunks of 256 x rows x columns,
     fp32 for two launches; 64-bit words plus a 256-byte header for the single
-    launch and for the library's choice; 0 for ineligible shapes."""
+    launch; for the library's choice both, the fp32 region starting at the
+    next 256-byte boundary after the words; 0 for ineligible shapes."""
     lib = _ffi.lib()
     bf = _ffi.MLORA_BF16
     kc = 4096 // 256
@@ -104,8 +105,8 @@ def test_grouped_workspace_sizes():
     assert two == kc * 128 * 16 * 4
     one = lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 1)
     assert one == 256 + kc * 128 * 16 * 8
-    # auto mode: the single-launch layout, whichever schedule a call takes
-    assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 0) == one
+    # auto mode: the single-launch layout, then the two-launch region
+    assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 0) == (one + 255) // 256 * 256 + two
     assert lib.mlora_grouped_workspace_bytes(4104, 16, 3, 10, 65, bf, 1) == 256 + 17 * 10 * 48 * 8
     assert lib.mlora_grouped_workspace_bytes(4100, 16, 1, 10, 65, bf, 1) == 0                # in_dim % 8
     assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, _ffi.MLORA_F32, 1) == 0   # fp32 not grouped

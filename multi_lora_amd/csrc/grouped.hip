@@ -483,8 +483,11 @@ __global__ __launch_bounds__(256) void grouped_shrink_kernel(GroupedArgs a) {
   shrink_item<T, NBT, FMT, SP>(a, slot, rem / a.kc, rem % a.kc, s_rows, s_tmp, red);
 }
 
+// Four workgroups a CU except for 512-column items at r_max > 32 (169
+// VGPRs).  512-column items at r_max <= 32 fit in 126 VGPRs without spills:
+// q|k|v at 128 rank-32 adapters 39.5 vs 40.0 us for the pair at three a CU.
 template <class T, int FMT, int WN, int RS>
-__global__ __launch_bounds__(256, WN == 1 ? 4 : 2) void grouped_expand_kernel(GroupedArgs a) {
+__global__ __launch_bounds__(256, WN == 1 || RS == 1 ? 4 : 2) void grouped_expand_kernel(GroupedArgs a) {
   __shared__ __attribute__((aligned(16))) ExpandLds<T, WN> lds;
   const int slot = blockIdx.x / a.n_tiles;
   expand_item<T, FMT, WN, RS>(a, slot, blockIdx.x - slot * a.n_tiles, lds);

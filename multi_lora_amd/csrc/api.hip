@@ -172,6 +172,9 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
     const mlora_slice& sl = slices[s];
     if (sl.b == nullptr) return fail(kBadArg, "slice %d: B is null", s);
     if (sl.out_dim <= 0 || sl.out_col < 0) return fail(kBadArg, "slice %d: out_dim %d, out_col %d", s, sl.out_dim, sl.out_col);
+    if (static_cast<int64_t>(sl.out_col) + sl.out_dim > out_row_stride)
+      return fail(kBadArg, "slice %d: columns [%d, %lld) exceed the output row stride %lld", s, sl.out_col,
+                  static_cast<long long>(sl.out_col) + sl.out_dim, (long long)out_row_stride);
     if (sl.b_row_stride < r_max || sl.b_slot_stride < static_cast<int64_t>(sl.out_dim) * sl.b_row_stride)
       return fail(kBadArg, "slice %d: B strides (%lld, %lld) do not hold [out=%d, r_max=%d] rows", s,
                   (long long)sl.b_slot_stride, (long long)sl.b_row_stride, sl.out_dim, r_max);
@@ -362,6 +365,9 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
     const mlora_slice& sl = slices[s];
     if (sl.a == nullptr || sl.b == nullptr) return fail(kBadArg, "slice %d: A or B is null", s);
     if (sl.out_dim <= 0 || sl.out_col < 0) return fail(kBadArg, "slice %d: out_dim %d, out_col %d", s, sl.out_dim, sl.out_col);
+    if (static_cast<int64_t>(sl.out_col) + sl.out_dim > out_row_stride)
+      return fail(kBadArg, "slice %d: columns [%d, %lld) exceed the output row stride %lld", s, sl.out_col,
+                  static_cast<long long>(sl.out_col) + sl.out_dim, (long long)out_row_stride);
     if (sl.a_row_stride < in_dim || sl.a_slot_stride < static_cast<int64_t>(r_max) * sl.a_row_stride ||
         sl.b_row_stride < r_max || sl.b_slot_stride < static_cast<int64_t>(sl.out_dim) * sl.b_row_stride)
       return fail(kBadArg, "slice %d: A/B strides do not hold their [r_max, in] / [out, r_max] rows", s);

@@ -181,6 +181,7 @@ template <class T, int BM, bool AL>
 hipError_t launch_t(const ExpandArgs& args, hipStream_t stream) {
   const int64_t blocks = dense_tiles(args.meta.bs, args.m_tiles, args.rows, BM) * args.n_tiles;
   if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   if constexpr (sizeof(typename T::raw_t) == 2) {
     if (args.ks > 1) {
       hipLaunchKernelGGL((expand_kernel<T, BM, AL, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
@@ -207,6 +208,7 @@ hipError_t launch_streamed(ExpandArgs args, hipStream_t stream) {
   args.m_tiles = (args.m_tiles + 1) / 2;
   const int64_t blocks = dense_tiles(args.meta.bs, args.m_tiles, args.rows, BM) * args.n_tiles;
   if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((expand_dma_kernel<T, BM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
   return hipGetLastError();
 }

@@ -520,6 +520,7 @@ hipError_t launch_t(const GroupedArgs& args, int mode, int phases, hipStream_t s
   const int64_t g1 = static_cast<int64_t>(args.meta.num_slots) * args.s_groups * args.kc;
   const int64_t g2 = static_cast<int64_t>(args.meta.num_slots) * args.n_tiles;
   if (g1 <= 0 || g2 <= 0) return hipSuccess;
+  if (!grid_fits(g1 + g2)) return hipErrorInvalidConfiguration;
   if (mode == kGroupLinked) {
     hipLaunchKernelGGL((grouped_linked_kernel<T, NBT, WN, RS>), dim3(static_cast<unsigned>(g1 + g2)), dim3(256), 0, stream,
                        args);
@@ -649,8 +650,9 @@ __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, Gro
 template <class T, bool FUSED>
 hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int long_units, int short_units,
                           hipStream_t stream) {
-  const int64_t blocks = static_cast<int64_t>(long_units + short_units) * ea.n_tiles;
+  const int64_t blocks = (static_cast<int64_t>(long_units) + short_units) * ea.n_tiles;
   if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   if (ga.r_max <= T::KSTEP)
     hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                        ea, ga, long_units, short_units);

@@ -8,6 +8,12 @@ namespace mlora {
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// A launch's work-items per grid dimension must fit in 32 bits: at most this
+// many 256-thread workgroups.  Launchers return hipErrorInvalidConfiguration
+// beyond it instead of launching a truncated grid.
+constexpr int64_t kMaxBlocks = ((int64_t{1} << 32) - 1) / 256;
+inline bool grid_fits(int64_t blocks) { return blocks <= kMaxBlocks; }
+
 // Workgroups that cover every dense row tile of bm rows (dense_tile): each
 // segment has ceil(len / bm) tiles and the segments' lengths add up to at
 // most `rows`, so there are at most (rows + bs * (bm - 1)) / bm tiles, and at

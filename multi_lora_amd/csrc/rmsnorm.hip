@@ -173,6 +173,7 @@ hipError_t launch_t(const RmsArgs& args, hipStream_t stream) {
   const int rpb = 256 / args.tpr;
   const int64_t blocks = (args.rows + rpb - 1) / rpb;
   if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(blocks));
   switch (args.nc) {
     case 1: return launch_nc<T, 1>(args, grid, stream);

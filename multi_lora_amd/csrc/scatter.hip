@@ -85,6 +85,7 @@ hipError_t launch_scatter(const ScatterArgs& args, int64_t max_numel, int elem_b
   const int64_t nblk = (max_numel + kScatterElems - 1) / kScatterElems;
   const int64_t ny = static_cast<int64_t>(args.n_keys) * args.h;
   if (nblk <= 0 || ny <= 0) return hipSuccess;
+  if (!grid_fits(nblk) || ny > 0xffffffffLL) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(ny));
   if (elem_bytes == 2)
     hipLaunchKernelGGL((scatter_kernel<uint16_t>), grid, dim3(256), 0, stream, args);

@@ -704,10 +704,12 @@ hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const Shri
   const int64_t tiles = p.bm == 16 ? static_cast<int64_t>(args.meta.bs) * p.m_tiles
                                    : dense_tiles(args.meta.bs, p.m_tiles, args.rows, p.bm);
   if (tiles <= 0) return hipSuccess;
+  if (!grid_fits(tiles * p.ks)) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * p.ks)), dim3(256), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1 || args.skip_reduce) return e;
   const int64_t r_tiles = dense_tiles(args.meta.bs, p.m_tiles * (p.bm / kReduceRows), args.rows, kReduceRows);
+  if (!grid_fits(r_tiles)) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(r_tiles)), dim3(256), 0, stream, args);
   return hipGetLastError();
 }

@@ -73,6 +73,15 @@ def test_invalid_arguments_are_rejected_before_launch():
     # mid row too narrow for the slices
     rc = lib.mlora_expand(None, 4, 4, sl, 1, 8, None, 16, ctypes.byref(fake), _ffi.MLORA_BF16, None)
     assert rc < 0 and b"mid row stride" in lib.mlora_last_error()
+    # slice columns past the output row stride (its last row would run off the row)
+    wide = _ffi.SliceArray()
+    wide[0] = _ffi.Slice(1 << 20, 8 * 64, 64, 2 << 20, 16 * 8, 8, 16, 8)
+    rc = lib.mlora_expand(4096, 8, 4, wide, 1, 8, 8192, 16, ctypes.byref(fake), _ffi.MLORA_BF16, None)
+    assert rc < 0 and b"exceed the output row stride" in lib.mlora_last_error()
+    ws = 3 << 20
+    rc = lib.mlora_apply_grouped(4096, 64, 4, 64, wide, 1, 8, 8192, 16, ctypes.byref(fake), _ffi.MLORA_BF16,
+                                 ws, 1 << 20, 2, 3, None)
+    assert rc < 0 and b"exceed the output row stride" in lib.mlora_last_error()
     # unsupported rank width with several slices
     rc = lib.mlora_shrink(4096, 64, 4, 64, sl, 2, 256, 1, 8192, 512, ctypes.byref(fake), _ffi.MLORA_BF16, None, 0, None)
     assert rc < 0

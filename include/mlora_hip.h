@@ -73,7 +73,8 @@ typedef struct mlora_seg_meta {
 /* One LoRA slice of a (possibly fused) projection.
  *   a: A stack [num_slots, r_max, in_dim]   (a_slot_stride, a_row_stride)
  *   b: B stack [num_slots, out_dim, r_max]  (b_slot_stride, b_row_stride)
- *   out_col: first column of this slice in the output rows.
+ *   out_col: first column of this slice in the output rows;
+ *            out_col + out_dim must not exceed the output row stride.
  * The pool layout of multi_lora/pool.py:146-155 is exactly this. */
 typedef struct mlora_slice {
   const void* a;

@@ -138,6 +138,20 @@ __device__ __forceinline__ float load_scaling(const void* p, int idx, int dtype)
   return static_cast<const float*>(p)[idx];
 }
 
+// load_scaling for a wave-uniform index, as a scalar load: a 16-bit value is
+// taken from the 4-byte aligned word that holds it (that word lies in the
+// aligned 4-byte window of a valid element, so it never crosses a page), so
+// waiting for it waits for the scalar queue only, not for vector loads the
+// wave has in flight.
+__device__ __forceinline__ float load_scaling_uniform(const void* p, int idx, int dtype) {
+  if (dtype != MLORA_BF16 && dtype != MLORA_F16) return static_cast<const float*>(p)[idx];
+  const char* v = static_cast<const char*>(p) + 2 * static_cast<int64_t>(idx);
+  const int mis = static_cast<int>(reinterpret_cast<uintptr_t>(v) & 3);
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(v - mis);
+  const uint16_t h = static_cast<uint16_t>(mis ? (w >> 16) : (w & 0xffffu));
+  return dtype == MLORA_BF16 ? BF16::to_f32(h) : F16::to_f32(h);
+}
+
 // Kernel-side view of the per-step segment table.
 struct SegView {
   const int32_t* indptr;

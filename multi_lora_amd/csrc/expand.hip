@@ -89,23 +89,7 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
   const int out_dim = a.slices[s].out_dim;
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
 
-  // Output tile -> LDS.  Instructions whose rows all lie past the segment
-  // are skipped (those LDS rows are never stored); within one, a row past
-  // the segment reads its last row and chunks past out_dim read the tile's
-  // first chunk (both discarded at the store).
-  const int rows_here = min(BM, end - row0);
-#pragma unroll
-  for (int i = 0; i < IPW; ++i) {
-    const int ins = wave * IPW + i;
-    if (ins * RPI >= rows_here) break;
-    const int r = ins * RPI + lane / CPR;
-    const int q = (lane % CPR) ^ (r & 15);
-    const int n = n0 + q * VEC < out_dim ? n0 + q * VEC : n0;
-    const raw* src = out + static_cast<int64_t>(min(row0 + r, end - 1)) * a.out_stride + n;
-    __builtin_amdgcn_global_load_lds((gvoid_t*)src, (lvoid_t*)(tile + ins * 64 * 16), 16, 0, 0);
-  }
-  const float scale = load_scaling(a.meta.scalings, slot, a.meta.scal_dtype);
-
+  const float scale = load_scaling_uniform(a.meta.scalings, slot, a.meta.scal_dtype);
   const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
   const int64_t brs = a.slices[s].b_row_stride;
   const raw* brow[4];
@@ -118,12 +102,50 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
     mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
                static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
 
+  // The first K-step's mid and B fragments go out before the output tile,
+  // unmasked (masked at the MFMA): loads complete in issue order, so waiting
+  // for them leaves the tile's loads in flight.
+  u32x4 yv0[TB], bv0[4];
+  {
+    const int kk = g * VEC;
+    const int off = kk < rank ? kk : 0;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) yv0[tb] = ld_chunk(mrow[tb] + off);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) bv0[nb] = ld_chunk(brow[nb] + off);
+  }
+
+  // Output tile -> LDS, every instruction issued (a fixed count keeps the
+  // wait below exact): a row past the segment reads the segment's last row
+  // and chunks past out_dim read the tile's first chunk, both discarded at
+  // the store.
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int ins = wave * IPW + i;
+    const int r = ins * RPI + lane / CPR;
+    const int q = (lane % CPR) ^ (r & 15);
+    const int n = n0 + q * VEC < out_dim ? n0 + q * VEC : n0;
+    const raw* src = out + static_cast<int64_t>(min(row0 + r, end - 1)) * a.out_stride + n;
+    __builtin_amdgcn_global_load_lds((gvoid_t*)src, (lvoid_t*)(tile + ins * 64 * 16), 16, 0, 0);
+  }
+  // The fragments have landed; the scheduling barrier keeps their MFMAs
+  // (and the wait) below the tile's loads.
+  wait_vmcnt<IPW>();
+  __builtin_amdgcn_sched_barrier(0);
+
   f32x4 acc[4][TB];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < rank; k0 += KSTEP) {
+  {
+    const u32x4 m = keep_mask<T>(rank - g * VEC);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = T::mma(acc[nb][tb], bv0[nb] & m, yv0[tb] & m);
+  }
+  for (int k0 = KSTEP; k0 < rank; k0 += KSTEP) {
     const int kk = k0 + g * VEC;
     const int valid = rank - kk;
     u32x4 yv[TB];

@@ -135,20 +135,6 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
   return (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
 }
 
-// An empty asm that takes the registers of `r` in and out: instructions
-// that use them cannot move above it, and neither can the wait for their
-// loads.  It costs no instruction.
-template <class V, int A>
-__device__ __forceinline__ void fence_regs(V (&r)[A]) {
-#pragma unroll
-  for (int i = 0; i < A; ++i) asm volatile("" : "+v"(r[i]));
-}
-template <class V, int A, int B>
-__device__ __forceinline__ void fence_regs(V (&r)[A][B]) {
-#pragma unroll
-  for (int i = 0; i < A; ++i) fence_regs(r[i]);
-}
-
 // Linked-schedule workspace: [error word | pad to 256 B][tagged sums
 // [kc][rows][n_slices * r_max]].
 struct LinkedView {

@@ -73,6 +73,30 @@ __device__ __forceinline__ void store_row_chunk(typename T::raw_t* p, u32x4 v, i
   }
 }
 
+// An empty asm that takes the registers of `r` in and out: instructions
+// that use them cannot move above it, and neither can the wait for their
+// loads.  It costs no instruction.
+template <class V, int A>
+__device__ __forceinline__ void fence_regs(V (&r)[A]) {
+#pragma unroll
+  for (int i = 0; i < A; ++i) asm volatile("" : "+v"(r[i]));
+}
+template <class V, int A, int B>
+__device__ __forceinline__ void fence_regs(V (&r)[A][B]) {
+#pragma unroll
+  for (int i = 0; i < A; ++i) fence_regs(r[i]);
+}
+
+// s_waitcnt with vmcnt <= N and the other counters unconstrained (gfx9
+// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+// Vector memory loads, direct-to-LDS ones included, complete in issue order,
+// so this waits for every load but the N most recent.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Workgroup barrier that orders LDS accesses only: the fences are scoped to
 // the local address space, so the wait before s_barrier is lgkmcnt(0) and
 // global loads and stores still in flight stay in flight.  __syncthreads()

@@ -464,14 +464,6 @@ constexpr int kDmaStages = 3;
 template <int CPR>
 __device__ __forceinline__ int dma_swz(int r) { return (r / (16 / CPR)) & (CPR - 1); }
 
-// s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9
-// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
 

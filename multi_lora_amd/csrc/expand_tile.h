@@ -59,7 +59,7 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
   while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
   const int n0 = (nt_g - a.tile_base[s]) * BN;
   const int out_dim = a.slices[s].out_dim;
-  const float scale = load_scaling(a.meta.scalings, slot, a.meta.scal_dtype);
+  const float scale = load_scaling_uniform(a.meta.scalings, slot, a.meta.scal_dtype);
 
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
 

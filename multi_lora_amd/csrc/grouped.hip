@@ -340,7 +340,7 @@ __device__ void expand_item(const GroupedArgs& a, int slot, int nt_g, ExpandLds<
 
   const SegEntry first = load_seg(a.meta, tid);
   const int rank = slot_rank(a, slot);
-  const float scale = (slot < a.meta.num_slots) ? load_scaling(a.meta.scalings, slot, a.meta.scal_dtype) : 0.f;
+  const float scale = (slot < a.meta.num_slots) ? load_scaling_uniform(a.meta.scalings, slot, a.meta.scal_dtype) : 0.f;
   if (rank == 0) return;
   int s = 0;
   while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;

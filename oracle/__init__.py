@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
 the ``cpu_baseline`` leg of ``bench.py`` may import this package, and only
-as the checker (or the timed CPU baseline); the product package
+to check results against (or as the timed CPU baseline); the product package
 ``multi_lora_amd`` never imports it and has no CPU path.
 
 Modules and the reference code each one restates:

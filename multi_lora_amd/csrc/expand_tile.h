@@ -63,18 +63,6 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
 
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
 
-  // Prefetch this thread's share of the output tile (rows clamped to the
-  // segment; chunks past out_dim read the row start and are masked).
-  u32x4 ov[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int c = tid + i * 256;
-    const int row = c / CPR;
-    const int n = n0 + (c - row * CPR) * VEC;
-    const int t = min(row0 + row, end - 1);
-    ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
-  }
-
   const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
   const int64_t brs = a.slices[s].b_row_stride;
   const raw* brow[4];
@@ -86,6 +74,33 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
   for (int tb = 0; tb < TB; ++tb)
     mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
                static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
+
+  // Aligned y from mid: the first K-step's mid and B fragments are requested
+  // before the output tile, unmasked (masked at the MFMA).  Loads complete in
+  // issue order, so the first MFMAs wait for them only, with the tile's loads
+  // still in flight.
+  constexpr bool kEarly = AL && !FUSED;
+  u32x4 yv0[TB], bv0[4];
+  if constexpr (kEarly) {
+    const int kk = g * VEC;
+    const int off = kk < rank ? kk : 0;
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) yv0[tb] = ld_chunk(mrow[tb] + off);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) bv0[nb] = ld_chunk(brow[nb] + off);
+  }
+
+  // Prefetch this thread's share of the output tile (rows clamped to the
+  // segment; chunks past out_dim read the row start and are masked).
+  u32x4 ov[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / CPR;
+    const int n = n0 + (c - row * CPR) * VEC;
+    const int t = min(row0 + row, end - 1);
+    ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
+  }
 
   f32x4 acc[4][TB];
 #pragma unroll
@@ -124,7 +139,19 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
     }
   }
 
-  for (int k0 = 0; k0 < rank; k0 += KSTEP) {
+  int k_first = 0;
+  if constexpr (kEarly) {
+    // The scheduling barrier keeps these MFMAs (and their wait) below the
+    // output tile's loads.
+    __builtin_amdgcn_sched_barrier(0);
+    const u32x4 m = keep_mask<T>(rank - g * VEC);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) acc[nb][tb] = T::mma(acc[nb][tb], bv0[nb] & m, yv0[tb] & m);
+    k_first = KSTEP;
+  }
+  for (int k0 = k_first; k0 < rank; k0 += KSTEP) {
     const int kk = k0 + g * VEC;
     const int valid = rank - kk;
     u32x4 yv[TB];

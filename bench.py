@@ -31,6 +31,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "seg-LoRA shrink+expand µs & HBM GB/s, 8B shapes, 128 mixed-adapter decode"
+HEADLINE_WORKLOAD = "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -46,9 +47,13 @@ def parse():
     ap.add_argument("--workload", choices=("decode_q",) + tuple(OTHER_WORKLOADS), default="decode_q",
                     help="decode_q is the headline; the others print a line of the same form for their shape")
     ap.add_argument("--profile-traffic", action="store_true",
-                    help="launch only the headline kernel and a copy kernel of known size, for rocprofv3 --pmc runs")
+                    help="launch only the planned decode kernel of --workload (decode_q, decode_q_resident or "
+                         "decode_qkv) and a copy kernel of known size, for rocprofv3 --pmc runs")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn rocprofv3 FETCH_SIZE / WRITE_SIZE runs of --profile-traffic into the traffic file")
+    ap.add_argument("--regions", type=int, default=0,
+                    help="timed regions of exactly --steps steps each (default: enough for ~2000 steps, 5..101); "
+                         "the step time is their median")
     return ap.parse_args()
 
 
@@ -57,6 +62,8 @@ OTHER_WORKLOADS = {
     "prefill_down": "prefill MLP down 14336->4096, 8 segments of U[64,1024] tokens, ranks {16,32,64}, r_max 64",
     "decode_qkv": "RMSNorm then q|k|v 4096->[4096,1024,1024], 256 one-token segments, 256-slot pool, "
                   "128 rank-32 adapters",
+    "decode_q_resident": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool holding 64 resident "
+                         "rank-16 adapters, tokens drawn over 32 of them",
     "pool_upload": "pool upload scatter, Llama-3-8B 32 layers x 7 projections (224 keys), rank 16, "
                    "4 staged adapters (84 MB each) into an 8-slot pool",
     "c5_step": "Llama-3-8B 32-layer LoRA step: 7 projections per layer at rank 16 (q|k|v and gate|up fused), "
@@ -347,10 +354,8 @@ def bench_other(args) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     name = args.workload
-    if name.startswith("prefill"):
-        host = synthetic.prefill_mlp(device="cpu", part=name.split("_", 1)[1])
-    else:
-        host = synthetic.decode_qkv(device="cpu")
+    host = grouped_host(name) if name in GROUPED_WORKLOADS else synthetic.prefill_mlp(
+        device="cpu", part=name.split("_", 1)[1])
     meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
     e = host.x.element_size()
     rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + 2 * host.base.numel()) * e
@@ -386,13 +391,7 @@ def bench_other(args) -> int:
 
         def lora(i):
             _, a, b, out = reps[i % n_rep]
-            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=0,
-                                 linked_workspace=be.linked_workspace)
-
-        def lora_linked(i):
-            _, a, b, out = reps[i % n_rep]
-            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=1,
-                                 linked_workspace=be.linked_workspace)
+            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.linked_workspace, mode=0)
 
         def step(i):
             x, a, b, out = reps[i % n_rep]
@@ -401,7 +400,7 @@ def bench_other(args) -> int:
 
         def lora_two(i):
             _, a, b, out = reps[i % n_rep]
-            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.workspace, mode=2)
+            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.linked_workspace, mode=2)
 
         resid = [torch.randn_like(r[0]) for r in reps]
         ys = [torch.empty_like(r[0]) for r in reps]
@@ -422,13 +421,28 @@ def bench_other(args) -> int:
 
         total_bytes = lora_bytes + norm_bytes
         add_bytes = 4 * S * in_dim * e + in_dim * e
-        parts = {"rmsnorm": (norm, norm_bytes), "grouped (3 slices, the library's schedule)": (lora, lora_bytes),
-                 "grouped linked (schedule comparison)": (lora_linked, lora_bytes),
-                 "grouped two launches, mode 2 on its own workspace (schedule comparison)": (lora_two, lora_bytes),
+        parts = {"rmsnorm": (norm, norm_bytes), "planned decode (3 slices, one launch)": (lora, lora_bytes),
+                 "planned decode, two launches (schedule comparison)": (lora_two, lora_bytes),
                  "add_rmsnorm fused (schedule comparison)": (add_norm, add_bytes),
                  "add then rmsnorm, unfused (schedule comparison)": (add_then_norm, add_bytes)}
-        path = ("rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-grouped; the library picks the "
-                "linked launch or two launches by work items per CU: two launches at this shape)")
+        path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-planned decode, one launch)"
+    elif name in GROUPED_WORKLOADS:
+        def lora(i):
+            x, a, b, out = reps[i % n_rep]
+            assert apply_grouped(x, a, b, meta, out, cols, be.linked_workspace, mode=0)
+
+        def lora_two(i):
+            x, a, b, out = reps[i % n_rep]
+            assert apply_grouped(x, a, b, meta, out, cols, be.linked_workspace, mode=2)
+
+        def step(i):
+            x, a, b, out = reps[i % n_rep]
+            be.apply_lora_multi(x, a, b, out, cols)
+
+        total_bytes = lora_bytes
+        parts = {"planned decode (one launch)": (lora, lora_bytes),
+                 "planned decode, two launches (schedule comparison)": (lora_two, lora_bytes)}
+        path = "HipLoRABackend.apply_lora (slot-planned decode, one launch)"
     else:
         mids = [torch.empty(S, n * r_max, dtype=host.x.dtype, device=dev) for _ in range(n_rep)]
         ws = Workspace()
@@ -461,6 +475,9 @@ def bench_other(args) -> int:
     for k, (fn, nbytes) in parts.items():
         ms = time_graph(torch, capture(torch, fn, per_graph), calls, per_graph, stream)
         kernels[k] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9}
+    fb, pe = be.linked_workspace.counters()
+    if pe:
+        raise RuntimeError(f"{pe} plan errors; timings are void")
     dom = max((k for k in kernels if "schedule" not in k), key=lambda k: kernels[k]["us"])
     fl = synthetic.flops(host)
     result = {
@@ -481,11 +498,12 @@ def bench_other(args) -> int:
         "data": "synthetic",
         "config": {"workload": OTHER_WORKLOADS[name], "tokens": S, "segments": len(host.seg_lens),
                    "algorithmic_bytes_per_step": total_bytes, "flops_per_step": fl, "replicas": n_rep,
-                   "timing": "HIP graph replay, HIP events on the launch stream", "path": path},
+                   "timing": "HIP graph replay, HIP events on the launch stream", "path": path,
+                   "handoff_fallback_chunks": fb},
         "kernels": kernels,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(kernels[dom]["GB/s"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kernels[dom]["GB/s"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": traffic_bytes(name) if name in GROUPED_WORKLOADS else None},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_other(name, host, total_bytes, args.cpu_seconds)
@@ -538,25 +556,49 @@ def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> di
 # --profile-traffic: the copy kernel used to calibrate the counters moves
 # COPY_ELEMS bf16 values (read once, written once).
 COPY_ELEMS = 32 << 20
-HEADLINE_KERNEL = "grouped_linked"
-TRAFFIC_FILE = ROOT / "profiles" / f"{HEADLINE_KERNEL}_decode_q_traffic.json"
+PLANNED_KERNEL = "planned_kernel"
+GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_qkv")
 
 
-def profile_traffic(launches: int = 64, copies: int = 16) -> int:
-    """Headline kernel over rotating replicas, then a plain copy kernel."""
+def grouped_host(name: str):
+    from multi_lora_amd import synthetic
+
+    if name == "decode_q":
+        return synthetic.decode_q(device="cpu")
+    if name == "decode_q_resident":
+        return synthetic.decode_q(device="cpu", resident=64)
+    return synthetic.decode_qkv(device="cpu")
+
+
+def traffic_file(name: str) -> Path:
+    return ROOT / "profiles" / f"planned_decode_{name}_traffic.json"
+
+
+def traffic_bytes(name: str):
+    f = traffic_file(name)
+    return json.loads(f.read_text()).get("hbm_bytes_per_launch") if f.exists() else None
+
+
+def profile_traffic(name: str, launches: int = 64, copies: int = 16) -> int:
+    """The planned decode kernel of a workload over rotating replicas (its
+    input already normalised for decode_qkv), then a plain copy kernel."""
     import torch
 
     from multi_lora_amd import synthetic
     from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, apply_grouped
 
     dev = torch.device("cuda", 0)
-    host = synthetic.decode_q(device="cpu")
+    host = grouped_host(name)
     meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
-    reps = [(host.x.to(dev), host.a_stacks[0].to(dev), host.b_stacks[0].to(dev), host.base.to(dev)) for _ in range(32)]
+    e = host.x.element_size()
+    rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + host.base.numel()) * e
+    n_rep = max(2, -(-600_000_000 // rep_bytes))
+    reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
+             host.base.to(dev)) for _ in range(n_rep)]
     lws = LinkedWorkspace()
     for i in range(launches):
         x, a, b, out = reps[i % len(reps)]
-        assert apply_grouped(x, [a], [b], meta, out, [0], mode=1, linked_workspace=lws)
+        assert apply_grouped(x, a, b, meta, out, host.col_offsets, lws, mode=1)
     torch.cuda.synchronize()
     src = torch.randn(COPY_ELEMS, device=dev).bfloat16()
     dst = torch.empty_like(src)
@@ -564,12 +606,14 @@ def profile_traffic(launches: int = 64, copies: int = 16) -> int:
     for _ in range(copies):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    print(json.dumps({"headline_launches": launches, "copy_launches": copies, "copy_bytes_each_way": COPY_ELEMS * 2}))
+    fb, pe = lws.counters()
+    print(json.dumps({"workload": name, "launches": launches, "copy_launches": copies,
+                      "copy_bytes_each_way": COPY_ELEMS * 2, "fallback_chunks": fb, "plan_errors": pe}))
     return 0
 
 
 def _pmc_means(directory: str, counter: str) -> dict:
-    """Mean per-dispatch value of `counter` for the headline and copy kernels."""
+    """Mean per-dispatch value of `counter` for the planned decode kernel and the copy kernel."""
     import csv
 
     files = sorted(Path(directory).rglob("*counter_collection.csv"))
@@ -583,7 +627,7 @@ def _pmc_means(directory: str, counter: str) -> dict:
                     continue
                 name = row.get("Kernel_Name", "")
                 v = float(row["Counter_Value"])
-                if HEADLINE_KERNEL in name:
+                if PLANNED_KERNEL in name:
                     vals["headline"].append(v)
                 elif "neg" in name:
                     vals["copy"].append(v)
@@ -592,7 +636,9 @@ def _pmc_means(directory: str, counter: str) -> dict:
     return {k: sum(v) / len(v) for k, v in vals.items()} | {"dispatches": {k: len(v) for k, v in vals.items()}}
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+def summarize_pmc(name: str, fetch_dir: str, write_dir: str) -> int:
+    from multi_lora_amd import synthetic
+
     fetch = _pmc_means(fetch_dir, "FETCH_SIZE")
     write = _pmc_means(write_dir, "WRITE_SIZE")
     copy_kib = COPY_ELEMS * 2 / 1024
@@ -600,12 +646,15 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
     w_scale = copy_kib / write["copy"]
     fetch_b = fetch["headline"] * f_scale * 1024
     write_b = write["headline"] * w_scale * 1024
+    algo = synthetic.algorithmic_bytes(grouped_host(name))
     out = {
-        "kernel": HEADLINE_KERNEL,
-        "workload": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters",
+        "kernel": f"{PLANNED_KERNEL} (single launch)",
+        "workload": OTHER_WORKLOADS.get(name, HEADLINE_WORKLOAD),
+        "algorithmic_bytes_per_launch": algo,
         "hbm_bytes_per_launch": round(fetch_b + write_b),
         "fetch_bytes_per_launch": round(fetch_b),
         "write_bytes_per_launch": round(write_b),
+        "traffic_over_algorithmic": round((fetch_b + write_b) / algo, 4),
         "raw_kib_per_dispatch": {"FETCH_SIZE": fetch["headline"], "WRITE_SIZE": write["headline"]},
         "copy_calibration": {
             "bytes_each_way": COPY_ELEMS * 2,
@@ -614,12 +663,14 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
         },
         "dispatches": {"FETCH_SIZE": fetch["dispatches"], "WRITE_SIZE": write["dispatches"]},
         "commands": [
-            "timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d <FETCH_DIR> -f csv -- python3 bench.py --profile-traffic",
-            "timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d <WRITE_DIR> -f csv -- python3 bench.py --profile-traffic",
-            "python3 bench.py --summarize-pmc <FETCH_DIR> <WRITE_DIR>",
+            f"timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d <FETCH_DIR> -f csv -- python3 bench.py "
+            f"--profile-traffic --workload {name}",
+            f"timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d <WRITE_DIR> -f csv -- python3 bench.py "
+            f"--profile-traffic --workload {name}",
+            f"python3 bench.py --workload {name} --summarize-pmc <FETCH_DIR> <WRITE_DIR>",
         ],
     }
-    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    traffic_file(name).write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
     return 0
 
@@ -648,14 +699,14 @@ def cpu_model() -> str:
 def main() -> int:
     args = parse()
     if args.summarize_pmc:
-        return summarize_pmc(*args.summarize_pmc)
+        return summarize_pmc(args.workload, *args.summarize_pmc)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding of this path is design-only", file=sys.stderr)
         return 2
 
     if args.profile_traffic:
-        return profile_traffic()
+        return profile_traffic(args.workload)
     if args.workload == "pool_upload":
         return bench_pool_upload(args)
     if args.workload == "c5_step":
@@ -687,47 +738,61 @@ def main() -> int:
         if mode is None:
             be.apply_lora(x, a, b, out)
         else:
-            launched = apply_grouped(x, [a], [b], meta, out, [0], be.workspace, phases=phases, mode=mode,
-                                     linked_workspace=be.linked_workspace)
-            assert launched, "decode workload is expected to take the slot-grouped path"
+            launched = apply_grouped(x, [a], [b], meta, out, [0], be.linked_workspace, phases=phases, mode=mode)
+            assert launched, "decode workload is expected to take the slot-planned path"
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
 
     # The host enqueues a call in ~10-20 us, slower than the kernels run, so
-    # timing is done on HIP graphs: one graph holds a pass over every replica
-    # and is replayed back to back, keeping the GPU busy.
-    def capture(phases=3, mode=None):
+    # steps are timed as HIP graph replays: a graph of one pass over the
+    # replicas, and one of the remaining steps, make up exactly `steps` steps.
+    def capture(n, phases=3, mode=None):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for i in range(len(reps)):
+            for i in range(n):
                 step(i, phases, mode)
         torch.cuda.synchronize()
         return g
 
-    def time_graph(g, calls):
-        replays = max(1, calls // len(reps))
-        g.replay()
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record(stream)
-        for _ in range(replays):
-            g.replay()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1) / (replays * len(reps)), replays * len(reps)
+    def region_timer(k, phases=3, mode=None):
+        """Times regions of exactly k steps (ms per step of each region)."""
+        full, rem = divmod(k, len(reps))
+        g_full = capture(len(reps), phases, mode) if full else None
+        g_rem = capture(rem, phases, mode) if rem else None
 
-    g_step = capture()
-    ms_per_step, timed_steps = time_graph(g_step, args.steps)
-    # Per-kernel durations, each from a graph holding only that launch.  The
-    # backend's path for this shape is the single linked launch; the two-launch
+        def run():
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for _ in range(full):
+                g_full.replay()
+            if g_rem is not None:
+                g_rem.replay()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            return t0.elapsed_time(t1) / k
+
+        run()  # first replay of fresh graphs, untimed
+        return run
+
+    def median_ms(k, regions, phases=3, mode=None):
+        run = region_timer(k, phases, mode)
+        times = sorted(run() for _ in range(regions))
+        return times[len(times) // 2]
+
+    regions = args.regions or min(101, max(5, -(-2000 // args.steps)))
+    ms_per_step = median_ms(args.steps, regions)
+    timed_steps = args.steps
+    # The backend's step is one launch of the planned kernel; the two-launch
     # schedule of the same work items is timed for comparison.
-    linked_ms, _ = time_graph(capture(3, mode=1), args.kernel_steps)
-    shrink_ms, _ = time_graph(capture(1, mode=2), args.kernel_steps)
-    expand_ms, _ = time_graph(capture(2, mode=2), args.kernel_steps)
-    if be.linked_workspace.error_word() != 0:
-        raise RuntimeError("a wait between linked work items timed out; timings are void")
+    kreg = max(1, -(-args.kernel_steps // len(reps)))
+    shrink_ms = median_ms(len(reps), kreg, 1, mode=2)
+    expand_ms = median_ms(len(reps), kreg, 2, mode=2)
+    fb, pe = be.linked_workspace.counters()
+    if pe:
+        raise RuntimeError(f"{pe} plan errors; timings are void")
 
     e = 2
     used = sorted({s for s in host.seg_slots if host.slot_ranks[s] > 0})
@@ -742,16 +807,14 @@ def main() -> int:
         return {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9}
 
     kernels = {
-        "grouped_linked": entry(linked_ms, total_bytes),
-        "grouped_shrink (two-launch schedule)": entry(shrink_ms, shrink_bytes),
-        "grouped_expand (two-launch schedule)": entry(expand_ms, expand_bytes),
+        "planned_decode (one launch)": entry(ms_per_step, total_bytes),
+        "planned_decode shrink half (two-launch schedule)": entry(shrink_ms, shrink_bytes),
+        "planned_decode expand half (two-launch schedule)": entry(expand_ms, expand_bytes),
         "two-launch schedule total": entry(shrink_ms + expand_ms, total_bytes),
     }
-    dom_name = "grouped_linked"
+    dom_name = "planned_decode (one launch)"
     dom = kernels[dom_name]
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    traffic = traffic_bytes("decode_q")
 
     result = {
         "metric": METRIC,
@@ -769,13 +832,15 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters",
+            "workload": HEADLINE_WORKLOAD,
             "tokens": host.tokens,
             "distinct_slots": len(used),
             "algorithmic_bytes_per_step": total_bytes,
             "replicas": args.replicas,
-            "timing": "HIP graph replay, HIP events on the launch stream",
-            "path": "slot-grouped shrink + expand, one linked launch",
+            "timing": (f"median over {regions} regions of exactly {args.steps} steps, each a HIP graph replay "
+                       f"timed with HIP events on the launch stream"),
+            "path": "slot-planned shrink + expand, one launch (HipLoRABackend.apply_lora)",
+            "handoff_fallback_chunks": fb,
         },
         "kernels": kernels,
         "roofline": {

@@ -68,7 +68,40 @@ typedef struct mlora_seg_meta {
   int32_t long_segs;
   int32_t long_rows;
   int32_t short_slots;
+  /* Optional plan of the table for mlora_apply_grouped (device pointer,
+   * layout below), NULL when none; plan_cap: entries it holds;
+   * plan_entries: its entry count if the host knows it, else -1 (it only
+   * sizes the grid). */
+  const int32_t* plan;
+  int32_t plan_cap;
+  int32_t plan_entries;
 } mlora_seg_meta;
+
+/* Plan of a segment table (no counterpart in the reference: it is the
+ * slot-grouped gather list of the table, made once per table and used by
+ * every mlora_apply_grouped call on it).  int32 words:
+ *   header [MLORA_PLAN_HEADER_WORDS]: [0] entries, [1] rows planned,
+ *     [2] entry capacity, rest 0;
+ *   entry e at MLORA_PLAN_HEADER_WORDS + e * MLORA_PLAN_ENTRY_WORDS:
+ *     [0] slot, [1] its rank (lora_ranks[slot]), [2] its scaling as fp32
+ *     bits, [3] rows n (1..MLORA_PLAN_ROWS), [4] position of the entry's
+ *     first row among all planned rows, [5..7] 0,
+ *     [MLORA_PLAN_ROW_WORD + i] row i of the entry (i < n; words i >= n
+ *     repeat row 0), remaining words 0.
+ * Entries take the slots in ascending order, slots outside [0, num_slots)
+ * and rank-0 slots excluded; a slot's rows (segment bounds clamped to the
+ * call's rows), in row order, fill consecutive entries of MLORA_PLAN_ROWS,
+ * and positions count the rows of all earlier entries. */
+#define MLORA_PLAN_HEADER_WORDS 16
+#define MLORA_PLAN_ENTRY_WORDS 32
+#define MLORA_PLAN_ROWS 16
+#define MLORA_PLAN_ROW_WORD 8
+
+/* Header words (int32) at the start of an mlora_apply_grouped workspace. */
+#define MLORA_WS_FALLBACKS 0   /* K chunks a waiting work item computed itself (counter) */
+#define MLORA_WS_WAIT_TICKS 1  /* wait limit in 10 ns ticks: 0 = library default; < 0 = no wait at all:
+                                  every waiting work item computes each K chunk itself (a test mode) */
+#define MLORA_WS_PLAN_ERRORS 2 /* plan entries the call could not take (counter; should stay 0) */
 
 /* One LoRA slice of a (possibly fused) projection.
  *   a: A stack [num_slots, r_max, in_dim]   (a_slot_stride, a_row_stride)
@@ -152,37 +185,35 @@ int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, 
                          int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
                          size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace mlora_apply_grouped needs for this shape and `mode`;
- * 0 when the shape is not eligible (or mode is not 0..2).  mode 2 (two
- * launches): fp32 sums of each 256-wide K chunk for every row and slice.
- * mode 1: a 256-byte header (error word) and the same sums as 64-bit tagged
- * words.  mode 0: mode 1's layout, then (at the next 256-byte boundary) mode
- * 2's, for the calls it runs as two launches.  `num_slots` is accepted for
- * layouts that depend on it; none does now. */
+/* Bytes of workspace mlora_apply_grouped needs for this shape (any mode; 0
+ * when the shape is not eligible or mode is not 0..2): a 256-byte header
+ * (MLORA_WS_* words), per-entry chunk flags, the fp32 sums of each 256-wide
+ * K chunk for every row and slice, and room for a plan of num_rows entries
+ * (used when the caller passes none).  `num_slots` is accepted for layouts
+ * that depend on it; none does now. */
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
                                      int32_t num_slots, int32_t dtype, int32_t mode);
 
 /* Slot-grouped shrink + expand for decode-shaped batches:
  *   out[t, out_col_s + n] += round(scaling * round(x[t] . A_s[slot,:rank]) . B_s[slot, n, :rank])
  * with the same roundings as mlora_shrink followed by mlora_expand; no `mid`
- * is materialised.  Work items are indexed by (slot, chunk) and gather the
- * rows of their slot from the segment table, so each referenced adapter's A
- * and B are read from HBM once per call however many rows use it.
- * `mode`: 2 = two launches (shrink items, then expand items; the workspace
- * carries fp32 K-chunk sums and may be any scratch);
- * 1 = single launch (expand items wait, with a bounded spin, on the sums
- * the shrink items of the same launch publish, each tagged with the launch's
- * dispatch id on its hardware queue);
- * 0 = the library's choice per call: the single launch while all work items
- * fit on the chip at once (num_slots * items per slot <= 16 per CU), else
- * two launches whose fp32 sums go to the region after the tagged words, so
- * neither schedule ever reads the other's sums.
- * The workspace of modes 0 and 1 must be zero-filled before its first use,
- * passed to nothing but calls of the same mode afterwards, and used from one
- * stream only (give each stream its own); it is never cleared between calls.
- * Its first int32 is a sticky error word that becomes non-zero if a wait ever
- * timed out (results of that launch are then unreliable).  Calls sharing a
- * workspace must not overlap.
+ * is materialised.  Work follows the table's plan (meta->plan, or one built
+ * on the device into the workspace first when it is NULL; pools of up to
+ * 2048 slots then): each entry's A and B are read once per call for all of
+ * its rows, and slots no row uses are never read.
+ * `mode`: 0 = the library's choice (the single launch while the work items
+ * fit on the chip about at once, at most 16 a CU, else two launches); 1 = single launch
+ * (work items of one entry run on one XCD and hand the K-chunk sums over
+ * through its L2; a work item that does not receive a chunk in time, or
+ * from its own XCD, computes it itself, so results never depend on timing
+ * or placement); 2 = two launches (shrink items, then expand items).  All
+ * modes give bit-identical results.
+ * The workspace must be zero-filled before its first use and is never
+ * cleared afterwards (sums are tagged with the launch's dispatch id on its
+ * hardware queue); calls that overlap in time need separate workspaces, and
+ * one workspace serves one stream.  Its MLORA_WS_* header words count chunks
+ * computed after a wait gave up and plan errors, and may set the wait
+ * limit.
  * `phases` (two-launch mode only; must be 3 otherwise): 1 = shrink half
  * (leaves its sums in the workspace), 2 = expand half (consumes them), 3 = both.
  * Requirements (else -2 and nothing launched): bf16 or fp16; r_max <= 64 and
@@ -194,6 +225,17 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
                         const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
                         int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
                         size_t workspace_bytes, int32_t mode, int32_t phases, void* stream);
+
+/* Bytes of a plan with room for `entries_cap` entries. */
+size_t mlora_plan_bytes(int32_t entries_cap);
+
+/* Build the plan of meta's table for calls of num_rows rows into `plan`
+ * (device memory of mlora_plan_bytes(plan_cap) bytes), on the device: the
+ * same words the layout above defines.  Entries past plan_cap are not
+ * written (the header still counts them).  Pools of up to 2048 slots.
+ * No counterpart in the reference; the slot-grouped gather indices of its
+ * batch metadata (multi_lora/batch_info.py:128-179) made on the device. */
+int mlora_build_plan(const mlora_seg_meta* meta, int32_t num_rows, int32_t* plan, int32_t plan_cap, void* stream);
 
 /* Fused RMSNorm: y[row] = round(x[row] * rsqrt(mean(x[row]^2) + eps) * w) in
  * fp32, one rounding.  Row `row` of x starts at

@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MLORA_F32, MLORA_F16, MLORA_BF16 = 0, 1, 2
 MAX_SLICES = 4
@@ -38,7 +38,19 @@ EXPORTS = (
     "mlora_rmsnorm",
     "mlora_pool_scatter",
     "mlora_add_rmsnorm",
+    "mlora_plan_bytes",
+    "mlora_build_plan",
 )
+
+# Plan layout (include/mlora_hip.h: MLORA_PLAN_*) and workspace header words
+# of mlora_apply_grouped (MLORA_WS_*).
+PLAN_HEADER_WORDS = 16
+PLAN_ENTRY_WORDS = 32
+PLAN_ROWS = 16
+PLAN_ROW_WORD = 8
+WS_FALLBACKS = 0
+WS_WAIT_TICKS = 1
+WS_PLAN_ERRORS = 2
 
 
 # Segments of at most this many rows are short in the table summary
@@ -61,6 +73,9 @@ class SegMeta(ctypes.Structure):
         ("long_segs", ctypes.c_int32),
         ("long_rows", ctypes.c_int32),
         ("short_slots", ctypes.c_int32),
+        ("plan", ctypes.c_void_p),
+        ("plan_cap", ctypes.c_int32),
+        ("plan_entries", ctypes.c_int32),
     ]
 
 
@@ -138,6 +153,8 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
     ),
+    "mlora_plan_bytes": (_sz, [_i32]),
+    "mlora_build_plan": (ctypes.c_int, [ctypes.POINTER(SegMeta), _i32, _vp, _i32, _vp]),
 }
 
 

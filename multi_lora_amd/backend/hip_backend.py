@@ -85,8 +85,7 @@ class HipLoRABackend(LoRABackend):
         a_stacks = [a.contiguous() for a in a_stacks]
         b_stacks = [b.contiguous() for b in b_stacks]
         if meta.max_len <= GROUPED_MAX_LEN and apply_grouped(
-            x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace,
-            linked_workspace=self.linked_workspace,
+            x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.linked_workspace,
         ):
             return base_output
         return apply_segments(x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace)

@@ -10,6 +10,11 @@ rules) so callers of the reference can switch without edits:
 * ``group_rows``         run-length merge of adjacent equal names (:70-97).
 * ``write_kernel_input_metadata`` rewrites resident tensors in place when
   they are large enough, so addresses stay fixed across steps (:128-179).
+* ``build_plan``         the slot-grouped row lists of a table (no
+                         counterpart in the reference; it lists, per
+                         referenced slot, the rows that use it, in entries of
+                         16), packed with the table so every call of a step
+                         reuses it.
 """
 
 from __future__ import annotations
@@ -23,6 +28,72 @@ import torch
 # Segments of at most this many rows count as short (decode-like) in the
 # table summary; the library's mixed-batch expand uses the same bound.
 SHORT_SEG_ROWS = 16
+
+# Plan layout (include/mlora_hip.h, MLORA_PLAN_*).
+PLAN_HEADER_WORDS = 16
+PLAN_ENTRY_WORDS = 32
+PLAN_ROWS = 16
+PLAN_ROW_WORD = 8
+
+
+def plan_words(cap: int) -> int:
+    """int32 words of a plan with room for ``cap`` entries."""
+    return PLAN_HEADER_WORDS + cap * PLAN_ENTRY_WORDS
+
+
+def build_plan(indptr, slots, ranks, scal_f32, num_slots: int, rows: int, out: np.ndarray) -> int:
+    """Write the plan of a segment table into ``out`` (int32 words); returns its entry count.
+
+    Entries take the slots in ascending order (slots outside
+    ``[0, num_slots)`` and rank-0 slots excluded); each slot's rows, segment
+    bounds clamped to ``[0, rows)``, in segment order, fill entries of 16:
+    slot, rank, scaling (fp32 bits), row count, position of the first row
+    among all planned rows, then the rows (unused words repeat the first).
+    Entries past the room in ``out`` are left out; the header still counts
+    them.  ``scal_f32``: each slot's scaling as the kernels read it (the
+    pool dtype's value in fp32).
+    """
+    cap = (out.shape[0] - PLAN_HEADER_WORDS) // PLAN_ENTRY_WORDS
+    ip = np.asarray(indptr, dtype=np.int64)
+    w = np.asarray(slots, dtype=np.int64)
+    rk = np.asarray(ranks, dtype=np.int64)[:num_slots]
+    starts = np.clip(ip[:-1], 0, rows)
+    ends = np.clip(ip[1:], 0, rows)
+    inside = (w >= 0) & (w < num_slots)
+    live = inside & (ends > starts)
+    live[inside] &= rk[w[inside]] > 0
+    lens = (ends - starts)[live]
+    seg_slot = w[live]
+    total = int(lens.sum())
+    # Concatenated row ranges of the live segments, in segment order, then
+    # stably grouped by slot.
+    first = np.repeat(starts[live] - (np.cumsum(lens) - lens), lens)
+    tok_rows = first + np.arange(total, dtype=np.int64)
+    rows_sorted = tok_rows[np.argsort(np.repeat(seg_slot, lens), kind="stable")]
+    slot_rows = np.bincount(seg_slot, weights=lens, minlength=num_slots).astype(np.int64)
+    uniq = np.nonzero(slot_rows)[0]
+    counts = slot_rows[uniq]
+    n_ent = (counts + PLAN_ROWS - 1) // PLAN_ROWS
+    n_entries = int(n_ent.sum())
+    out[:PLAN_HEADER_WORDS] = 0
+    out[0], out[1], out[2] = n_entries, total, cap
+    e_take = min(n_entries, cap)
+    if e_take:
+        ent_slot = np.repeat(uniq, n_ent)[:e_take]
+        k = (np.arange(n_entries) - np.repeat(np.cumsum(n_ent) - n_ent, n_ent))[:e_take]
+        pos = np.repeat(np.cumsum(counts) - counts, n_ent)[:e_take] + PLAN_ROWS * k
+        nr = np.minimum(PLAN_ROWS, np.repeat(counts, n_ent)[:e_take] - PLAN_ROWS * k)
+        ent = out[PLAN_HEADER_WORDS:PLAN_HEADER_WORDS + e_take * PLAN_ENTRY_WORDS].reshape(e_take, PLAN_ENTRY_WORDS)
+        ent[:] = 0
+        ent[:, 0] = ent_slot
+        ent[:, 1] = rk[ent_slot]
+        ent[:, 2] = np.asarray(scal_f32, dtype=np.float32)[ent_slot].view(np.int32)
+        ent[:, 3] = nr
+        ent[:, 4] = pos
+        i = np.arange(PLAN_ROWS)
+        idx = pos[:, None] + np.where(i[None, :] < nr[:, None], i[None, :], 0)
+        ent[:, PLAN_ROW_WORD:PLAN_ROW_WORD + PLAN_ROWS] = rows_sorted[idx]
+    return n_entries
 
 
 @dataclass
@@ -54,6 +125,13 @@ class KernelInputMetaData:
     # host mirror (a GPU table made by write_kernel_input_metadata): a
     # rewrite is then one asynchronous copy instead of five.
     packed: Optional["PackedColumns"] = None
+    # The table's plan (build_plan) when the table carries one: an int32
+    # device tensor, its entry capacity and its entry count.  Packed tables
+    # rebuild it on every rewrite; without one, the library builds it on the
+    # device for each grouped call.
+    plan: Optional[torch.Tensor] = None
+    plan_cap: int = 0
+    plan_entries: int = -1
     # Host copies of the segment lengths and slots (set by
     # write_kernel_input_metadata; None when unknown).  They give the
     # library a summary of the table (table_summary) with which a batch
@@ -84,20 +162,24 @@ class KernelInputMetaData:
 
 
 class PackedColumns:
-    """One device buffer holding the five columns, and a pinned host mirror.
+    """One device buffer holding the five columns and the table's plan, and a pinned host mirror.
 
     Layout (each section 64-byte aligned): weight_indices[capacity],
     seg_lens[capacity], seg_indptr[capacity + 1] (int32), lora_ranks[num_slots]
-    (int32), scalings[num_slots] (the pool dtype).  ``write`` fills the
-    mirror and copies it in one transfer on the current stream; before
-    touching the mirror it waits for the previous transfer to have read it.
+    (int32), scalings[num_slots] (the pool dtype), then the plan (int32, room
+    for capacity + min(capacity, num_slots) entries: every table of segments
+    of at most 16 rows fits).  ``write`` fills the mirror, builds the plan in
+    it, and copies everything up to the plan's last entry in one transfer on
+    the current stream; before touching the mirror it waits for the previous
+    transfer to have read it.
     """
 
     def __init__(self, capacity: int, num_slots: int, device: torch.device, dtype: torch.dtype) -> None:
         self.capacity, self.num_slots = capacity, num_slots
+        self.plan_cap = max(1, capacity + min(capacity, num_slots))
         layout = [("weight_indices", capacity, torch.int32), ("seg_lens", capacity, torch.int32),
                   ("seg_indptr", capacity + 1, torch.int32), ("lora_ranks", num_slots, torch.int32),
-                  ("scalings", num_slots, dtype)]
+                  ("scalings", num_slots, dtype), ("plan", plan_words(self.plan_cap), torch.int32)]
         offs, cur = [], 0
         for name, n, dt in layout:
             cur = (cur + 63) // 64 * 64
@@ -109,6 +191,8 @@ class PackedColumns:
         self.host_cols: Dict[str, torch.Tensor] = {}
         host_np = self.host.numpy()
         self.host_np = {}
+        self.plan_off = offs[-1][1]
+        self.plan_entries = 0
         for name, off, n, dt in offs:
             es = torch.empty(0, dtype=dt).element_size()
             self.dev_cols[name] = self.dev[off:off + n * es].view(dt)
@@ -121,6 +205,7 @@ class PackedColumns:
     def write(self, columns: Dict[str, Tuple[list, float]]) -> None:
         if self.pending:
             self.event.synchronize()
+        rows = columns["seg_indptr"][0][-1] if columns["seg_indptr"][0] else 0
         for name, (values, pad) in columns.items():
             n = len(values)
             arr = self.host_np.get(name)
@@ -132,7 +217,13 @@ class PackedColumns:
             if n:
                 col[:n].copy_(torch.tensor(values, dtype=col.dtype))  # same conversion as fill_column
             col[n:].fill_(pad)
-        self.dev.copy_(self.host, non_blocking=True)
+        np_cols = self.host_np
+        nb = len(columns["weight_indices"][0])
+        self.plan_entries = build_plan(
+            np_cols["seg_indptr"][:nb + 1], np_cols["weight_indices"][:nb], np_cols["lora_ranks"],
+            self.host_cols["scalings"].float().numpy(), self.num_slots, rows, np_cols["plan"])
+        used = self.plan_off + 4 * plan_words(min(self.plan_entries, self.plan_cap))
+        self.dev[:used].copy_(self.host[:used], non_blocking=True)
         self.event.record()
         self.pending = True
 
@@ -246,6 +337,7 @@ def write_kernel_input_metadata(
         pk.write(columns)
         meta.bs = rows
         meta.max_len = max_len
+        meta.plan_entries = pk.plan_entries
         meta.set_host_copies(lens, pool_batch.weight_indices)
         return meta
 
@@ -256,7 +348,8 @@ def write_kernel_input_metadata(
             c = pk.dev_cols
             fresh = KernelInputMetaData(bs=rows, seg_lens=c["seg_lens"], seg_indptr=c["seg_indptr"],
                                         weight_indices=c["weight_indices"], lora_ranks=c["lora_ranks"],
-                                        scalings=c["scalings"], max_len=max_len, packed=pk)
+                                        scalings=c["scalings"], max_len=max_len, packed=pk, plan=c["plan"],
+                                        plan_cap=pk.plan_cap, plan_entries=pk.plan_entries)
         else:
             fresh = KernelInputMetaData(
                 bs=rows,

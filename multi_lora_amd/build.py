@@ -32,6 +32,11 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Leading pointer / integer kernel arguments arrive preloaded in SGPRs
+    # (gfx950), so a kernel's first loads need not wait for the kernel
+    # argument segment.
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
 ]
 
 

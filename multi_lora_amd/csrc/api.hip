@@ -57,6 +57,7 @@ int check_meta(const mlora_seg_meta* m) {
   if (m->bs > 0 && (m->seg_indptr == nullptr || m->weight_indices == nullptr || m->lora_ranks == nullptr))
     return fail(kBadArg, "null segment table pointer");
   if (m->bs > 0 && m->num_slots > 0 && m->scalings == nullptr) return fail(kBadArg, "null scalings pointer");
+  if (m->plan != nullptr && m->plan_cap < 1) return fail(kBadArg, "plan given with capacity %d", m->plan_cap);
   return 0;
 }
 
@@ -225,24 +226,9 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
 
 }  // namespace
 
-namespace {
-
-// Workspace of mlora_apply_grouped: mode 2 the fp32 sums; mode 1 the linked
-// header and words; mode 0 the linked region, then (256-byte aligned) an
-// fp32 region for the calls it runs as two launches.
-size_t auto_plain_offset(size_t linked) { return (linked + 255) / 256 * 256; }
-
-size_t grouped_ws_bytes(int mode, size_t linked, size_t plain) {
-  if (mode == mlora::kGroupTwo) return plain;
-  if (mode == mlora::kGroupLinked) return linked;
-  return auto_plain_offset(linked) + plain;
-}
-
-}  // namespace
-
 extern "C" {
 
-int mlora_abi_version(void) { return 4; }
+int mlora_abi_version(void) { return 5; }
 
 const char* mlora_last_error(void) { return g_err; }
 
@@ -323,12 +309,28 @@ int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, 
 size_t mlora_grouped_workspace_bytes(int32_t in_dim, int32_t r_max, int32_t n_slices, int32_t num_rows,
                                      int32_t num_slots, int32_t dtype, int32_t mode) {
   (void)num_slots;
-  int kc, k_chunk, nbt, s_groups;
-  size_t linked = 0, plain = 0;
+  mlora::DecodeShape sh;
   if (mode < 0 || mode > 2) return 0;
-  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &s_groups, &linked, &plain))
-    return 0;
-  return grouped_ws_bytes(mode, linked, plain);
+  if (!mlora::plan_decode(in_dim, r_max, n_slices, num_rows, dtype, &sh)) return 0;
+  return sh.bytes;
+}
+
+size_t mlora_plan_bytes(int32_t entries_cap) {
+  if (entries_cap < 0) return 0;
+  return sizeof(int32_t) * (MLORA_PLAN_HEADER_WORDS + static_cast<size_t>(entries_cap) * MLORA_PLAN_ENTRY_WORDS);
+}
+
+int mlora_build_plan(const mlora_seg_meta* meta, int32_t num_rows, int32_t* plan, int32_t plan_cap, void* stream) {
+  g_err[0] = '\0';
+  if (int rc = check_meta(meta)) return rc;
+  if (plan == nullptr || plan_cap < 1 || num_rows < 0)
+    return fail(kBadArg, "plan %p, plan_cap %d, num_rows %d", static_cast<void*>(plan), plan_cap, num_rows);
+  if (meta->num_slots > mlora::kPlanBuildMaxSlots)
+    return fail(kUnsupported, "device plan build takes pools of up to %d slots, got %d", mlora::kPlanBuildMaxSlots,
+                meta->num_slots);
+  const hipError_t e = mlora::launch_build_plan(seg_view(meta), num_rows, plan, plan_cap, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "plan build launch");
+  return 0;
 }
 
 int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
@@ -348,18 +350,19 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   if (x == nullptr || out == nullptr) return fail(kBadArg, "x or out is null");
   if (mode != mlora::kGroupTwo && phases != 3)
     return fail(kBadArg, "phases %d: only the two-launch mode runs one half (use phases=3)", phases);
-  int kc, k_chunk, nbt, s_groups;
-  size_t linked = 0, plain = 0;
-  if (!mlora::plan_grouped(in_dim, r_max, n_slices, num_rows, dtype, &kc, &k_chunk, &nbt, &s_groups, &linked, &plain))
+  mlora::DecodeShape sh;
+  if (!mlora::plan_decode(in_dim, r_max, n_slices, num_rows, dtype, &sh))
     return fail(kUnsupported, "grouped path needs bf16/fp16, r_max <= %d and a multiple of 8, in_dim a multiple of 8",
                 mlora::kGroupMaxRank);
-  const size_t ws = grouped_ws_bytes(mode, linked, plain);
-  if (workspace == nullptr || workspace_bytes < ws)
-    return fail(kWorkspace, "grouped workspace too small: need %zu bytes, got %zu", ws, workspace_bytes);
+  if (workspace == nullptr || workspace_bytes < sh.bytes)
+    return fail(kWorkspace, "grouped workspace too small: need %zu bytes, got %zu", sh.bytes, workspace_bytes);
+  if (meta->plan == nullptr && meta->num_slots > mlora::kPlanBuildMaxSlots)
+    return fail(kUnsupported, "no plan given and the pool has %d slots (the device builder takes up to %d)",
+                meta->num_slots, mlora::kPlanBuildMaxSlots);
   const int vec = vec_elems(dtype);
   const int eb = elem_bytes(dtype);
   bool aligned = al16(x) && x_row_stride % vec == 0 && out_row_stride % vec == 0 && al16(workspace);
-  mlora::GroupedArgs args{};
+  mlora::DecodeArgs args{};
   int tiles = 0;
   for (int s = 0; s < n_slices; ++s) {
     const mlora_slice& sl = slices[s];
@@ -375,10 +378,32 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
               sl.b_slot_stride % vec == 0 && sl.b_row_stride % vec == 0 && sl.out_dim % vec == 0 &&
               al16(static_cast<const char*>(out) + static_cast<int64_t>(sl.out_col) * eb);
     args.slices[s] = slice_view(sl);
+    args.tile_base[s] = tiles;
     tiles += mlora::cdiv(sl.out_dim, mlora::kExpandBN);
   }
+  args.tile_base[n_slices] = tiles;
   if (!aligned)
     return fail(kUnsupported, "grouped path needs 16-byte aligned rows (pointers, strides and widths)");
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int32_t* plan = meta->plan;
+  int plan_cap = meta->plan_cap;
+  int known = meta->plan_entries;
+  if (plan == nullptr) {
+    int32_t* built = reinterpret_cast<int32_t*>(ws + sh.plan_off);
+    plan_cap = sh.e_cap;
+    const hipError_t e = mlora::launch_build_plan(seg_view(meta), num_rows, built, plan_cap, st);
+    if (e != hipSuccess) return hip_fail(e, "plan build launch");
+    plan = built;
+    known = -1;
+  }
+  // Grid rows: the host's entry count when known, else a bound on it (each
+  // slot's rows fill ceil(n / 16) entries).
+  if (known < 0) {
+    const int64_t bound = mlora::cdiv(num_rows, mlora::kPlanRows) + std::min(meta->bs, meta->num_slots);
+    known = static_cast<int>(std::min<int64_t>(num_rows, bound));
+  }
+  known = std::max(1, std::min(known, std::min(plan_cap, sh.e_cap)));
   args.x = x;
   args.x_stride = x_row_stride;
   args.rows = num_rows;
@@ -387,39 +412,28 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   args.r_max = r_max;
   args.out = out;
   args.out_stride = out_row_stride;
-  args.meta = seg_view(meta);
+  args.num_slots = meta->num_slots;
+  args.kc = sh.kc;
+  args.k_chunk = sh.k_chunk;
+  args.s_groups = sh.s_groups;
+  args.n_tiles = tiles;
+  args.e_grid = (known + 7) / 8 * 8;
+  args.e_cap = sh.e_cap;
+  args.plan_cap = plan_cap;
+  args.ws_rows = num_rows;
+  args.header = reinterpret_cast<int*>(ws);
+  args.flags = reinterpret_cast<uint64_t*>(ws + sh.flags_off);
+  args.partials = reinterpret_cast<float*>(ws + sh.partials_off);
+  // Mode 0: the single launch while its work items fit on the chip about at
+  // once; beyond that expand items wait behind shrink items and two launches
+  // are faster (q|k|v over 110 entries, 8064 items: 28.5 vs 34.6 us; the
+  // 128-token q_proj batch, 1024 items: 7.4 vs 9.1 us).
   int m = mode;
   if (m == mlora::kGroupAuto) {
-    const int64_t items = static_cast<int64_t>(meta->num_slots) * (s_groups * kc + tiles);
-    m = (items <= static_cast<int64_t>(mlora::kLinkedItemsPerCu) * num_cus()) ? mlora::kGroupLinked : mlora::kGroupTwo;
+    const int64_t items = static_cast<int64_t>(args.e_grid) * (sh.s_groups * sh.kc + tiles);
+    m = items <= static_cast<int64_t>(mlora::kLinkedItemsPerCu) * num_cus() ? mlora::kGroupLinked : mlora::kGroupTwo;
   }
-  // Mode 0's two launches use the fp32 region after the linked words, so a
-  // later single launch on this workspace never reads their sums as words.
-  args.partials = static_cast<float*>(workspace);
-  if (mode == mlora::kGroupAuto && m == mlora::kGroupTwo)
-    args.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + auto_plain_offset(linked));
-  // The plan's chunks are the single launch's; two launches take chunks
-  // kGroupStepsTwo / kGroupStepsLinked times wider (fewer sums, so the
-  // workspace planned above is large enough).
-  if (m == mlora::kGroupTwo) {
-    k_chunk = k_chunk / mlora::kGroupStepsLinked * mlora::kGroupStepsTwo;
-    kc = mlora::cdiv(in_dim, k_chunk);
-  }
-  args.kc = kc;
-  args.k_chunk = k_chunk;
-  args.s_groups = s_groups;
-  // Expand items cover 256 columns in the single launch and 512 with two
-  // launches (measured: decode q_proj linked 8.8 vs 9.5 us with 512; the
-  // q|k|v expand half at 128 rank-32 adapters 15.8 vs 17.5 us with 256).
-  args.expand_wn = (m == mlora::kGroupTwo) ? 2 : 1;
-  tiles = 0;
-  for (int s = 0; s < n_slices; ++s) {
-    args.tile_base[s] = tiles;
-    tiles += mlora::cdiv(slices[s].out_dim, mlora::kExpandBN * args.expand_wn);
-  }
-  args.tile_base[n_slices] = tiles;
-  args.n_tiles = tiles;
-  const hipError_t e = mlora::launch_grouped(args, dtype, nbt, m, phases, static_cast<hipStream_t>(stream));
+  const hipError_t e = mlora::launch_planned(plan, args, dtype, sh.nbt, m, phases, st);
   if (e != hipSuccess) return hip_fail(e, "grouped launch");
   return 0;
 }

@@ -1,0 +1,694 @@
+// Slot-planned shrink+expand for decode-shaped batches (gfx950).
+//
+// The reference runs one GEMV program per token in decode, so every token
+// streams its adapter's whole A and B (multi_lora/kernels/sgemm_lora_a.py:118-183,
+// sgemm_lora_b.py:93-153).  Here the work follows a per-step *plan* of the
+// segment table: one entry per (referenced slot, up to 16 of its rows), with
+// the slot, its rank and scaling, the rows, and their position in the
+// workspace (layout in include/mlora_hip.h).  Slots no row uses, and rank-0
+// slots, have no entry, so their A and B are never read.
+//
+//   shrink item  (entry, slice group, K chunk of 4 waves x SP x 32): the
+//                entry (with its rows) comes in one scalar load, then the
+//                chunk's A fragments and the entry's x rows together; they
+//                are multiplied on MFMA (16 rank rows x 16 token rows a
+//                tile), the four waves' sums added in LDS, and the chunk's
+//                fp32 sums stored to the workspace.
+//   expand item  (entry, 256 output columns of one slice): B fragments and
+//                the output rows are requested first; once the sums of every
+//                K chunk are there they are added (four chunk groups, each in
+//                chunk order, then the groups in order) and rounded to the
+//                storage type (the
+//                reference's `mid` rounding, sgemm_lora_a.py:109), multiplied
+//                with B on MFMA, scaled and rounded (sgemm_lora_b.py:84-89),
+//                and added into the output rows through an LDS transpose.
+//
+// Single launch (linked).  Workgroup b is item b / E of entry slot b % E,
+// with E a multiple of 8.  Workgroups are placed on the XCDs round-robin
+// (b mod 8), so every item of an entry runs on one XCD and shares its L2.
+// A shrink item stores its fp32 sums with plain stores, which stay in that
+// L2, waits for their acknowledgement (vmcnt(0)), then stores the chunk's
+// 64-bit flag {launch tag, XCC id}.  Expand items poll the flags and read
+// the sums with device-scope (sc1) loads, which skip the CU's L1 and are
+// served by the L2 (a workgroup-scope load may be served by the L1, which
+// keeps the first value it fetched while another CU updates the line;
+// device-scope stores would write through past the L2, so the reads after
+// them go to memory).  The tag is an odd function of the launch's dispatch
+// id on its hardware queue (fresh for every launch and graph replay), so
+// the workspace is never cleared.  An expand item takes a chunk once its
+// flag carries this launch's tag and its own XCC id; a chunk it does not
+// get that way before a deadline (a late producer, or one on another XCD,
+// whose L2 it cannot see) it computes itself from x and A, bit for bit as
+// the shrink item would, and publishes it; the workspace header counts such
+// chunks.  So results never depend on placement or timing, only speed
+// does.  Shrink items come first in the grid and never wait, so every wait
+// also ends on its own.  (Sums carried as 64-bit words {tag, value}, which
+// need no flag and no acknowledgement, were measured slower: twice the
+// bytes to store under load.)
+//
+// Two launches: shrink items, then expand items, with the same bodies and
+// the same sums (bit-identical results); the kernel boundary orders them.
+#include "kernels.h"
+#include "loads.h"
+
+namespace mlora {
+
+// The launch's dispatch id (its AQL packet index on the hardware queue).
+__device__ uint64_t planned_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+namespace {
+
+constexpr int kDefaultWaitTicks = 20000;  // 200 us of s_memrealtime (100 MHz)
+constexpr int kGroups = 4;                // chunk groups summed separately, then in order
+
+struct Entry {
+  int slot;
+  int rank;   // clamped to [0, r_max]; 0 for a slot outside the call's pool
+  int nr;     // rows, [0, 16]
+  int pos;    // first workspace row
+  float scale;
+};
+
+// Entry e of the plan; e is wave-uniform, so these are scalar loads.
+__device__ __forceinline__ Entry load_entry(const int32_t* plan, int e, int r_max, int num_slots) {
+  const int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords;
+  Entry en;
+  en.slot = p[kPlanSlot];
+  const int r = p[kPlanRank];
+  en.scale = __int_as_float(p[kPlanScale]);
+  en.nr = min(max(p[kPlanRowCount], 0), kPlanRows);
+  en.pos = p[kPlanPos];
+  en.rank = (en.slot >= 0 && en.slot < num_slots) ? min(max(r, 0), r_max) : 0;
+  return en;
+}
+
+// Row i (< 16) of entry e (a vector load: its address needs no other load,
+// so it goes out together with the entry's scalar loads), clamped to
+// [0, rows).  The plan pads an entry's unused row words with its first row.
+__device__ __forceinline__ int load_entry_row(const int32_t* plan, int e, int i) {
+  return plan[kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord + i];
+}
+
+__device__ __forceinline__ int clamp_row(int r, int rows) { return min(max(r, 0), rows - 1); }
+
+// This launch's tag: odd (a zero-filled workspace never matches), equal for
+// every workgroup of the launch, different for launches on one queue fewer
+// than 2^31 packets apart; the queue address salts it.
+__device__ __forceinline__ uint32_t launch_tag() {
+  const uint64_t q = reinterpret_cast<uint64_t>(__builtin_amdgcn_queue_ptr());
+  const uint32_t salt = static_cast<uint32_t>(q ^ (q >> 32)) * 0x9E3779B1u;
+  return ((static_cast<uint32_t>(planned_dispatch_id()) + salt) << 1) | 1u;
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xfu;
+}
+
+__device__ __forceinline__ uint64_t flag_word() { return (static_cast<uint64_t>(launch_tag()) << 32) | xcc_id(); }
+
+__device__ __forceinline__ uint64_t* flag_ptr(const DecodeArgs& a, int e, int sg, int c) {
+  return a.flags + (static_cast<int64_t>(e) * a.s_groups + sg) * a.kc + c;
+}
+
+// Workspace row `pos`, chunk c, column col: fp32 sum of one K chunk.
+__device__ __forceinline__ int64_t sum_index(const DecodeArgs& a, int pos, int c, int col) {
+  return (static_cast<int64_t>(pos) * a.kc + c) * (a.n_slices * a.r_max) + col;
+}
+
+// One K chunk of one entry's shrink, for the slices of group sg:
+// sums[i][n] = sum over the chunk of x[row_i, k] * A_s[slot, n, k], stored to
+// the workspace by wave 0 for the entry's rows, then (flag != 0) the chunk's
+// flag once the sums are acknowledged.  xrow: this lane's x row (row
+// lane & 15 of the entry).  All threads call it; it ends with an LDS barrier.
+template <class T, int NBT, int SP>
+__device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xrow, int sg, int c,
+                             f32x4 (*red)[kWave], uint64_t flag) {
+  using raw = typename T::raw_t;
+  constexpr int VEC = T::VEC;
+  constexpr int KSTEP = T::KSTEP;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int rank = en.rank;
+  const int nb_act = (rank + 15) >> 4;
+  const int s_first = (a.s_groups == 1) ? 0 : sg;
+  const int nbt = ((a.s_groups == 1) ? a.n_slices : 1) * nb_act;
+  const int kbeg = c * a.k_chunk;
+
+  // A fragments, loaded unmasked (clamped in bounds) and dropped past in_dim
+  // where the MFMA uses them, so nothing between here and the x loads waits
+  // for them.  in_dim is a multiple of the chunk: a chunk is wholly inside
+  // or wholly outside.
+  u32x4 af[SP][NBT];
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) {
+    const int jj = j < nbt ? j : 0;
+    const int sl = jj / nb_act;  // slice within the group
+    const raw* arow = slice_a<raw>(a.slices, s_first + sl, en.slot, min((jj - sl * nb_act) * 16 + r16, rank - 1));
+#pragma unroll
+    for (int sp = 0; sp < SP; ++sp) {
+      const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+      af[sp][j] = ld_chunk(arow + (kk < a.in_dim ? kk : 0));
+    }
+  }
+  const raw* xr = static_cast<const raw*>(a.x) + static_cast<int64_t>(xrow) * a.x_stride;
+  u32x4 xv[SP];
+#pragma unroll
+  for (int sp = 0; sp < SP; ++sp) {
+    const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+    const u32x4 v = ld_chunk(xr + (kk < a.in_dim ? kk : 0));
+    xv[sp] = kk < a.in_dim ? v : zero_chunk();
+  }
+  fence_regs(af);
+  f32x4 acc[NBT];
+#pragma unroll
+  for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < SP; ++sp) {
+    const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+#pragma unroll
+    for (int j = 0; j < NBT; ++j)
+      if (j < nbt) acc[j] = T::mma(acc[j], kk < a.in_dim ? af[sp][j] : zero_chunk(), xv[sp]);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < NBT; ++j)
+      if (j < nbt) red[(wave - 1) * NBT + j][lane] = acc[j];
+  }
+  lds_barrier();
+  if (wave == 0) {
+#pragma unroll 1
+    for (int w2 = 0; w2 < 3; ++w2)
+#pragma unroll
+      for (int j = 0; j < NBT; ++j)
+        if (j < nbt) acc[j] += red[w2 * NBT + j][lane];
+    // Lane l holds token row l & 15 and rank columns 4 (l >> 4) .. + 3 of
+    // each 16-column block.
+    if (r16 < en.nr) {
+#pragma unroll
+      for (int j = 0; j < NBT; ++j) {
+        if (j >= nbt) break;
+        const int sl = j / nb_act;
+        const int n = (j - sl * nb_act) * 16 + 4 * g;
+        if (n >= a.r_max) continue;
+        *reinterpret_cast<f32x4*>(a.partials + sum_index(a, en.pos + r16, c, (s_first + sl) * a.r_max + n)) = acc[j];
+      }
+    }
+    if (flag != 0) {
+      // The flag goes out only once every sum of the chunk has reached the L2.
+      asm volatile("" ::: "memory");
+      wait_vmcnt<0>();
+      asm volatile("" ::: "memory");
+      if (lane == 0) __hip_atomic_store(flag_ptr(a, e, sg, c), flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  lds_barrier();
+}
+
+template <class T, int WN>
+struct DecodeLds {
+  using raw = typename T::raw_t;
+  raw delta[16 * (kExpandBN * WN + T::VEC)];
+  raw ytile[16 * (kGroupMaxRank + T::VEC)];
+  f32x4 part[kGroups][16][kGroupMaxRank / 4];  // per chunk group: sums of each (row, 4 columns)
+  uint64_t missing;                             // chunks not received
+};
+
+// 16 bytes of the workspace at byte offset `off`, read past the L1 (sc1):
+// the L2 holds what other workgroups of this XCD stored.
+__device__ __forceinline__ u32x4 load16_l2(__amdgpu_buffer_rsrc_t rsrc, int64_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(off), 0, /*sc1*/ 16));
+}
+
+// The y sums of rows < nr and columns < rank of slice s into lds.part: unit
+// u = (group, row, quad) adds the chunks of its group in chunk order, up to
+// four chunks' sums requested together.
+template <class T, int WN>
+__device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeLds<T, WN>& lds) {
+  const int quads = (en.rank + 3) >> 2;
+  const int per = (a.kc + kGroups - 1) / kGroups;  // chunks per group
+  const int units = kGroups * en.nr * quads;
+  const int ncols = a.n_slices * a.r_max;
+  const int64_t bytes = static_cast<int64_t>(a.ws_rows) * a.kc * ncols * 4;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      a.partials, 0, static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff), kBufferRsrcWord3);
+  for (int u = threadIdx.x; u < units; u += 256) {
+    const int grp = u / (en.nr * quads);
+    const int rem = u - grp * (en.nr * quads);
+    const int row = rem / quads;
+    const int q = rem - row * quads;
+    const int c0 = grp * per;
+    const int c1 = min(c0 + per, a.kc);
+    const int64_t base = sum_index(a, en.pos + row, 0, s * a.r_max + 4 * q);
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = c0; cb < c1; cb += 4) {
+      u32x4 w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = load16_l2(rsrc, (base + static_cast<int64_t>(min(cb + k, c1 - 1)) * ncols) * 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (cb + k < c1) sum += __builtin_bit_cast(f32x4, w[k]);
+    }
+    lds.part[grp][row][q] = sum;
+  }
+  lds_barrier();
+}
+
+// Expand item (entry e, column tile nt_g).  LINKED: the sums come as tagged
+// words from this launch's shrink items (or are computed here), else as
+// fp32 from the previous launch.
+template <class T, int NBT, int SP, int WN, int RS, bool LINKED>
+__device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, const Entry& en, int nt_g,
+                             const int (&orow_raw)[16 * kExpandBN * WN / T::VEC / 256], DecodeLds<T, WN>& lds,
+                             f32x4 (*red)[kWave]) {
+  using raw = typename T::raw_t;
+  constexpr int VEC = T::VEC;
+  constexpr int KSTEP = T::KSTEP;
+  constexpr int BN = kExpandBN * WN;
+  constexpr int NBW = 4 * WN;  // 16-column blocks per wave
+  constexpr int LDS_STRIDE = BN + VEC;
+  constexpr int CPR = BN / VEC;  // chunks per output row
+  constexpr int RPT = 16 * CPR / 256;
+  constexpr int YS = kGroupMaxRank + VEC;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int rank = en.rank;
+
+  int s = 0;
+  while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
+  const int n0 = (nt_g - a.tile_base[s]) * BN;
+  const int out_dim = a.slices[s].out_dim;
+  const int sg = (a.s_groups == 1) ? 0 : s;
+
+  // The workspace's wait limit (written by other launches, so a vector load).
+  const int over = LINKED ? a.header[kWsWaitOverride] : 0;
+  raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
+  int orow[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) orow[i] = clamp_row(orow_raw[i], a.rows);
+  // B fragments: rows clamped to out_dim, loaded unmasked and masked to the
+  // rank where the MFMA uses them.
+  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(en.slot) * a.slices[s].b_slot_stride;
+  u32x4 bf[RS][NBW];
+  u32x4 ov[RPT];
+  auto load_b = [&]() {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      const raw* brow =
+          B + static_cast<int64_t>(min(n0 + (wave * NBW + nb) * 16 + r16, out_dim - 1)) * a.slices[s].b_row_stride;
+#pragma unroll
+      for (int ks = 0; ks < RS; ++ks) {
+        const int kk = ks * KSTEP + g * VEC;
+        bf[ks][nb] = ld_chunk(brow + (kk < rank ? kk : 0));
+      }
+    }
+  };
+  auto load_out = [&]() {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int cidx = tid + i * 256;
+      const int row = cidx / CPR;
+      const int n = n0 + (cidx - row * CPR) * VEC;
+      ov[i] = load_row_chunk<T, true>(out + static_cast<int64_t>(orow[i]) * a.out_stride, n, out_dim - n);
+    }
+  };
+  // B and the output rows are requested at once: requested later (after a
+  // delay, or once the flags are in), their arrival moves the end of the
+  // item by as much (measured: +0.5 us per 0.5 us of delay).
+  load_b();
+  load_out();
+
+  if constexpr (LINKED) {
+    // Wave 0 polls the flags of the chunks this slice needs (at most 64),
+    // one lane per chunk, until each carries this launch's tag and this XCD,
+    // or the deadline passes; the rest are computed here.
+    const uint64_t want = flag_word();
+    if (wave == 0) {
+      // 0 waiting, 1 arrived, 2 this launch's tag from another XCD (its sums
+      // sit in that XCD's L2, out of reach of these loads).
+      int st = lane >= a.kc ? 1 : 0;
+      const uint64_t* fp = flag_ptr(a, e, sg, min(lane, a.kc - 1));
+      const uint64_t limit = over > 0 ? static_cast<uint64_t>(over) : kDefaultWaitTicks;
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      // A negative limit skips the wait: every chunk is computed here.
+      while (over >= 0) {
+        if (st == 0) {
+          const uint64_t w = __hip_atomic_load(fp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (w == want)
+            st = 1;
+          else if ((w >> 32) == (want >> 32))
+            st = 2;
+        }
+        if (__all(st != 0)) break;
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= limit) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const uint64_t miss = __ballot(st != 1);
+      if (lane == 0) lds.missing = miss;
+    }
+    lds_barrier();
+    uint64_t miss = lds.missing;
+    if (miss != 0) {
+      // Compute the missing chunks here, bit for bit as their shrink items
+      // would, and publish them for the entry's other expand items.
+      const int xrow = clamp_row(load_entry_row(plan, e, r16), a.rows);
+      if (tid == 0) atomicAdd(a.header + kWsFallbacks, __popcll(miss));
+      while (miss != 0) {
+        const int z = __builtin_ctzll(miss);
+        miss &= miss - 1;
+        shrink_chunk<T, NBT, SP>(a, e, en, xrow, sg, z, red, want);
+      }
+      // The prefetched B fragments and output rows are requested again, so
+      // they hold no registers across the computation above (a rare path).
+      load_b();
+      load_out();
+    }
+  }
+  gather_sums<T, WN>(a, en, s, lds);
+  fence_regs(bf);
+
+  // y = the chunk groups' sums added in group order, rounded like the
+  // reference's mid; zero at and past the rank and for rows past the entry's.
+  {
+    const int quads = a.r_max / 4;
+    for (int q = tid; q < 16 * quads; q += 256) {
+      const int row = q / quads;
+      const int c4 = (q - row * quads) * 4;
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (row < en.nr && c4 < rank) {
+#pragma unroll
+        for (int grp = 0; grp < kGroups; ++grp) sum += lds.part[grp][row][c4 / 4];
+      }
+      raw* y = lds.ytile + row * YS + c4;
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) y[q2] = T::from_f32(c4 + q2 < rank ? sum[q2] : 0.f);
+    }
+  }
+  lds_barrier();
+
+  f32x4 acc[NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < RS; ++ks) {
+    if (ks * KSTEP >= rank) break;
+    const int kk = ks * KSTEP + g * VEC;
+    const u32x4 yv = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(lds.ytile + r16 * YS + kk) : zero_chunk();
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) acc[nb] = T::mma(acc[nb], bf[ks][nb] & keep_mask<T>(rank - kk), yv);
+  }
+  const float scale = en.scale;
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    const f32x4 v = acc[nb];
+    uint2 w;
+    w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) | (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
+    w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) | (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
+    *reinterpret_cast<uint2*>(lds.delta + r16 * LDS_STRIDE + (wave * NBW + nb) * 16 + 4 * g) = w;
+  }
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int cidx = tid + i * 256;
+    const int row = cidx / CPR;
+    const int cc = cidx - row * CPR;
+    const int n = n0 + cc * VEC;
+    if (row < en.nr && n < out_dim) {
+      const u32x4 d = *reinterpret_cast<const u32x4*>(lds.delta + row * LDS_STRIDE + cc * VEC);
+      float f[VEC];
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) f[q] = chunk_elem<T>(ov[i], q) + chunk_elem<T>(d, q);
+      st_chunk(out + static_cast<int64_t>(orow[i]) * a.out_stride + n, pack_chunk<T>(f));
+    }
+  }
+  lds_barrier();
+}
+
+// Items [0, n_shrink) of an entry are its shrink items, the next n_tiles its
+// expand items; workgroup b is item b / e_grid of entry b % e_grid, then of
+// entries b % e_grid + e_grid, + 2 e_grid, ... while the plan has them.
+template <class T, int NBT, int WN, int RS, int SCHED>
+__global__ __launch_bounds__(256, NBT >= 8 ? 2 : 4) void planned_kernel(const int32_t* __restrict__ plan, DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
+  __shared__ f32x4 red[3 * NBT][kWave];
+  constexpr int SP = kGroupStepsLinked;
+  const int n_shrink = (SCHED == kGroupExpandOnly) ? 0 : a.s_groups * a.kc;
+  const int item = blockIdx.x / a.e_grid;
+  const int j = blockIdx.x - item * a.e_grid;
+  constexpr int RPT = 16 * kExpandBN * WN / T::VEC / 256;  // output chunks per thread of an expand item
+  const bool shrink = item < n_shrink;
+  // The first entry, its rows this thread needs and the plan's entry count
+  // go out together.
+  int e = j;
+  const int ef = min(e, a.plan_cap - 1);
+  int rows_raw[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    rows_raw[i] = load_entry_row(plan, ef, shrink ? (threadIdx.x & 15) : (threadIdx.x + i * 256) * T::VEC / (kExpandBN * WN));
+  Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
+  const int n_ent = min(plan[0], min(a.plan_cap, a.e_cap));
+  if (j == 0 && item == 0 && threadIdx.x == 0 && plan[0] > min(a.plan_cap, a.e_cap))
+    atomicAdd(a.header + kWsPlanErrors, 1);
+  while (e < n_ent) {
+    if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows) {
+      if (shrink) {
+        if constexpr (SCHED != kGroupExpandOnly)
+          shrink_chunk<T, NBT, SP>(a, e, en, clamp_row(rows_raw[0], a.rows), item / a.kc, item % a.kc, red,
+                                   SCHED == kGroupLinked ? flag_word() : 0);
+      } else if constexpr (SCHED != kGroupShrinkOnly) {
+        expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked>(a, plan, e, en, item - n_shrink, rows_raw, lds, red);
+      }
+    } else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0) {
+      atomicAdd(a.header + kWsPlanErrors, 1);
+    }
+    e += a.e_grid;
+    if (e >= n_ent) break;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      rows_raw[i] = load_entry_row(plan, e, shrink ? (threadIdx.x & 15) : (threadIdx.x + i * 256) * T::VEC / (kExpandBN * WN));
+    en = load_entry(plan, e, a.r_max, a.num_slots);
+  }
+}
+
+template <class T, int NBT, int WN, int RS>
+hipError_t launch_sched(const int32_t* plan, const DecodeArgs& a, int sched, int n_items, hipStream_t stream) {
+  const int64_t blocks = static_cast<int64_t>(n_items) * a.e_grid;
+  if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  switch (sched) {
+    case kGroupLinked:
+      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupLinked>), grid, dim3(256), 0, stream, plan, a);
+      break;
+    case kGroupShrinkOnly:
+      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupShrinkOnly>), grid, dim3(256), 0, stream, plan, a);
+      break;
+    default:
+      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupExpandOnly>), grid, dim3(256), 0, stream, plan, a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+template <class T, int NBT, int WN, int RS>
+hipError_t launch_t(const int32_t* plan, const DecodeArgs& a, int mode, int phases, hipStream_t stream) {
+  const int n_shrink = a.s_groups * a.kc;
+  if (mode == kGroupLinked) return launch_sched<T, NBT, WN, RS>(plan, a, kGroupLinked, n_shrink + a.n_tiles, stream);
+  // Two launches: the shrink grid holds the shrink items, the expand grid
+  // the expand items (item i of entry j is workgroup i * e_grid + j there).
+  if (phases & 1) {
+    const hipError_t e = launch_sched<T, NBT, WN, RS>(plan, a, kGroupShrinkOnly, n_shrink, stream);
+    if (e != hipSuccess) return e;
+  }
+  if (phases & 2) return launch_sched<T, NBT, WN, RS>(plan, a, kGroupExpandOnly, a.n_tiles, stream);
+  return hipSuccess;
+}
+
+template <class T, int WN, int RS>
+hipError_t launch_nbt(const int32_t* plan, const DecodeArgs& a, int nbt, int mode, int phases, hipStream_t stream) {
+  switch (nbt) {
+    case 1: return launch_t<T, 1, WN, RS>(plan, a, mode, phases, stream);
+    case 2: return launch_t<T, 2, WN, RS>(plan, a, mode, phases, stream);
+    default: return launch_t<T, 4, WN, RS>(plan, a, mode, phases, stream);
+  }
+}
+
+template <class T>
+hipError_t launch_dtype(const int32_t* plan, const DecodeArgs& a, int nbt, int mode, int phases, hipStream_t stream) {
+  if (a.r_max <= T::KSTEP) return launch_nbt<T, 1, 1>(plan, a, nbt, mode, phases, stream);
+  return launch_nbt<T, 1, 2>(plan, a, nbt, mode, phases, stream);
+}
+
+// Plan of a segment table, built on the device by one workgroup of 1024
+// threads (for callers that pass no plan): the same plan, word for word, as
+// the host's (multi_lora_amd/batch_info.py: build_plan).  Entries follow the
+// slots in ascending order; a slot's rows, in row order, fill entries of 16.
+// Segment bounds are clamped to [0, rows); slots outside [0, num_slots) and
+// rank-0 slots get no entry.  Entries past `cap` are not written (the header
+// still counts them, and the apply kernels report a plan error).
+constexpr int kBuildThreads = 1024;
+constexpr int kBuildSegs = 1024;  // segments staged in LDS per pass
+
+__global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, int rows, int32_t* plan, int cap) {
+  __shared__ int cnt[kPlanBuildMaxSlots];
+  __shared__ int eoff[kPlanBuildMaxSlots];
+  __shared__ int poff[kPlanBuildMaxSlots];
+  __shared__ int seg_slot[kBuildSegs];
+  __shared__ int seg_start[kBuildSegs];
+  __shared__ int seg_len[kBuildSegs];
+  __shared__ int tmp[kBuildThreads / kWave];
+  __shared__ int run[2];
+  const int tid = threadIdx.x;
+  const int ns = m.num_slots;
+  for (int s = tid; s < ns; s += kBuildThreads) cnt[s] = 0;
+  __syncthreads();
+  auto seg_of = [&](int i, int* slot, int* st, int* len) {
+    const int a0 = min(max(m.indptr[i], 0), rows);
+    const int a1 = min(max(m.indptr[i + 1], 0), rows);
+    const int w = m.widx[i];
+    const bool live = w >= 0 && w < ns && m.ranks[w] > 0 && a1 > a0;
+    *slot = live ? w : -1;
+    *st = a0;
+    *len = live ? a1 - a0 : 0;
+  };
+  for (int i = tid; i < m.bs; i += kBuildThreads) {
+    int w, st, len;
+    seg_of(i, &w, &st, &len);
+    if (w >= 0) atomicAdd(&cnt[w], len);
+  }
+  __syncthreads();
+  // Exclusive scans over the slots (in chunks of kBuildThreads): entries and rows.
+  if (tid == 0) run[0] = run[1] = 0;
+  __syncthreads();
+  for (int s0 = 0; s0 < ns; s0 += kBuildThreads) {
+    const int s = s0 + tid;
+    const int c = s < ns ? cnt[s] : 0;
+    int tot_e, tot_r;
+    const int ex_e = block_exclusive_scan<kBuildThreads / kWave>((c + kPlanRows - 1) / kPlanRows, tmp, &tot_e);
+    const int ex_r = block_exclusive_scan<kBuildThreads / kWave>(c, tmp, &tot_r);
+    if (s < ns) {
+      eoff[s] = run[0] + ex_e;
+      poff[s] = run[1] + ex_r;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      run[0] += tot_e;
+      run[1] += tot_r;
+    }
+    __syncthreads();
+  }
+  const int n_entries = run[0];
+  if (tid == 0) {
+    plan[0] = n_entries;
+    plan[1] = run[1];
+    plan[2] = cap;
+  }
+  // Entry headers, with every row word first set to an invalid row.
+  for (int s = tid; s < ns; s += kBuildThreads) {
+    const int c = cnt[s];
+    if (c == 0) continue;
+    const float sc = load_scaling(m.scalings, s, m.scal_dtype);
+    for (int k = 0; k * kPlanRows < c; ++k) {
+      const int e = eoff[s] + k;
+      if (e >= cap) break;
+      int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords;
+      for (int w = 0; w < kPlanEntryWords; ++w) p[w] = 0;
+      p[kPlanSlot] = s;
+      p[kPlanRank] = m.ranks[s];
+      p[kPlanScale] = __float_as_int(sc);
+      p[kPlanRowCount] = min(kPlanRows, c - k * kPlanRows);
+      p[kPlanPos] = poff[s] + k * kPlanRows;
+    }
+  }
+  // Rows: each thread walks the segments in order for its slots, so a
+  // slot's rows come out in row order.
+  for (int s = tid; s < ((ns + kBuildThreads - 1) / kBuildThreads) * kBuildThreads; s += kBuildThreads) {
+    const bool mine = s < ns && cnt[s] > 0;
+    int q = 0;
+    for (int b0 = 0; b0 < m.bs; b0 += kBuildSegs) {
+      __syncthreads();
+      for (int i = tid; i < kBuildSegs; i += kBuildThreads) {
+        int w = -1, st = 0, len = 0;
+        if (b0 + i < m.bs) seg_of(b0 + i, &w, &st, &len);
+        seg_slot[i] = w;
+        seg_start[i] = st;
+        seg_len[i] = len;
+      }
+      __syncthreads();
+      if (!mine) continue;
+      const int nseg = min(kBuildSegs, m.bs - b0);
+      for (int i = 0; i < nseg; ++i) {
+        if (seg_slot[i] != s) continue;
+        for (int r = 0; r < seg_len[i]; ++r, ++q) {
+          const int e = eoff[s] + q / kPlanRows;
+          if (e < cap)
+            plan[kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord + q % kPlanRows] =
+                seg_start[i] + r;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // Pad each entry's unused row words with its first row.  (Global writes
+  // of this workgroup above are visible to it after the barrier: same CU.)
+  __threadfence_block();
+  for (int e = tid; e < min(n_entries, cap); e += kBuildThreads) {
+    int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords;
+    const int nr = p[kPlanRowCount];
+    const int r0 = p[kPlanRowWord];
+    for (int i = nr; i < kPlanRows; ++i) p[kPlanRowWord + i] = r0;
+  }
+}
+
+}  // namespace
+
+namespace {
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+}  // namespace
+
+bool plan_decode(int in_dim, int r_max, int n_slices, int rows, int dtype, DecodeShape* sh) {
+  if (dtype != MLORA_BF16 && dtype != MLORA_F16) return false;
+  if (in_dim <= 0 || rows <= 0 || n_slices < 1 || n_slices > kMaxSlices) return false;
+  if (r_max <= 0 || r_max > kGroupMaxRank || r_max % 8 != 0 || in_dim % 8 != 0) return false;
+  // More than four 16-row A blocks in all: one shrink item per slice, so an
+  // item never holds more than four blocks of A fragments.
+  const int blocks = n_slices * cdiv(r_max, 16);
+  sh->s_groups = (blocks > 4) ? n_slices : 1;
+  const int item_blocks = blocks / sh->s_groups;
+  int b = 1;
+  while (b < item_blocks) b *= 2;
+  sh->nbt = b;
+  sh->k_chunk = 4 * kGroupStepsLinked * BF16::KSTEP;
+  sh->kc = cdiv(in_dim, sh->k_chunk);
+  if (sh->kc > kWave) return false;  // one polling lane per chunk: in_dim <= 16384
+  // Every entry holds at least one row: at most `rows` entries.
+  sh->e_cap = rows;
+  const size_t n_sums = static_cast<size_t>(rows) * sh->kc * n_slices * r_max;
+  if (n_sums * sizeof(float) >= 0x7fffffffu) return false;  // read through a 32-bit buffer range
+  sh->flags_off = kWsHeaderBytes;
+  sh->partials_off = sh->flags_off + round256(static_cast<size_t>(sh->e_cap) * sh->s_groups * sh->kc * sizeof(uint64_t));
+  sh->plan_off = sh->partials_off + round256(n_sums * sizeof(float));
+  sh->bytes = sh->plan_off + sizeof(int32_t) * (kPlanHeaderWords + static_cast<size_t>(sh->e_cap) * kPlanEntryWords);
+  return true;
+}
+
+hipError_t launch_build_plan(const SegView& m, int rows, int32_t* plan, int cap, hipStream_t stream) {
+  hipLaunchKernelGGL(build_plan_kernel, dim3(1), dim3(kBuildThreads), 0, stream, m, rows, plan, cap);
+  return hipGetLastError();
+}
+
+hipError_t launch_planned(const int32_t* plan, const DecodeArgs& args, int dtype, int nbt, int mode, int phases,
+                          hipStream_t stream) {
+  if (dtype == MLORA_BF16) return launch_dtype<BF16>(plan, args, nbt, mode, phases, stream);
+  return launch_dtype<F16>(plan, args, nbt, mode, phases, stream);
+}
+
+}  // namespace mlora

@@ -158,7 +158,11 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
       if constexpr (FUSED)
-        yv[tb] = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(ytile + (tb * 16 + r16) * YS + kk) : zero_chunk();
+        // Masked to the rank: when r_max is not a multiple of the chunk,
+        // the chunk's tail past r_max lies in LDS the fill never wrote.
+        yv[tb] = (kk < a.r_max) ? *reinterpret_cast<const u32x4*>(ytile + (tb * 16 + r16) * YS + kk) &
+                                      keep_mask<T>(valid)
+                                : zero_chunk();
       else
         yv[tb] = load_row_chunk<T, AL>(mrow[tb], kk, valid);
     }

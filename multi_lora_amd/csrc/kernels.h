@@ -95,27 +95,22 @@ constexpr int kFuseMaxTiles = 16;
 
 hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream);
 
-// -------------------------------------------------------------- grouped decode
-// Slot-grouped shrink+expand: work items are indexed by (slot, chunk), find
-// their slot's rows by scanning the segment table, and read each slot's A / B
-// once per chunk.  Shrink items leave fp32 K-chunk sums in the workspace;
-// expand items add them in chunk order and apply the expand.
+// -------------------------------------------------------------- slot-grouped items
+// Shared by the mixed-batch expand (grouped.hip): work items indexed by
+// (slot, column tile) that find their slot's rows by scanning the segment
+// table and read each slot's B tile once for all of them.
 constexpr int kGroupRows = 256;  // rows gathered per pass
-// K-steps per wave per K chunk (chunk = 4 waves x steps x 32): 256-wide
-// chunks in the single launch, 512-wide with two launches (measured: decode
-// q_proj linked 8.4 vs 8.7 us with 512; q|k|v at 128 rank-32 adapters, two
-// launches with 64-bit sums, 42.4 vs 45.4 us with 256).
+// K-steps per wave per K chunk of the planned decode shrink (chunk = 4 waves
+// x steps x 32 = 256 elements).
 constexpr int kGroupStepsLinked = 2;
-constexpr int kGroupStepsTwo = 4;
-constexpr int kGroupAuto = 0;    // mode: the library picks one of the two below
-constexpr int kGroupLinked = 1;  // mode: one launch, sums passed as tagged words
-constexpr int kGroupTwo = 2;     // mode: two launches, sums passed as plain fp32
-// kGroupAuto takes the single launch while num_slots * (shrink + expand items
-// per slot) is at most this many per CU: beyond that the items no longer fit
-// on the chip at once, and expand items left waiting cost more than the
-// second launch.
+constexpr int kGroupAuto = 0;    // mode: the library's choice (the single launch)
+constexpr int kGroupLinked = 1;  // mode: one launch, sums handed over through the L2
+constexpr int kGroupTwo = 2;     // mode: two launches
+constexpr int kGroupShrinkOnly = 3;  // launch schedules of the two-launch mode
+constexpr int kGroupExpandOnly = 4;
+// kGroupAuto takes the single launch while the grid holds at most this many
+// work items per CU, else two launches.
 constexpr int kLinkedItemsPerCu = 16;
-constexpr size_t kLinkedHeader = 256;  // linked workspace: error word, padded
 
 struct GroupedArgs {
   const void* x;
@@ -128,23 +123,89 @@ struct GroupedArgs {
   void* out;
   int64_t out_stride;
   SegView meta;
-  float* partials;   // two launches: [kc][rows][n_slices * r_max]; linked: the linked workspace
-  int kc;            // K chunks
-  int k_chunk;       // reduction elements per chunk
-  int s_groups;      // shrink items per (slot, chunk): 1 (all slices) or n_slices (one each)
+  float* partials;   // split sums [kc][rows][n_slices * r_max]
+  int kc;            // K splits
+  int k_chunk;
+  int s_groups;
   int n_tiles;       // expand items per slot (column tiles over all slices)
   int tile_base[kMaxSlices + 1];
-  int expand_wn;     // 256-column blocks per expand item (1 or 2)
-  // Mixed-batch expand (launch_mixed): expand items take the rows of the
-  // slot's short segments only (at most kShortSegRows rows), and y from
-  // `mid` (or, with split sums, from `partials` with kc = the split count).
+  int expand_wn;     // 256-column blocks per expand item
+  // Expand items take the rows of the slot's short segments only (at most
+  // kShortSegRows rows), and y from `mid` (or, with split sums, from
+  // `partials` with kc = the split count).
   int short_only;
   const void* mid;
   int64_t mid_stride;
 };
 
-// Largest r_max (per slice) the grouped path handles.
+// Largest r_max (per slice) the grouped and planned paths handle.
 constexpr int kGroupMaxRank = 64;
+
+// -------------------------------------------------------------- planned decode
+// Plan of a segment table (int32 words; the layout callers see in
+// include/mlora_hip.h).  Header: [0] entries, [1] rows planned, [2] entry
+// capacity.  Entry: slot, rank, scaling (fp32 bits), row count (1..16),
+// workspace position of its first row, then 16 row numbers (unused ones
+// repeat the first).
+constexpr int kPlanHeaderWords = MLORA_PLAN_HEADER_WORDS;
+constexpr int kPlanEntryWords = MLORA_PLAN_ENTRY_WORDS;
+constexpr int kPlanRows = MLORA_PLAN_ROWS;
+constexpr int kPlanSlot = 0;
+constexpr int kPlanRank = 1;
+constexpr int kPlanScale = 2;
+constexpr int kPlanRowCount = 3;
+constexpr int kPlanPos = 4;
+constexpr int kPlanRowWord = MLORA_PLAN_ROW_WORD;
+// Pools of up to this many slots get their plan built on the device when
+// the caller passes none (LDS tables of the builder).
+constexpr int kPlanBuildMaxSlots = 2048;
+
+// Workspace of the planned decode: a header of int32 words, the chunk
+// flags (64-bit) and the fp32 K-chunk sums, each region 256-byte aligned,
+// then a plan region used when the caller passes no plan.
+constexpr size_t kWsHeaderBytes = 256;
+constexpr int kWsFallbacks = MLORA_WS_FALLBACKS;       // chunks an expand item computed itself
+constexpr int kWsWaitOverride = MLORA_WS_WAIT_TICKS;   // wait limit in 10 ns ticks: 0 default, < 0 none
+constexpr int kWsPlanErrors = MLORA_WS_PLAN_ERRORS;    // entries the call could not take
+// Buffer resource word 3 for raw buffer loads on gfx9 (data format 32 bit).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+struct DecodeArgs {
+  const void* x;
+  int64_t x_stride;
+  int rows;
+  int in_dim;
+  SliceView slices[kMaxSlices];
+  int n_slices;
+  int r_max;
+  void* out;
+  int64_t out_stride;
+  int num_slots;     // slots of the call's stacks (entries of other slots are skipped)
+  int kc;            // K chunks
+  int k_chunk;       // reduction elements per chunk
+  int s_groups;      // shrink items per (entry, chunk): 1 (all slices) or n_slices (one each)
+  int n_tiles;       // expand items per entry (256-column tiles over all slices)
+  int tile_base[kMaxSlices + 1];
+  int e_grid;        // entries per row of the grid (multiple of 8)
+  int e_cap;         // entries the workspace flags hold
+  int plan_cap;      // entries the plan holds
+  int ws_rows;       // rows the workspace sums hold
+  int* header;
+  uint64_t* flags;   // [plan_cap][s_groups][kc] {launch tag, XCC id}
+  float* partials;   // [ws_rows][kc][n_slices * r_max]
+};
+
+// Shape check and plan of the work: K chunks, A blocks per shrink item,
+// shrink items per chunk, and the workspace regions.
+struct DecodeShape {
+  int kc, k_chunk, nbt, s_groups;
+  size_t flags_off, partials_off, plan_off, bytes;
+  int e_cap;
+};
+bool plan_decode(int in_dim, int r_max, int n_slices, int rows, int dtype, DecodeShape* sh);
+hipError_t launch_planned(const int32_t* plan, const DecodeArgs& args, int dtype, int nbt, int mode, int phases,
+                          hipStream_t stream);
+hipError_t launch_build_plan(const SegView& m, int rows, int32_t* plan, int cap, hipStream_t stream);
 
 // ------------------------------------------------------ mixed-batch expand
 // Segments of at most this many rows are "short" (decode-like) in a mixed
@@ -162,12 +223,6 @@ constexpr int kMixedMaxSlots = 2048;
 // exit.
 hipError_t launch_mixed(const ExpandArgs& args, int dtype, int long_units, int short_units, hipStream_t stream);
 
-// Shape check and plan.  Workspaces: linked_bytes for the single launch
-// (header + tagged words, also used by the auto mode whichever schedule it
-// picks), plain_bytes for two launches (fp32 sums).
-bool plan_grouped(int in_dim, int r_max, int n_slices, int rows, int dtype, int* kc, int* k_chunk, int* nbt,
-                  int* s_groups, size_t* linked_bytes, size_t* plain_bytes);
-hipError_t launch_grouped(GroupedArgs args, int dtype, int nbt, int mode, int phases, hipStream_t stream);
 
 // -------------------------------------------------------------- rmsnorm
 struct RmsArgs {

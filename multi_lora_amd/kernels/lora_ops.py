@@ -49,12 +49,14 @@ class Workspace:
 
 
 class LinkedWorkspace:
-    """Workspaces of the single-launch grouped path, one per stream.
+    """Workspaces of the grouped (decode) path, one per stream.
 
-    Each buffer is zero-filled on allocation and used by nothing else: the
-    kernel tags the words it publishes with the launch's dispatch id on its
-    hardware queue, which keeps launches on one stream apart without ever
-    clearing the buffer; launches on different streams get separate buffers.
+    Each buffer is zero-filled on allocation and used by nothing else.  The
+    single launch tags the flags its work items publish with the launch's
+    dispatch id on its hardware queue, which keeps launches on one stream
+    apart without ever clearing the buffer; launches on different streams
+    get separate buffers.  Its header words count K chunks that a work item
+    computed itself after a wait gave up, and plan errors.
     """
 
     def __init__(self) -> None:
@@ -67,11 +69,22 @@ class LinkedWorkspace:
             buf = self.bufs[key] = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         return buf.data_ptr(), buf.numel()
 
-    def error_word(self) -> int:
-        """Sticky error word over all buffers (synchronises): non-zero once a
-        wait between work items of some launch timed out, after which that
-        launch's results are not trustworthy."""
-        return max((int(b[:4].view(torch.int32).item()) for b in self.bufs.values()), default=0)
+    def counters(self) -> Tuple[int, int]:
+        """(chunks computed after a wait gave up, plan errors) summed over all
+        buffers (synchronises).  The first only costs time; the second means a
+        table's plan did not fit the call and should stay 0."""
+        fb = pe = 0
+        for b in self.bufs.values():
+            h = b[:16].view(torch.int32).cpu()
+            fb += int(h[_ffi.WS_FALLBACKS])
+            pe += int(h[_ffi.WS_PLAN_ERRORS])
+        return fb, pe
+
+    def set_wait_ticks(self, ticks: int) -> None:
+        """Set the wait limit of every buffer (10 ns ticks; 0 = library default;
+        negative = no wait: every expand item computes every K chunk itself)."""
+        for b in self.bufs.values():
+            b[4 * _ffi.WS_WAIT_TICKS:4 * _ffi.WS_WAIT_TICKS + 4].view(torch.int32).fill_(int(ticks))
 
 
 def _default_workspace(device: torch.device, linked: bool = False) -> Workspace:
@@ -116,6 +129,9 @@ def seg_meta(meta: KernelInputMetaData, device: torch.device, num_slots: int) ->
     n_slots = min(ranks.numel(), int(num_slots))
     summary = getattr(meta, "table_summary", None)
     long_segs, long_rows, short_slots = summary(n_slots) if summary is not None else (-1, -1, -1)
+    plan = getattr(meta, "plan", None)
+    if plan is not None and (plan.device != device or plan.dtype != torch.int32):
+        plan = None
     m = _ffi.SegMeta(
         indptr.data_ptr(),
         widx.data_ptr(),
@@ -128,8 +144,11 @@ def seg_meta(meta: KernelInputMetaData, device: torch.device, num_slots: int) ->
         long_segs,
         long_rows,
         short_slots,
+        plan.data_ptr() if plan is not None else None,
+        int(meta.plan_cap) if plan is not None else 0,
+        int(meta.plan_entries) if plan is not None else -1,
     )
-    return m, [indptr, widx, ranks, scal]
+    return m, [indptr, widx, ranks, scal, plan]
 
 
 def _slices(a_stacks: Sequence[Optional[torch.Tensor]], b_stacks: Sequence[Optional[torch.Tensor]],
@@ -231,14 +250,14 @@ GROUPED_MAX_LEN = 16
 
 def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],
                   meta: KernelInputMetaData, out: torch.Tensor, out_cols: Sequence[int],
-                  workspace: Optional[Workspace] = None, phases: int = 3, mode: int = 0,
-                  linked_workspace: Optional[LinkedWorkspace] = None) -> bool:
+                  workspace: Optional[LinkedWorkspace] = None, phases: int = 3, mode: int = 0) -> bool:
     """Slot-grouped shrink+expand into ``out``; returns False (nothing launched) if the shape is not eligible.
 
-    ``mode`` 1 = single launch (shrink and expand work items linked through
-    ``linked_workspace``), 2 = two launches (sums through ``workspace``),
-    0 = the library's choice (the single launch).  With two launches,
-    ``phases`` 1 / 2 run only the shrink / expand half; 3 runs both.
+    Work follows the table's plan (``meta.plan``; built on the device when
+    the table has none).  ``mode`` 1 = single launch, 2 = two launches,
+    0 = the library's choice (the single launch while its work items fit on
+    the chip about at once); all give bit-identical results.  With two launches, ``phases`` 1 / 2 run only the shrink /
+    expand half; 3 runs both.  ``workspace`` holds one buffer per stream.
     """
     _require_gpu(x, "x")
     dev = x.device
@@ -266,10 +285,7 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
     if need == 0:
         return False
     stream = _ffi.stream_ptr(dev)
-    if mode == 2:
-        ws_ptr, ws_bytes = (workspace or _default_workspace(dev)).get(need, dev)
-    else:
-        ws_ptr, ws_bytes = (linked_workspace or _default_workspace(dev, linked=True)).get(need, dev, stream or 0)
+    ws_ptr, ws_bytes = (workspace or _default_workspace(dev, linked=True)).get(need, dev, stream or 0)
     sl = _slices(a_stacks, b_stacks, out_cols)
     rc = lib.mlora_apply_grouped(
         x.data_ptr(), x.stride(0), x.shape[0], in_dim, sl, n, r_max, out.data_ptr(), out.stride(0), ctypes.byref(m),
@@ -280,6 +296,22 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
         return False
     _ffi.check(rc, "mlora_apply_grouped")
     return True
+
+
+def build_plan_device(meta: KernelInputMetaData, num_rows: int, num_slots: int, cap: Optional[int] = None) -> torch.Tensor:
+    """The table's plan built on the device (``mlora_build_plan``) into a new int32 tensor."""
+    dev = meta.seg_indptr.device
+    _require_gpu(meta.seg_indptr, "metadata")
+    cap = int(num_rows) if cap is None else int(cap)
+    lib = _ffi.lib()
+    words = lib.mlora_plan_bytes(max(cap, 1)) // 4
+    plan = torch.zeros(words, dtype=torch.int32, device=dev)
+    m, keep = seg_meta(meta, dev, num_slots)
+    m.plan, m.plan_cap, m.plan_entries = None, 0, -1
+    rc = lib.mlora_build_plan(ctypes.byref(m), int(num_rows), plan.data_ptr(), max(cap, 1), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "mlora_build_plan")
+    del keep
+    return plan
 
 
 def apply_segments(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],

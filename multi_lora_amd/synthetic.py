@@ -23,9 +23,10 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import List, Optional
 
+import numpy as np
 import torch
 
-from .batch_info import KernelInputMetaData
+from .batch_info import KernelInputMetaData, build_plan, plan_words
 
 
 @dataclass
@@ -52,9 +53,10 @@ class LoRAWorkload:
 
 
 def make_meta(seg_lens: List[int], seg_slots: List[int], slot_ranks: List[int], scalings: List[float],
-              device, scal_dtype: torch.dtype, host_copies: bool = True) -> KernelInputMetaData:
+              device, scal_dtype: torch.dtype, host_copies: bool = True, with_plan: bool = True) -> KernelInputMetaData:
     """A segment table on ``device``; ``host_copies`` keeps the host lists for
-    the table summary, as write_kernel_input_metadata does."""
+    the table summary, and ``with_plan`` attaches the table's plan, as
+    write_kernel_input_metadata does."""
     indptr = [0]
     for n in seg_lens:
         indptr.append(indptr[-1] + n)
@@ -70,7 +72,22 @@ def make_meta(seg_lens: List[int], seg_slots: List[int], slot_ranks: List[int], 
     )
     if host_copies:
         meta.set_host_copies(seg_lens, seg_slots)
+    if with_plan and dev.type == "cuda":
+        attach_plan(meta, indptr, seg_slots, slot_ranks, scalings, scal_dtype)
     return meta
+
+
+def attach_plan(meta: KernelInputMetaData, indptr, seg_slots, slot_ranks, scalings, scal_dtype) -> None:
+    """Build the table's plan on the host and attach it (a device tensor) to ``meta``."""
+    n_slots = len(slot_ranks)
+    rows = int(indptr[-1]) if len(indptr) else 0
+    cap = max(1, len(seg_slots) + min(len(seg_slots), n_slots))
+    words = np.zeros(plan_words(cap), dtype=np.int32)
+    scal_f32 = torch.tensor(scalings, dtype=scal_dtype).float().numpy()
+    n = build_plan(indptr, seg_slots, slot_ranks, scal_f32, n_slots, rows, words)
+    meta.plan = torch.from_numpy(words).to(meta.seg_indptr.device)
+    meta.plan_cap = cap
+    meta.plan_entries = n
 
 
 def _normal(g: torch.Generator, shape, std: float, mean: float = 0.0) -> torch.Tensor:
@@ -126,14 +143,28 @@ def cpu_small(device="cpu", dtype=torch.float32) -> LoRAWorkload:
 
 
 def decode_q(device="cpu", dtype=torch.bfloat16, tokens: int = 128, in_dim: int = 4096, out: int = 4096,
-             n_slots: int = 64, n_adapters: int = 32, rank: int = 16, seed: int = 1) -> LoRAWorkload:
+             n_slots: int = 64, n_adapters: int = 32, rank: int = 16, seed: int = 1,
+             resident: Optional[int] = None) -> LoRAWorkload:
+    """Decode tokens, one segment each, over ``n_adapters`` adapters of a pool of ``n_slots``.
+
+    By default the adapters occupy slots 0..n_adapters-1 and the other slots
+    are empty (rank 0).  With ``resident`` > n_adapters, slots
+    0..resident-1 all hold adapters (as a pool in steady state does) and the
+    tokens use a random ``n_adapters`` of them.
+    """
     g = torch.Generator("cpu").manual_seed(seed)
     seg_slots = torch.randint(0, n_adapters, (tokens,), generator=g).tolist()
+    resident = n_adapters if resident is None else resident
+    name = "decode_q"
+    if resident > n_adapters:
+        used = torch.randperm(resident, generator=g)[:n_adapters].tolist()
+        seg_slots = [used[s] for s in seg_slots]
+        name = "decode_q_resident"
     seg_lens = [1] * tokens
-    ranks = [rank] * n_adapters + [0] * (n_slots - n_adapters)
+    ranks = [rank] * resident + [0] * (n_slots - resident)
     x = _normal(g, (tokens, in_dim), 1.0)
     a, b = _stacks(g, n_slots, ranks, rank, in_dim, [out], in_dim ** -0.5, 0.02)
-    return _finish("decode_q", g, seg_lens, seg_slots, ranks, [2.0] * n_slots, x, a, b, out, dtype, device, [0])
+    return _finish(name, g, seg_lens, seg_slots, ranks, [2.0] * n_slots, x, a, b, out, dtype, device, [0])
 
 
 def prefill_mlp(device="cpu", dtype=torch.bfloat16, part: str = "gate_up", n_seg: int = 8, min_len: int = 64,

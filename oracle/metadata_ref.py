@@ -7,7 +7,13 @@ Follows multi_lora/batch_info.py:45-179 in behaviour, written independently:
 * ``resident_columns``   — what each resident column holds after an in-place
                            rewrite, padding included (batch_info.py:169-178);
 * ``token_slots``        — slot of every token: ``repeat_interleave(weight_indices, seg_lens)``;
-* ``slot_gather_order``  — tokens grouped by slot, stable within a slot.
+* ``slot_gather_order``  — tokens grouped by slot, stable within a slot;
+* ``plan_ref``           — the per-table plan the decode kernels follow
+                           (include/mlora_hip.h, MLORA_PLAN_*): the gather
+                           order cut into entries of 16 rows.  It has no
+                           counterpart in the reference; it regroups
+                           ``slot_gather_order``, which the reference's
+                           batch metadata implies (batch_info.py:128-179).
 """
 
 from __future__ import annotations
@@ -77,3 +83,39 @@ def slot_gather_order(
         tokens.extend(per_slot[slot])
         offsets.append(len(tokens))
     return slots, offsets, tokens
+
+
+PLAN_HEADER_WORDS, PLAN_ENTRY_WORDS, PLAN_ROWS, PLAN_ROW_WORD = 16, 32, 16, 8
+
+
+def plan_ref(indptr: Sequence[int], weight_indices: Sequence[int], lora_ranks: Sequence[int],
+             scal_bits: Sequence[int], num_slots: int, rows: int, cap: int) -> List[int]:
+    """The plan's int32 words for a table, by plain loops.
+
+    Segment bounds are clamped to ``[0, rows)``; slots outside
+    ``[0, num_slots)`` and rank-0 slots get no entry.  ``scal_bits``: each
+    slot's scaling as fp32 bit patterns (int).  Entries past ``cap`` are not
+    written, but the header counts them.
+    """
+    bs = len(weight_indices)
+    cl = [min(max(int(v), 0), rows) for v in indptr]
+    ranks = [int(r) for r in lora_ranks[:num_slots]]
+    slots, offsets, tokens = slot_gather_order(cl, weight_indices, ranks, bs)
+    words = [0] * (PLAN_HEADER_WORDS + cap * PLAN_ENTRY_WORDS)
+    e = 0
+    for g, slot in enumerate(slots):
+        mine = tokens[offsets[g]:offsets[g + 1]]
+        for k in range(0, len(mine), PLAN_ROWS):
+            part = mine[k:k + PLAN_ROWS]
+            if e < cap:
+                base = PLAN_HEADER_WORDS + e * PLAN_ENTRY_WORDS
+                words[base + 0] = slot
+                words[base + 1] = ranks[slot]
+                words[base + 2] = int(scal_bits[slot])
+                words[base + 3] = len(part)
+                words[base + 4] = offsets[g] + k
+                for i in range(PLAN_ROWS):
+                    words[base + PLAN_ROW_WORD + i] = part[i] if i < len(part) else part[0]
+            e += 1
+    words[0], words[1], words[2] = e, len(tokens), cap
+    return words

@@ -102,26 +102,76 @@ def test_errors_map_to_reference_exception_types():
         _ffi.check(rc, "mlora_expand")
 
 
+def _r256(b):
+    return (b + 255) // 256 * 256
+
+
 def test_grouped_workspace_sizes():
-    """Workspace sizes are host arithmetic: K chunks of 256 x rows x columns,
-    fp32 for two launches; 64-bit words plus a 256-byte header for the single
-    launch; for the library's choice both, the fp32 region starting at the
-    next 256-byte boundary after the words; 0 for ineligible shapes."""
+    """Workspace sizes are host arithmetic, the same for every mode: a
+    256-byte header, a 64-bit flag per (entry, slice group, 256-wide K chunk)
+    for up to `rows` entries, fp32 sums per (row, chunk, column), and a plan
+    of `rows` entries; 0 for ineligible shapes."""
     lib = _ffi.lib()
     bf = _ffi.MLORA_BF16
-    kc = 4096 // 256
-    two = lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 2)
-    assert two == kc * 128 * 16 * 4
-    one = lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 1)
-    assert one == 256 + kc * 128 * 16 * 8
-    # auto mode: the single-launch layout, then the two-launch region
-    assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 0) == (one + 255) // 256 * 256 + two
-    assert lib.mlora_grouped_workspace_bytes(4104, 16, 3, 10, 65, bf, 1) == 256 + 17 * 10 * 48 * 8
+
+    def want(in_dim, r_max, n, rows):
+        kc = -(-in_dim // 256)
+        groups = n if n * -(-r_max // 16) > 4 else 1
+        return 256 + _r256(rows * groups * kc * 8) + _r256(rows * kc * n * r_max * 4) + 4 * (16 + 32 * rows)
+
+    for mode in (0, 1, 2):
+        assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, mode) == want(4096, 16, 1, 128) == 164160
+    assert lib.mlora_grouped_workspace_bytes(4104, 16, 3, 10, 65, bf, 1) == want(4104, 16, 3, 10)
+    assert lib.mlora_grouped_workspace_bytes(4096, 32, 3, 256, 256, bf, 0) == want(4096, 32, 3, 256)  # per-slice items
+    assert lib.mlora_grouped_workspace_bytes(16384, 16, 1, 8, 8, bf, 1) == want(16384, 16, 1, 8)       # 64 chunks
+    assert lib.mlora_grouped_workspace_bytes(16392, 16, 1, 8, 8, bf, 1) == 0                          # 65 chunks
     assert lib.mlora_grouped_workspace_bytes(4100, 16, 1, 10, 65, bf, 1) == 0                # in_dim % 8
     assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, _ffi.MLORA_F32, 1) == 0   # fp32 not grouped
     assert lib.mlora_grouped_workspace_bytes(4096, 72, 1, 128, 64, bf, 1) == 0               # r_max > 64
     assert lib.mlora_grouped_workspace_bytes(4096, 12, 1, 128, 64, bf, 2) == 0               # r_max % 8
     assert lib.mlora_grouped_workspace_bytes(4096, 16, 1, 128, 64, bf, 3) == 0               # bad mode
+    assert lib.mlora_plan_bytes(10) == 4 * (16 + 32 * 10)
+
+
+def test_plan_layout_matches_the_header():
+    """The plan and workspace-header constants the host uses are the ones include/mlora_hip.h defines."""
+    import re
+    from pathlib import Path
+
+    from multi_lora_amd import batch_info
+
+    text = (Path(__file__).resolve().parents[1] / "include" / "mlora_hip.h").read_text()
+    defs = {k: int(v) for k, v in re.findall(r"#define (MLORA_(?:PLAN|WS)_\w+) (\d+)", text)}
+    assert defs["MLORA_PLAN_HEADER_WORDS"] == _ffi.PLAN_HEADER_WORDS == batch_info.PLAN_HEADER_WORDS
+    assert defs["MLORA_PLAN_ENTRY_WORDS"] == _ffi.PLAN_ENTRY_WORDS == batch_info.PLAN_ENTRY_WORDS
+    assert defs["MLORA_PLAN_ROWS"] == _ffi.PLAN_ROWS == batch_info.PLAN_ROWS
+    assert defs["MLORA_PLAN_ROW_WORD"] == _ffi.PLAN_ROW_WORD == batch_info.PLAN_ROW_WORD
+    assert defs["MLORA_WS_FALLBACKS"] == _ffi.WS_FALLBACKS
+    assert defs["MLORA_WS_WAIT_TICKS"] == _ffi.WS_WAIT_TICKS
+    assert defs["MLORA_WS_PLAN_ERRORS"] == _ffi.WS_PLAN_ERRORS
+
+
+def test_grouped_rejects_bad_plans_and_missing_room():
+    lib = _ffi.lib()
+    sl = _ffi.SliceArray()
+    sl[0] = _ffi.Slice(1 << 20, 16 * 64, 64, 2 << 20, 64 * 16, 16, 64, 0)
+    # a plan pointer with no capacity
+    bad = _ffi.SegMeta(256, 512, 768, 1024, 4, 1, 8, _ffi.MLORA_BF16, -1, -1, -1, 4096, 0, -1)
+    rc = lib.mlora_apply_grouped(4096, 64, 4, 64, sl, 1, 16, 8192, 64, ctypes.byref(bad), _ffi.MLORA_BF16,
+                                 3 << 20, 1 << 20, 1, 3, None)
+    assert rc < 0 and b"capacity" in lib.mlora_last_error()
+    # no plan and a pool larger than the device plan builder takes
+    big = _ffi.SegMeta(256, 512, 768, 1024, 4, 1, 4096, _ffi.MLORA_BF16, -1, -1, -1, None, 0, -1)
+    rc = lib.mlora_apply_grouped(4096, 64, 4, 64, sl, 1, 16, 8192, 64, ctypes.byref(big), _ffi.MLORA_BF16,
+                                 3 << 20, 1 << 20, 1, 3, None)
+    assert rc == -2 and b"device builder" in lib.mlora_last_error()
+    rc = lib.mlora_build_plan(ctypes.byref(big), 4, 4096, 8, None)
+    assert rc == -2
+    # workspace too small
+    ok = _ffi.SegMeta(256, 512, 768, 1024, 4, 1, 8, _ffi.MLORA_BF16, -1, -1, -1, 4096, 8, 1)
+    rc = lib.mlora_apply_grouped(4096, 64, 4, 64, sl, 1, 16, 8192, 64, ctypes.byref(ok), _ffi.MLORA_BF16,
+                                 3 << 20, 16, 1, 3, None)
+    assert rc == -3
 
 
 def test_pool_key_struct_layout():

@@ -3,7 +3,9 @@
 The five device columns must equal, bit for bit, what the column-by-column
 path writes on the CPU (itself pinned to the reference's padding rules in
 test_oracle_known_answers.py), keep their addresses while the capacity holds
-the batch, and drive a captured graph correctly after each rewrite.
+the batch, and drive a captured graph correctly after each rewrite.  The
+table's plan, built on the host and packed with the columns, must equal the
+plan the device builder makes of the same table.
 """
 
 import random
@@ -14,6 +16,7 @@ import torch
 from multi_lora_amd import HipLoRABackend, synthetic
 from multi_lora_amd.batch_info import (BatchLoRAInfo, empty_kernel_input_metadata,
                                        write_kernel_input_metadata)
+from multi_lora_amd.kernels.lora_ops import build_plan_device
 
 pytestmark = pytest.mark.gpu
 
@@ -24,6 +27,10 @@ def random_batch(rng, rows, k):
     return BatchLoRAInfo(weight_indices=[rng.randrange(k) for _ in range(rows)],
                          lora_ranks=[rng.choice([0, 8, 16]) for _ in range(k)],
                          scalings=[rng.choice([0.0, 0.5, 2.0]) for _ in range(k)])
+
+
+def pb_rows(meta):
+    return meta.bs
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -52,6 +59,12 @@ def test_packed_columns_match_cpu_path_and_keep_addresses(dev, dtype):
             assert torch.equal(g[:n], h[:n]), c
             if c in ("lora_ranks", "scalings"):
                 assert g.shape == h.shape
+        # The plan packed with the table equals the device builder's plan of the same table.
+        assert gmeta.plan is not None and gmeta.plan_entries >= 0
+        total = int(cmeta.seg_indptr[pb_rows(cmeta)].item())
+        used = 16 + 32 * min(gmeta.plan_entries, gmeta.plan_cap)
+        built = build_plan_device(gmeta, total, k, gmeta.plan_cap).cpu()
+        assert torch.equal(gmeta.plan.cpu()[:used], built[:used])
 
 
 def test_graph_replay_follows_packed_rewrites(dev):

@@ -42,6 +42,13 @@ def case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, seed):
     ("long", [150, 200, 130], [0, 1, 0], [16, 32], 4096, [1024, 256], 32, torch.bfloat16),
     ("fp32", [20, 1, 33], [0, 1, 0], [8, 16], 1024, [256], 16, torch.float32),
     ("short_k", [30, 2, 17], [1, 0, 1], [16, 16], 64, [128], 16, torch.bfloat16),
+    # r_max % 8 == 4 with split K: the expand's y tile is a chunk wider than
+    # r_max, and the chunk's tail must not reach the MFMA unmasked
+    ("rmax4_split", [1] * 24 + [3], [i % 5 for i in range(25)], [4, 4, 0, 3, 4], 4096, [512], 4, torch.bfloat16),
+    ("rmax4_split_f16", [2] * 20, [i % 3 for i in range(20)], [4, 2, 4], 4096, [264], 4, torch.float16),
+    ("rmax12_split", [1] * 30, [i % 6 for i in range(30)], [12, 12, 7, 0, 12, 5], 4096, [640], 12, torch.float16),
+    ("rmax12_mixed_bf16", [40] + [1] * 20 + [33], [0] + [i % 4 for i in range(20)] + [2], [12, 9, 12, 4], 4096,
+     [512, 256], 12, torch.bfloat16),
 ])
 def test_one_call_equals_two_calls(dev, name, lens, slots, ranks, in_dim, outs, r_max, dtype):
     x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, len(name))
@@ -52,7 +59,30 @@ def test_one_call_equals_two_calls(dev, name, lens, slots, ranks, in_dim, outs, 
     apply_segments(xd, Ad, Bd, meta, one, cols, workspace=Workspace())
     torch.cuda.synchronize()
     assert torch.equal(one.cpu(), two), f"{name}: one-call result differs from shrink + expand"
+    assert not torch.isnan(one).any().item(), name
     assert_tol_f64(one.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), name)
+
+
+@pytest.mark.parametrize("r_max", [4, 12])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_backend_decode_at_rank_widths_the_grouped_path_refuses(dev, r_max, dtype):
+    """Decode batches whose r_max is not a multiple of 8 go to the one-call
+    segment path; at in_dim 4096 its expand adds the split sums itself.
+    The result has no NaN, equals shrink + expand and matches float64."""
+    lens = [1] * 40
+    slots = [(7 * i) % 6 for i in range(40)]
+    ranks = [r_max, r_max - 1, 0, r_max, 2, r_max]
+    x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens, slots, ranks, 4096, [1024], r_max, dtype, r_max)
+    meta = make_meta(lens, slots, ranks, scal, dev, dtype)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(meta)
+    got = be.apply_lora(xd, Ad[0], Bd[0], base.to(dev).clone())
+    _, two = run_hip(xd, Ad, Bd, meta, base.to(dev), cols)
+    torch.cuda.synchronize()
+    assert not torch.isnan(got).any().item()
+    assert torch.equal(got.cpu(), two)
+    assert_tol_f64(got.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), f"r_max {r_max}")
 
 
 def test_backend_mixed_batch_uses_one_call_and_replays_in_a_graph(dev):

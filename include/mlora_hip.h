@@ -226,6 +226,21 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
                         int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
                         size_t workspace_bytes, int32_t mode, int32_t phases, void* stream);
 
+/* mlora_apply_grouped without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it); no counterpart in the reference.  The library
+ * keeps its own workspace, MLORA_STATIC_SCRATCH_BYTES of device memory per
+ * GPU held for the life of the process; a shape that needs more (see
+ * mlora_grouped_workspace_bytes) returns -3 with nothing launched.  The
+ * call allocates nothing.  Every call on one GPU shares that workspace:
+ * calls that overlap in time on one GPU (on different streams) race, and
+ * must not be made.  Arguments and results are those of mlora_apply_grouped. */
+#define MLORA_STATIC_SCRATCH_BYTES (16 << 20)
+int mlora_apply_grouped_static(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                               const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                               int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, int32_t mode,
+                               int32_t phases, void* stream);
+
 /* Bytes of a plan with room for `entries_cap` entries. */
 size_t mlora_plan_bytes(int32_t entries_cap);
 

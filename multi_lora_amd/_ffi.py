@@ -40,7 +40,11 @@ EXPORTS = (
     "mlora_add_rmsnorm",
     "mlora_plan_bytes",
     "mlora_build_plan",
+    "mlora_apply_grouped_static",
 )
+
+# include/mlora_hip.h: MLORA_STATIC_SCRATCH_BYTES
+STATIC_SCRATCH_BYTES = 16 << 20
 
 # Plan layout (include/mlora_hip.h: MLORA_PLAN_*) and workspace header words
 # of mlora_apply_grouped (MLORA_WS_*).
@@ -154,6 +158,11 @@ _SIGNATURES = {
         [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
     ),
     "mlora_plan_bytes": (_sz, [_i32]),
+    "mlora_apply_grouped_static": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _i32, ctypes.POINTER(Slice), _i32, _i32, _vp, _i64, ctypes.POINTER(SegMeta), _i32, _i32,
+         _i32, _vp],
+    ),
     "mlora_build_plan": (ctypes.c_int, [ctypes.POINTER(SegMeta), _i32, _vp, _i32, _vp]),
 }
 

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "kernels.h"
 
@@ -333,11 +334,12 @@ int mlora_build_plan(const mlora_seg_meta* meta, int32_t num_rows, int32_t* plan
   return 0;
 }
 
-int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
-                        const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
-                        int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
-                        size_t workspace_bytes, int32_t mode, int32_t phases, void* stream) {
-  g_err[0] = '\0';
+// mlora_apply_grouped on a given workspace (the caller's, or the static
+// scratch of mlora_apply_grouped_static).
+static int apply_grouped_impl(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                              const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                              int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                              size_t workspace_bytes, int32_t mode, int32_t phases, void* stream) {
   if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
   if (int rc = check_meta(meta)) return rc;
   if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
@@ -436,6 +438,76 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   const hipError_t e = mlora::launch_planned(plan, args, dtype, sh.nbt, m, phases, st);
   if (e != hipSuccess) return hip_fail(e, "grouped launch");
   return 0;
+}
+
+int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                        const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                        int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                        size_t workspace_bytes, int32_t mode, int32_t phases, void* stream) {
+  g_err[0] = '\0';
+  return apply_grouped_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, out, out_row_stride, meta,
+                            dtype, workspace, workspace_bytes, mode, phases, stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ static scratch
+// Workspace of mlora_apply_grouped_static: device memory the library holds
+// for the life of the process, one copy per GPU (zero at load, which is
+// what the launch-tagged flags need; never cleared afterwards).
+static __device__ __align__(256) unsigned char scratch[MLORA_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the host-side name is only a stand-in).  nullptr on failure, with
+// the error text set.
+void* scratch_ptr() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    hip_fail(e, "hipGetDevice");
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(kUnsupported, "device %d beyond the %d the static scratch serves", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlora_apply_grouped_static(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                               const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                               int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, int32_t mode,
+                               int32_t phases, void* stream) {
+  g_err[0] = '\0';
+  const size_t need = mlora_grouped_workspace_bytes(in_dim, r_max, n_slices, num_rows, meta ? meta->num_slots : 0,
+                                                    dtype, mode);
+  if (need > MLORA_STATIC_SCRATCH_BYTES)
+    return fail(kWorkspace, "shape needs %zu bytes of workspace, more than the %d of the static scratch", need,
+                MLORA_STATIC_SCRATCH_BYTES);
+  void* ws = scratch_ptr();
+  if (ws == nullptr) return kUnsupported;
+  return apply_grouped_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, out, out_row_stride, meta,
+                            dtype, ws, MLORA_STATIC_SCRATCH_BYTES, mode, phases, stream);
 }
 
 }  // extern "C"

@@ -187,3 +187,20 @@ def test_pool_scatter_rejects_bad_arguments():
     assert lib.mlora_pool_scatter(None, 16, 1, None, None, 1, 2, 4, 16, 7, None) < 0                 # dtype
     assert lib.mlora_pool_scatter(None, 16, 1, None, None, 1, 2, 4, 16, _ffi.MLORA_BF16, None) < 0   # null stage
     assert lib.mlora_pool_scatter(None, 16, 0, None, None, 1, 2, 4, 16, _ffi.MLORA_BF16, None) == 0  # nothing to do
+
+
+def test_static_grouped_rejects_shapes_beyond_its_scratch():
+    """The no-allocation entry point refuses a shape whose workspace exceeds
+    its static scratch, before any HIP call, and the header's limit is the
+    one the binding knows."""
+    text = (ROOT / "include" / "mlora_hip.h").read_text()
+    m = re.search(r"#define MLORA_STATIC_SCRATCH_BYTES \((\d+) << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _ffi.STATIC_SCRATCH_BYTES
+    lib = _ffi.lib()
+    sl = _ffi.SliceArray()
+    meta = _ffi.SegMeta(256, 512, 768, 1024, 4, 1, 8, _ffi.MLORA_BF16, -1, -1, -1, None, 0, -1)
+    need = lib.mlora_grouped_workspace_bytes(16384, 64, 3, 4096, 8, _ffi.MLORA_BF16, 0)
+    assert need > _ffi.STATIC_SCRATCH_BYTES
+    rc = lib.mlora_apply_grouped_static(4096, 16384, 4096, 16384, sl, 3, 64, 8192, 16384, ctypes.byref(meta),
+                                        _ffi.MLORA_BF16, 0, 3, None)
+    assert rc == -3 and b"static scratch" in lib.mlora_last_error()

@@ -47,10 +47,11 @@ def parse():
     ap.add_argument("--workload", choices=("decode_q",) + tuple(OTHER_WORKLOADS), default="decode_q",
                     help="decode_q is the headline; the others print a line of the same form for their shape")
     ap.add_argument("--profile-traffic", action="store_true",
-                    help="launch only the planned decode kernel of --workload (decode_q, decode_q_resident or "
-                         "decode_qkv) and a copy kernel of known size, for rocprofv3 --pmc runs")
-    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="turn rocprofv3 FETCH_SIZE / WRITE_SIZE runs of --profile-traffic into the traffic file")
+                    help="run only the LoRA path of --workload (a decode or prefill workload) and a copy kernel "
+                         "of known size, for rocprofv3 --pmc runs")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
+                    help="FETCH_SIZE and WRITE_SIZE run directories of --profile-traffic (and optionally an MFMA "
+                         "counter run's) -> the workload's counter summary under profiles/")
     ap.add_argument("--regions", type=int, default=0,
                     help="timed regions of exactly --steps steps each (default: enough for ~2000 steps, 5..101); "
                          "the step time is their median")
@@ -318,6 +319,27 @@ def bench_pool_upload(args) -> int:
     return 0
 
 
+def time_calls(torch, fn, k: int, per_graph: int, stream) -> float:
+    """Milliseconds per call over exactly ``k`` calls of ``fn``: graphs of
+    ``per_graph`` calls replayed back to back, then one graph of the rest."""
+    full, rem = divmod(k, per_graph)
+    g_full = capture(torch, fn, per_graph) if full else None
+    g_rem = capture(torch, fn, rem) if rem else None
+    for g in (g_full, g_rem):
+        if g is not None:
+            g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(full):
+        g_full.replay()
+    if g_rem is not None:
+        g_rem.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / k
+
+
 def time_graph(torch, g, calls: int, per_graph: int, stream) -> float:
     """Milliseconds per call of a graph holding `per_graph` calls, replayed back to back."""
     replays = max(1, calls // per_graph)
@@ -421,11 +443,17 @@ def bench_other(args) -> int:
 
         total_bytes = lora_bytes + norm_bytes
         add_bytes = 4 * S * in_dim * e + in_dim * e
-        parts = {"rmsnorm": (norm, norm_bytes), "planned decode (3 slices, one launch)": (lora, lora_bytes),
+        def lora_one(i):
+            _, a, b, out = reps[i % n_rep]
+            assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.linked_workspace, mode=1)
+
+        parts = {"rmsnorm": (norm, norm_bytes),
+                 "planned decode (3 slices, the library's choice of schedule)": (lora, lora_bytes),
+                 "planned decode, one launch (schedule comparison)": (lora_one, lora_bytes),
                  "planned decode, two launches (schedule comparison)": (lora_two, lora_bytes),
                  "add_rmsnorm fused (schedule comparison)": (add_norm, add_bytes),
                  "add then rmsnorm, unfused (schedule comparison)": (add_then_norm, add_bytes)}
-        path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-planned decode, one launch)"
+        path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-planned decode, the library's schedule)"
     elif name in GROUPED_WORKLOADS:
         def lora(i):
             x, a, b, out = reps[i % n_rep]
@@ -440,9 +468,9 @@ def bench_other(args) -> int:
             be.apply_lora_multi(x, a, b, out, cols)
 
         total_bytes = lora_bytes
-        parts = {"planned decode (one launch)": (lora, lora_bytes),
+        parts = {"planned decode (the library's choice of schedule)": (lora, lora_bytes),
                  "planned decode, two launches (schedule comparison)": (lora_two, lora_bytes)}
-        path = "HipLoRABackend.apply_lora (slot-planned decode, one launch)"
+        path = "HipLoRABackend.apply_lora (slot-planned decode, the library's schedule)"
     else:
         mids = [torch.empty(S, n * r_max, dtype=host.x.dtype, device=dev) for _ in range(n_rep)]
         ws = Workspace()
@@ -471,21 +499,21 @@ def bench_other(args) -> int:
     # Each graph rotates through the replicas for at least 32 calls, so that a
     # replay's own launch cost is spread over many kernels.
     per_graph = max(32, n_rep)
-    step_ms = time_graph(torch, capture(torch, step, per_graph), calls, per_graph, stream)
+    step_ms = time_calls(torch, step, args.steps, per_graph, stream)
     for k, (fn, nbytes) in parts.items():
         ms = time_graph(torch, capture(torch, fn, per_graph), calls, per_graph, stream)
         kernels[k] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9}
     fb, pe = be.linked_workspace.counters()
     if pe:
         raise RuntimeError(f"{pe} plan errors; timings are void")
-    dom = max((k for k in kernels if "schedule" not in k), key=lambda k: kernels[k]["us"])
+    dom = max((k for k in kernels if "comparison" not in k), key=lambda k: kernels[k]["us"])
     fl = synthetic.flops(host)
     result = {
         "metric": METRIC,
         "value": round(total_bytes / (step_ms * 1e-3) / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": calls,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": step_ms,
         "us_per_step": step_ms * 1e3,
@@ -503,7 +531,7 @@ def bench_other(args) -> int:
         "kernels": kernels,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(kernels[dom]["GB/s"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kernels[dom]["GB/s"] / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_bytes(name) if name in GROUPED_WORKLOADS else None},
+                     "traffic": traffic_bytes(name, "" if name in GROUPED_WORKLOADS else dom)},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_other(name, host, total_bytes, args.cpu_seconds)
@@ -556,8 +584,10 @@ def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> di
 # --profile-traffic: the copy kernel used to calibrate the counters moves
 # COPY_ELEMS bf16 values (read once, written once).
 COPY_ELEMS = 32 << 20
-PLANNED_KERNEL = "planned_kernel"
+PROFILE_CALLS = 64
 GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_qkv")
+PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down")
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
 
 def grouped_host(name: str):
@@ -570,105 +600,172 @@ def grouped_host(name: str):
     return synthetic.decode_qkv(device="cpu")
 
 
+def workload_host(name: str):
+    from multi_lora_amd import synthetic
+
+    if name in GROUPED_WORKLOADS:
+        return grouped_host(name)
+    return synthetic.prefill_mlp(device="cpu", part=name.split("_", 1)[1])
+
+
 def traffic_file(name: str) -> Path:
-    return ROOT / "profiles" / f"planned_decode_{name}_traffic.json"
+    family = "planned_decode" if name in GROUPED_WORKLOADS else "segment"
+    return ROOT / "profiles" / f"{family}_{name}_traffic.json"
 
 
-def traffic_bytes(name: str):
+def traffic_bytes(name: str, prefix: str = ""):
+    """Counter HBM bytes per call of the workload's LoRA path, or of its kernels whose short name starts
+    with ``prefix``; None when no counter summary is committed."""
     f = traffic_file(name)
-    return json.loads(f.read_text()).get("hbm_bytes_per_launch") if f.exists() else None
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    if not prefix:
+        return d.get("hbm_bytes_per_call")
+    ks = [v for k, v in d.get("kernels", {}).items() if k.startswith(prefix)]
+    return round(sum(k["hbm_bytes_per_call"] for k in ks)) if ks else None
 
 
-def profile_traffic(name: str, launches: int = 64, copies: int = 16) -> int:
-    """The planned decode kernel of a workload over rotating replicas (its
-    input already normalised for decode_qkv), then a plain copy kernel."""
+def profile_traffic(name: str) -> int:
+    """PROFILE_CALLS calls of a workload's LoRA path as the backend runs it
+    (HipLoRABackend.apply_lora_multi; decode_qkv's input normalised
+    beforehand), over rotating replicas, then a plain copy kernel of known
+    size.  Meant to run under rocprofv3 --pmc."""
     import torch
 
-    from multi_lora_amd import synthetic
-    from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, apply_grouped
+    from multi_lora_amd import HipLoRABackend, synthetic
+    from multi_lora_amd.kernels.rmsnorm import rmsnorm_fwd
 
     dev = torch.device("cuda", 0)
-    host = grouped_host(name)
+    torch.cuda.set_device(dev)
+    host = workload_host(name)
     meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
     e = host.x.element_size()
     rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + host.base.numel()) * e
     n_rep = max(2, -(-600_000_000 // rep_bytes))
     reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
              host.base.to(dev)) for _ in range(n_rep)]
-    lws = LinkedWorkspace()
-    for i in range(launches):
-        x, a, b, out = reps[i % len(reps)]
-        assert apply_grouped(x, a, b, meta, out, host.col_offsets, lws, mode=1)
+    if "norm_weight" in host.extra:
+        w = host.extra["norm_weight"].to(dev)
+        reps = [(rmsnorm_fwd(x, w, host.extra["eps"]), a, b, out) for x, a, b, out in reps]
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(meta)
+    torch.cuda.synchronize()
+    for i in range(PROFILE_CALLS):
+        x, a, b, out = reps[i % n_rep]
+        be.apply_lora_multi(x, a, b, out, host.col_offsets)
     torch.cuda.synchronize()
     src = torch.randn(COPY_ELEMS, device=dev).bfloat16()
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    for _ in range(copies):
+    for _ in range(16):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    fb, pe = lws.counters()
-    print(json.dumps({"workload": name, "launches": launches, "copy_launches": copies,
+    fb, pe = be.linked_workspace.counters()
+    print(json.dumps({"workload": name, "calls": PROFILE_CALLS, "copy_launches": 16,
                       "copy_bytes_each_way": COPY_ELEMS * 2, "fallback_chunks": fb, "plan_errors": pe}))
     return 0
 
 
-def _pmc_means(directory: str, counter: str) -> dict:
-    """Mean per-dispatch value of `counter` for the planned decode kernel and the copy kernel."""
+def _short_kernel(name: str) -> str:
+    """``void mlora::(anonymous namespace)::planned_kernel<mlora::BF16, 2>(int const*, ...)``
+    -> ``planned_kernel<BF16, 2>``."""
+    s = name.replace("(anonymous namespace)::", "").replace("mlora::", "")
+    if s.startswith("void "):
+        s = s[5:]
+    depth = 0
+    for i, ch in enumerate(s):
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0:
+            return s[:i].strip()
+    return s.strip()
+
+
+def _pmc_sums(directory: str, counter: str) -> dict:
+    """Per short kernel name, the sum of ``counter`` over the LoRA path's
+    dispatches; the copy kernel's mean per dispatch under ``"copy"``."""
     import csv
 
     files = sorted(Path(directory).rglob("*counter_collection.csv"))
     if not files:
         raise SystemExit(f"no counter_collection.csv under {directory}")
-    vals = {"headline": [], "copy": []}
+    sums, copy = {}, []
     for f in files:
         with open(f, newline="") as fh:
             for row in csv.DictReader(fh):
                 if row.get("Counter_Name") != counter:
                     continue
-                name = row.get("Kernel_Name", "")
+                full = row.get("Kernel_Name", "")
                 v = float(row["Counter_Value"])
-                if PLANNED_KERNEL in name:
-                    vals["headline"].append(v)
-                elif "neg" in name:
-                    vals["copy"].append(v)
-    if not vals["headline"] or not vals["copy"]:
-        raise SystemExit(f"{counter}: kernels not found in {directory}")
-    return {k: sum(v) / len(v) for k, v in vals.items()} | {"dispatches": {k: len(v) for k, v in vals.items()}}
+                if "mlora::" in full:
+                    k = _short_kernel(full)
+                    if not k.startswith("rmsnorm_kernel"):
+                        sums[k] = sums.get(k, 0.0) + v
+                elif "neg" in full:
+                    copy.append(v)
+    if not sums:
+        raise SystemExit(f"{counter}: no path kernels in {directory}")
+    return {"kernels": sums, "copy": sum(copy) / len(copy) if copy else None}
 
 
-def summarize_pmc(name: str, fetch_dir: str, write_dir: str) -> int:
+def summarize_pmc(name: str, dirs) -> int:
+    """FETCH_SIZE and WRITE_SIZE runs (and optionally an MFMA-counter run) of
+    --profile-traffic -> the workload's counter summary under profiles/."""
     from multi_lora_amd import synthetic
 
-    fetch = _pmc_means(fetch_dir, "FETCH_SIZE")
-    write = _pmc_means(write_dir, "WRITE_SIZE")
+    fetch = _pmc_sums(dirs[0], "FETCH_SIZE")
+    write = _pmc_sums(dirs[1], "WRITE_SIZE")
     copy_kib = COPY_ELEMS * 2 / 1024
-    f_scale = copy_kib / fetch["copy"]
-    w_scale = copy_kib / write["copy"]
-    fetch_b = fetch["headline"] * f_scale * 1024
-    write_b = write["headline"] * w_scale * 1024
-    algo = synthetic.algorithmic_bytes(grouped_host(name))
+    f_scale, w_scale = copy_kib / fetch["copy"], copy_kib / write["copy"]
+    host = workload_host(name)
+    algo = synthetic.algorithmic_bytes(host)
+    kernels = {}
+    for k in sorted(set(fetch["kernels"]) | set(write["kernels"])):
+        fb = fetch["kernels"].get(k, 0.0) / PROFILE_CALLS * f_scale * 1024
+        wb = write["kernels"].get(k, 0.0) / PROFILE_CALLS * w_scale * 1024
+        kernels[k] = {"fetch_bytes_per_call": round(fb), "write_bytes_per_call": round(wb),
+                      "hbm_bytes_per_call": round(fb + wb)}
+    commands = [
+        f"timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d <FETCH_DIR> -f csv -- python3 bench.py "
+        f"--profile-traffic --workload {name}",
+        f"timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d <WRITE_DIR> -f csv -- python3 bench.py "
+        f"--profile-traffic --workload {name}",
+    ]
+    if len(dirs) > 2:
+        fl = synthetic.flops(host)
+        for c in MFMA_COUNTERS:
+            sums = _pmc_sums(dirs[2], c)["kernels"]
+            for k, v in sums.items():
+                kernels.setdefault(k, {})[c + "_per_call"] = round(v / PROFILE_CALLS)
+        mops = sum(kernels[k].get("SQ_INSTS_VALU_MFMA_MOPS_BF16_per_call", 0) for k in kernels)
+        mfma = {"algorithmic_flops_per_call": fl, "mfma_flops_per_call": mops * 512,
+                "mfma_over_algorithmic": round(mops * 512 / fl, 4) if fl else None,
+                "note": "SQ_INSTS_VALU_MFMA_MOPS_BF16 counts units of 512 flops; the excess over the "
+                        "algorithmic flops is the zero padding of rank and row tiles"}
+        commands.append(f"timeout -s KILL 60 rocprofv3 --pmc {' '.join(MFMA_COUNTERS)} -d <MFMA_DIR> -f csv -- "
+                        f"python3 bench.py --profile-traffic --workload {name}")
+    else:
+        mfma = None
+    total_f = sum(k.get("fetch_bytes_per_call", 0) for k in kernels.values())
+    total_w = sum(k.get("write_bytes_per_call", 0) for k in kernels.values())
+    commands.append(f"python3 bench.py --workload {name} --summarize-pmc <FETCH_DIR> <WRITE_DIR>"
+                    + (" <MFMA_DIR>" if len(dirs) > 2 else ""))
     out = {
-        "kernel": f"{PLANNED_KERNEL} (single launch)",
         "workload": OTHER_WORKLOADS.get(name, HEADLINE_WORKLOAD),
-        "algorithmic_bytes_per_launch": algo,
-        "hbm_bytes_per_launch": round(fetch_b + write_b),
-        "fetch_bytes_per_launch": round(fetch_b),
-        "write_bytes_per_launch": round(write_b),
-        "traffic_over_algorithmic": round((fetch_b + write_b) / algo, 4),
-        "raw_kib_per_dispatch": {"FETCH_SIZE": fetch["headline"], "WRITE_SIZE": write["headline"]},
-        "copy_calibration": {
-            "bytes_each_way": COPY_ELEMS * 2,
-            "FETCH_SIZE_kib": fetch["copy"], "WRITE_SIZE_kib": write["copy"],
-            "fetch_scale": f_scale, "write_scale": w_scale,
-        },
-        "dispatches": {"FETCH_SIZE": fetch["dispatches"], "WRITE_SIZE": write["dispatches"]},
-        "commands": [
-            f"timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d <FETCH_DIR> -f csv -- python3 bench.py "
-            f"--profile-traffic --workload {name}",
-            f"timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d <WRITE_DIR> -f csv -- python3 bench.py "
-            f"--profile-traffic --workload {name}",
-            f"python3 bench.py --workload {name} --summarize-pmc <FETCH_DIR> <WRITE_DIR>",
-        ],
+        "path": "HipLoRABackend.apply_lora_multi, the library's choice of kernels",
+        "calls": PROFILE_CALLS,
+        "algorithmic_bytes_per_call": algo,
+        "hbm_bytes_per_call": total_f + total_w,
+        "fetch_bytes_per_call": total_f,
+        "write_bytes_per_call": total_w,
+        "traffic_over_algorithmic": round((total_f + total_w) / algo, 4),
+        "fetch_over_algorithmic_reads": round(total_f / (algo - host.base.numel() * host.x.element_size()), 4),
+        "kernels": kernels,
+        "mfma": mfma,
+        "copy_calibration": {"bytes_each_way": COPY_ELEMS * 2, "FETCH_SIZE_kib": fetch["copy"],
+                             "WRITE_SIZE_kib": write["copy"], "fetch_scale": f_scale, "write_scale": w_scale},
+        "commands": commands,
     }
     traffic_file(name).write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
@@ -699,7 +796,9 @@ def cpu_model() -> str:
 def main() -> int:
     args = parse()
     if args.summarize_pmc:
-        return summarize_pmc(args.workload, *args.summarize_pmc)
+        if len(args.summarize_pmc) not in (2, 3):
+            raise SystemExit("--summarize-pmc takes FETCH_DIR WRITE_DIR [MFMA_DIR]")
+        return summarize_pmc(args.workload, args.summarize_pmc)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding of this path is design-only", file=sys.stderr)

@@ -157,7 +157,7 @@ def bench_c5_step(args) -> int:
     warm, timed = 96, max(20, min(args.steps // 20, 60))
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(timed)]
     step_ms, misses, host_ms = [], [], []
-    bank_bytes = pool.buffers._plan_for(R).total * 2
+    bank_bytes = pool.buffers.layout(R).total * 2
     for it in range(warm + timed):
         names = draw()
         wanted = list(dict.fromkeys(names))
@@ -275,7 +275,7 @@ def bench_pool_upload(args) -> int:
     reload_ms = (time.perf_counter() - t0) * 1e3
 
     buf = pool.buffers
-    plan = buf._plan_for(rank)
+    plan = buf.layout(rank)
     table = buf._key_table(plan)
     stage = torch.randn(h, plan.total, device=dev).bfloat16()
     slots = torch.arange(h, dtype=torch.int32, device=dev)
@@ -354,10 +354,27 @@ def time_graph(torch, g, calls: int, per_graph: int, stream) -> float:
     return t0.elapsed_time(t1) / (replays * per_graph)
 
 
+_CAPTURE_STREAM = []
+
+
+def capture_stream(torch):
+    """The one stream every graph of the bench is captured on."""
+    if not _CAPTURE_STREAM:
+        _CAPTURE_STREAM.append(torch.cuda.Stream())
+    return _CAPTURE_STREAM[0]
+
+
 def capture(torch, fn, n: int):
-    """Graph of fn(0), ..., fn(n-1)."""
+    """Graph of fn(0), ..., fn(n-1), captured after running the same calls
+    once on the capture stream (so per-stream workspaces exist beforehand
+    and nothing is allocated or cleared inside the graph)."""
+    s = capture_stream(torch)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n):
+            fn(i)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for i in range(n):
             fn(i)
     torch.cuda.synchronize()
@@ -848,8 +865,13 @@ def main() -> int:
     # steps are timed as HIP graph replays: a graph of one pass over the
     # replicas, and one of the remaining steps, make up exactly `steps` steps.
     def capture(n, phases=3, mode=None):
+        s = capture_stream(torch)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):  # the capture stream's workspace exists before capture
+            for i in range(n):
+                step(i, phases, mode)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=s):
             for i in range(n):
                 step(i, phases, mode)
         torch.cuda.synchronize()

@@ -1,8 +1,8 @@
-"""Everything one decode step touches, at fixed addresses, and its graph capture.
+"""Batched single-token decoding as one replayable HIP graph.
 
-Mirrors multi_lora/graph_decode.py:23-111 on the model of
-``multi_lora_amd.decoder`` (whose ``StaticKV`` plays the part of
-``transformers.StaticCache``):
+API of multi_lora/graph_decode.py:23-111 (``DecodeStep.new``, ``prefill``,
+``run``, ``rewind``, ``capture_graph`` and the resident tensors the
+reference's tests inspect), built on this package's decoder:
 
     step = DecodeStep.new(mgr, batch, start, max_len)
     first = step.prefill(mgr, input_ids, attention_mask, names)
@@ -10,63 +10,63 @@ Mirrors multi_lora/graph_decode.py:23-111 on the model of
     mgr._setup_forward_batch(names, seq_lens=[1] * batch)
     graph, out = capture_graph(mgr, step)        # then graph.replay() per step
 
-A decode step reads and writes only resident tensors: the KV cache is
-written in place at ``kv_pos``, the attention mask is recomputed in place
-from ``grid <= kv_pos``, and ``position_ids`` / ``kv_pos`` are advanced in
-place, so the captured graph advances by itself on every replay.  The LoRA
-launches inside read the resident segment table, which the manager rewrites
-in place between batches.
+Design.  The whole decode state is device memory that a step updates in
+place, so a captured step is its own successor:
+
+* one int64 counter, ``kv_pos``, is both the KV slot written this step and
+  every row's rotary position (``position_ids`` is a broadcast view of it);
+* the attention mask is kept, not recomputed: the prompt's slots are
+  visible from the start and each step makes its own slot visible with one
+  indexed write before the forward;
+* the KV cache (``decoder.StaticKV``) is written at ``kv_pos`` by the
+  attention layers.
+
+Slots past ``kv_pos`` may hold stale keys (from the warm-up or from an
+earlier pass before a rewind); they stay masked until the step that owns
+them overwrites them.  LoRA launches inside the step read the resident
+segment table, which the manager rewrites in place between batches.
 """
 
 from __future__ import annotations
-
-from dataclasses import dataclass
 
 import torch
 
 from .decoder import StaticKV
 
-WARMUP_ROUNDS = 3  # steps run before capture, on a second set of buffers
+WARMUP_STEPS = 3
 
 
-@dataclass
 class DecodeStep:
-    kv: StaticKV
-    input_ids: torch.Tensor     # (batch, 1) token fed this step
-    position_ids: torch.Tensor  # (batch, 1) rotary position
-    kv_pos: torch.Tensor        # (1,) KV slot written this step
-    attn_mask: torch.Tensor     # (batch, 1, 1, max_len) visible slots
-    grid: torch.Tensor          # (max_len,) 0..max_len-1, for the mask
-    batch: int
-    start: int                  # first position after the prompt; rewind target
-    max_len: int
+    """Resident state of ``batch`` sequences decoding one token per step from position ``start``."""
+
+    def __init__(self, mgr, batch: int, start: int, max_len: int) -> None:
+        if not 0 < start < max_len:
+            raise ValueError(f"need 0 < start < max_len (start={start}, max_len={max_len})")
+        device, dtype = mgr.pool.device, mgr.pool.dtype
+        self.batch, self.start, self.max_len = batch, start, max_len
+        self.kv = StaticKV(mgr.model.config, batch, max_len, device, dtype)
+        self.input_ids = torch.zeros((batch, 1), dtype=torch.long, device=device)
+        self.kv_pos = torch.full((1,), start, dtype=torch.long, device=device)
+        self.position_ids = self.kv_pos.view(1, 1).expand(batch, 1)
+        self.attn_mask = torch.zeros((batch, 1, 1, max_len), dtype=torch.bool, device=device)
+        self.attn_mask[..., :start] = True
 
     @classmethod
     def new(cls, mgr, batch: int, start: int, max_len: int) -> "DecodeStep":
-        device = mgr.pool.device
-        return cls(
-            kv=StaticKV(mgr.model.config, batch, max_len, device, mgr.pool.dtype),
-            input_ids=torch.zeros((batch, 1), device=device, dtype=torch.long),
-            position_ids=torch.full((batch, 1), start, device=device, dtype=torch.long),
-            kv_pos=torch.tensor([start], device=device, dtype=torch.long),
-            attn_mask=torch.zeros((batch, 1, 1, max_len), device=device, dtype=torch.bool),
-            grid=torch.arange(max_len, device=device, dtype=torch.long),
-            batch=batch,
-            start=start,
-            max_len=max_len,
-        )
-
-    def like_new(self, mgr) -> "DecodeStep":
-        return DecodeStep.new(mgr, self.batch, self.start, self.max_len)
+        return cls(mgr, batch, start, max_len)
 
     def rewind(self) -> None:
-        """Back to ``start``; KV slots past it are simply overwritten later."""
-        self.position_ids.fill_(self.start)
+        """Return to position ``start``: the counter and the mask, nothing else."""
         self.kv_pos.fill_(self.start)
+        self.attn_mask[..., self.start:] = False
 
     def prefill(self, mgr, input_ids: torch.Tensor, attention_mask: torch.Tensor, lora_names) -> torch.Tensor:
-        """Fill the first ``start`` KV slots; returns the next token (batch, 1)."""
+        """Run the prompt (``start`` tokens per row) through the model with each
+        row's adapter, filling KV slots ``[0, start)``; returns the greedy next
+        token of every row, shape ``(batch, 1)``."""
         t = int(input_ids.shape[1])
+        if t != self.start:
+            raise ValueError(f"prompt length {t} differs from the step's start position {self.start}")
         out = mgr.forward_with_lora(
             input_ids=input_ids, attention_mask=attention_mask, lora_names=lora_names,
             seq_lens=[t] * self.batch, past_key_values=self.kv, use_cache=True,
@@ -74,31 +74,36 @@ class DecodeStep:
         return out.logits[:, -1].argmax(dim=-1, keepdim=True)
 
     def run(self, mgr):
-        """One decode step: refresh the mask, forward (writing KV), advance the position."""
-        self.attn_mask.copy_((self.grid <= self.kv_pos).view(1, 1, 1, -1))
+        """One step: expose this step's KV slot, forward ``input_ids``, advance the counter."""
+        self.attn_mask.index_fill_(-1, self.kv_pos, True)
         out = mgr.model(input_ids=self.input_ids, attention_mask=self.attn_mask, position_ids=self.position_ids,
                         past_key_values=self.kv, cache_position=self.kv_pos, use_cache=True)
-        self.position_ids.add_(1)
         self.kv_pos.add_(1)
         return out
 
 
-def capture_graph(mgr, step: DecodeStep):
-    """Warm up on a second set of buffers, capture one step, rewind; returns (graph, output).
+def capture_graph(mgr, step: DecodeStep, warmup: int = WARMUP_STEPS):
+    """Capture one ``step.run`` into a HIP graph; returns ``(graph, output)``.
 
-    One-time work (library workspaces, allocator growth) cannot be recorded,
-    so it is done first in the warm-up, on a side stream.  The captured run
-    really executes once, hence the rewind before returning.
+    Warm-up steps run first on the stream the capture will use, on the
+    step's own buffers, so every lazily created resource (the decode
+    path's per-stream workspace, library handles, allocator blocks) exists
+    before capture and nothing is allocated or cleared inside the graph.
+    The warm-up advances the state and is rewound; the capture only
+    records, so the step is at ``start`` when this returns and the first
+    replay decodes position ``start``.  ``output`` is the captured run's
+    result, whose tensors every replay overwrites.
     """
-    warm = step.like_new(mgr)
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for _ in range(WARMUP_ROUNDS):
-            warm.run(mgr)
-    torch.cuda.current_stream().wait_stream(stream)
+    if step.start + warmup + 1 > step.max_len:
+        raise ValueError(f"max_len {step.max_len} leaves no room for {warmup} warm-up steps and the capture")
+    side = torch.cuda.Stream(device=step.kv_pos.device)
+    side.wait_stream(torch.cuda.current_stream(step.kv_pos.device))
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            step.run(mgr)
+        step.rewind()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         out = step.run(mgr)
-    step.rewind()
+    torch.cuda.current_stream(step.kv_pos.device).wait_stream(side)
     return graph, out

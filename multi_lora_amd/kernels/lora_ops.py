@@ -66,6 +66,11 @@ class LinkedWorkspace:
         key = (device, stream)
         buf = self.bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "the decode workspace of the capturing stream does not exist yet (or is too small): it would "
+                    "be allocated and zero-filled inside the graph; run the same calls once on that stream "
+                    "before capturing (torch.cuda.graph(g, stream=s) after running them on s)")
             buf = self.bufs[key] = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         return buf.data_ptr(), buf.numel()
 

@@ -127,17 +127,20 @@ class QKVProjGroup:
         return wrapper.add_delta(x, y)
 
 
+QKV_LEAVES = ("q_proj", "k_proj", "v_proj")
+
+
 def fuse_qkv_projections(wrappers: Dict[str, LinearWithLoRA]) -> int:
-    """Group the q/k/v wrappers that share a name prefix; returns the number of groups."""
-    by_prefix: Dict[str, Dict[str, LinearWithLoRA]] = {}
-    for key, wrapper in wrappers.items():
-        for suffix in ("q_proj", "k_proj", "v_proj"):
-            if key.endswith("." + suffix):
-                by_prefix.setdefault(key[: -len(suffix)], {})[suffix] = wrapper
-                break
-    groups = 0
-    for parts in by_prefix.values():
-        if len(parts) == 3:
-            QKVProjGroup([parts["q_proj"], parts["k_proj"], parts["v_proj"]])
-            groups += 1
-    return groups
+    """Fuse the base GEMMs of every attention block whose q, k and v
+    projections are all wrapped (multi_lora/layers.py:128-142); returns the
+    number of blocks fused.  Wrappers are matched by their parent module's
+    name, so ``...self_attn.q_proj`` joins ``...self_attn.k_proj``."""
+    blocks: Dict[str, Dict[str, LinearWithLoRA]] = {}
+    for name, wrapper in wrappers.items():
+        parent, dot, leaf = name.rpartition(".")
+        if dot and leaf in QKV_LEAVES:
+            blocks.setdefault(parent, {})[leaf] = wrapper
+    complete = [block for block in blocks.values() if len(block) == len(QKV_LEAVES)]
+    for block in complete:
+        QKVProjGroup([block[leaf] for leaf in QKV_LEAVES])
+    return len(complete)

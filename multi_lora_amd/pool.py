@@ -12,9 +12,9 @@ its slot tensors (pool.py:97-155):
   the eviction policy; the base slot goes last (pool.py:443-473).
 
 Upload.  The first time an adapter is loaded its weights are packed once
-into a flat host bank (pinned when the pool is on a GPU): all A blocks, then
-all B blocks, at offsets fixed per rank (the same packing the reference uses,
-pool.py:23-58).  A reload is then one contiguous H2D copy of the bank into a
+into a flat host bank (pinned when the pool is on a GPU), kept on the
+adapter object: all A blocks, then all B blocks, at offsets fixed per rank
+(the same packing the reference uses, pool.py:23-58).  A reload is then one contiguous H2D copy of the bank into a
 device staging row, on a side stream ordered after the compute stream; one
 ``mlora_pool_scatter`` launch per staged chunk then copies every key's
 blocks into the slots (the reference's scatter kernel,
@@ -77,9 +77,10 @@ class _GpuBuffers:
         self.dtype = dtype
         self.A: Dict[str, torch.Tensor] = {}
         self.B: Dict[str, torch.Tensor] = {}
-        self._plans: Dict[int, _RankPlan] = {}
-        self._plan_keys: Optional[tuple] = None
-        self._banks: Dict[int, tuple] = {}
+        # Bank layouts by (module signature, rank); the signature lists every
+        # module key with its (in, out) widths and grows with ensure().
+        self._layouts: Dict[Tuple[tuple, int], _RankPlan] = {}
+        self._signature: tuple = ()
         self._stage: Optional[torch.Tensor] = None
         self._copy_stream = None
         self._load_event = None
@@ -97,6 +98,8 @@ class _GpuBuffers:
             k, r = self.max_loras_per_batch, self.max_lora_rank
             self.A[key] = torch.zeros((k, r, in_dim), device=self.device, dtype=self.dtype)
             self.B[key] = torch.zeros((k, out_dim, r), device=self.device, dtype=self.dtype)
+        if len(self._signature) != len(self.A):
+            self._signature = tuple((k, int(self.A[k].shape[2]), int(self.B[k].shape[1])) for k in self.A)
 
     def get(self, key: str) -> Tuple[torch.Tensor, torch.Tensor]:
         if key not in self.A:
@@ -125,42 +128,55 @@ class _GpuBuffers:
         if self._load_event is not None:
             torch.cuda.current_stream(self.device).wait_event(self._load_event)
 
-    def _plan_for(self, rank: int) -> _RankPlan:
-        keys = tuple(self.A)
-        if keys != self._plan_keys:
-            self._plans.clear()
-            self._banks.clear()
-            self._plan_keys = keys
-        plan = self._plans.get(rank)
+    def layout(self, rank: int) -> _RankPlan:
+        """The upload bank layout of a rank-``rank`` adapter over the pool's current module keys."""
+        plan = self._layouts.get((self._signature, rank))
         if plan is None:
-            dims = {k: (int(self.A[k].shape[2]), int(self.B[k].shape[1])) for k in keys}
-            plan = _RankPlan(rank, list(keys), dims)
-            self._plans[rank] = plan
+            keys = [k for k, _, _ in self._signature]
+            plan = _RankPlan(rank, keys, {k: (i, o) for k, i, o in self._signature})
+            plan.signature = self._signature
+            self._layouts[(self._signature, rank)] = plan
         return plan
 
-    def _bank_for(self, weights: AdapterWeights, plan: _RankPlan) -> torch.Tensor:
-        """The adapter's packed host bank; built on first use and cached."""
-        hit = self._banks.get(id(weights))
-        if hit is not None and hit[0] is weights and hit[1] == plan.rank:
-            return hit[2]
+    def bank(self, weights: AdapterWeights, plan: _RankPlan) -> torch.Tensor:
+        """The adapter's flat upload bank for ``plan``, packed on first use.
+
+        The bank is kept on the adapter object (``weights.banks``), so it
+        lives exactly as long as the caller keeps the adapter, and one bank
+        serves every pool with the same layout.  With ``release_modules`` the
+        per-module tensors are dropped after packing; such an adapter can no
+        longer be packed for a different layout (a pool that grew new module
+        keys afterwards), which raises rather than upload zeros.
+        """
+        key = (plan.signature, plan.rank, self.dtype)
+        bank = weights.banks.get(key)
+        if bank is not None:
+            return bank
         if weights.flattened:
             raise RuntimeError(
-                f"adapter (rank {plan.rank}) was packed and released before the pool's module set "
-                f"changed to {len(plan.keys)} keys; its bank cannot be rebuilt"
-            )
-        bank = torch.zeros(plan.total, dtype=self.dtype, pin_memory=self.device.type == "cuda")
-        for key in plan.keys:
-            mod = weights.modules.get(key)
-            if mod is None:
-                continue  # missing module: its blocks stay zero
-            a, b = mod
-            ao, bo = plan.a_off[key], plan.b_off[key]
-            bank[ao : ao + a.numel()].copy_(a.reshape(-1))
-            bank[bo : bo + b.numel()].copy_(b.reshape(-1))
-        self._banks[id(weights)] = (weights, plan.rank, bank)
+                f"rank-{plan.rank} adapter's module tensors were released after packing for another module "
+                f"layout; the pool now has {len(plan.keys)} module keys and the bank cannot be rebuilt")
+        bank = self._pack(weights, plan)
+        weights.banks = {key: bank}
         if self.release_modules:
             weights.modules = {}
             weights.flattened = True
+        return bank
+
+    def _pack(self, weights: AdapterWeights, plan: _RankPlan) -> torch.Tensor:
+        """One host copy in the layout's order: every key's A block, then every
+        B block; a module the adapter lacks contributes zeros."""
+        pieces = []
+        for side in (0, 1):
+            for key in plan.keys:
+                mod = weights.modules.get(key)
+                shape = plan.a_shape[key] if side == 0 else plan.b_shape[key]
+                if mod is None:
+                    pieces.append(torch.zeros(shape[0] * shape[1], dtype=self.dtype))
+                else:
+                    pieces.append(mod[side].reshape(-1).to(self.dtype))
+        bank = torch.empty(plan.total, dtype=self.dtype, pin_memory=self.device.type == "cuda")
+        torch.cat(pieces, out=bank)
         return bank
 
     def _stage_rows(self, total: int) -> torch.Tensor:
@@ -174,7 +190,7 @@ class _GpuBuffers:
         for slot, w in pairs:
             by_rank.setdefault(int(w.rank), []).append((slot, w))
         for rank, group in by_rank.items():
-            plan = self._plan_for(rank)
+            plan = self.layout(rank)
             if self.device.type == "cuda":
                 stage = self._stage_rows(plan.total)
                 stage.record_stream(torch.cuda.current_stream(self.device))
@@ -182,10 +198,10 @@ class _GpuBuffers:
                 chunk = group[c0 : c0 + _BANK_CHUNK]
                 if self.device.type != "cuda":
                     for slot, w in chunk:
-                        self._scatter(self._bank_for(w, plan), slot, plan)
+                        self._scatter(self.bank(w, plan), slot, plan)
                     continue
                 for i, (slot, w) in enumerate(chunk):
-                    stage[i].copy_(self._bank_for(w, plan), non_blocking=non_blocking)
+                    stage[i].copy_(self.bank(w, plan), non_blocking=non_blocking)
                 self._scatter_staged(stage, [slot for slot, _ in chunk], plan)
 
     def _key_table(self, plan: _RankPlan) -> torch.Tensor:

@@ -27,6 +27,8 @@ class AdapterWeights:
     # Set once the pool has packed the modules into its pinned upload bank and
     # released the per-module tensors.
     flattened: bool = False
+    # Packed upload banks by (module layout, rank, dtype), filled by the pool.
+    banks: Dict[tuple, torch.Tensor] = field(default_factory=dict, repr=False, compare=False)
 
     def validate(self) -> None:
         for key, (a, b) in self.modules.items():

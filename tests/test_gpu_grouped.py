@@ -370,12 +370,15 @@ def test_hip_graph_replays_follow_metadata_rewrites(dev, plan):
         meta = make_meta(wl.seg_lens, wl.seg_slots, wl.slot_ranks, wl.scalings, dev, torch.bfloat16, with_plan=False)
     be = HipLoRABackend()
     be.set_kernel_input_metadata(meta)
-    eager = be.apply_lora(wl.x, a, b, wl.clone_base())
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):  # the capture stream's workspace exists before capture
+        eager = be.apply_lora(wl.x, a, b, wl.clone_base())
     torch.cuda.synchronize()
 
     out = wl.clone_base()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=stream):
         be.apply_lora(wl.x, a, b, out)
     for _ in range(4):
         out.copy_(wl.base)

@@ -80,10 +80,13 @@ def test_graph_replay_follows_packed_rewrites(dev):
     be = HipLoRABackend()
     be.set_kernel_input_metadata(meta)
     out = wl.clone_base()
-    be.apply_lora(wl.x, a, b, out)     # warm up (workspaces)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        be.apply_lora(wl.x, a, b, out)     # warm up the capture stream's workspace
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=stream):
         be.apply_lora(wl.x, a, b, out)
     rng = random.Random(9)
     for _ in range(4):

@@ -109,7 +109,7 @@ def test_backend_mixed_batch_uses_one_call_and_replays_in_a_graph(dev):
         be.apply_lora_multi(xd, Ad, Bd, out, cols)  # warm-up outside the graph
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=stream):
         be.apply_lora_multi(xd, Ad, Bd, out, cols)
     for rep in range(3):
         out.copy_(base.to(dev))
@@ -200,7 +200,7 @@ def test_mixed_batch_expand_in_a_replayed_graph_follows_table_rewrites(dev):
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=stream):
         apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)
     for rep, slots in enumerate((slots0, slots1, slots1, slots0)):
         meta.weight_indices.copy_(torch.tensor(slots, dtype=torch.int32))

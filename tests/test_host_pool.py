@@ -115,3 +115,57 @@ def test_rank_above_pool_max_raises():
     pool = LoRAMemoryPool(2, 4, torch.device("cpu"), torch.float32)
     with pytest.raises(ValueError):
         pool.prepare_lora_batch(["wide"], weight_store=st)
+
+
+def test_bank_is_packed_once_and_kept_on_the_adapter():
+    """Packing follows the layout (every A block, then every B block); a
+    reload reuses the adapter's bank, and a second pool with the same module
+    layout reuses it too."""
+    st = {"a": adapter(1, 4), "b": adapter(2, 4), "c": adapter(3, 4)}
+    a_mods = {k: (a.clone(), b.clone()) for k, (a, b) in st["a"].modules.items()}
+    pool = LoRAMemoryPool(2, 8, torch.device("cpu"), torch.float32)
+    pool.prepare_lora_batch(["a"], weight_store=st)
+    (bank,) = st["a"].banks.values()
+    plan = pool.buffers.layout(4)
+    want = torch.cat([a_mods[k][0].reshape(-1) for k in plan.keys] + [a_mods[k][1].reshape(-1) for k in plan.keys])
+    assert torch.equal(bank, want)
+    assert st["a"].flattened and not st["a"].modules
+    pool.prepare_lora_batch(["b", "c"], weight_store=st)   # evicts "a"
+    pool.prepare_lora_batch(["a"], weight_store=st)        # reload from the kept bank
+    (again,) = st["a"].banks.values()
+    assert again is bank
+    s = pool.get_slot_id("a")
+    for k in plan.keys:
+        a_stack, b_stack = pool.get_module_buffers(k)
+        assert torch.equal(a_stack[s, :4], a_mods[k][0]) and torch.equal(b_stack[s, :, :4], a_mods[k][1])
+    # a pool that learned the same module keys from another adapter reuses the bank
+    other = LoRAMemoryPool(2, 8, torch.device("cpu"), torch.float32)
+    other.prepare_lora_batch(["d"], weight_store={"d": adapter(4, 4)})
+    other.prepare_lora_batch(["a"], weight_store=st)
+    assert next(iter(st["a"].banks.values())) is bank
+    s = other.get_slot_id("a")
+    assert torch.equal(other.get_module_buffers("v_proj")[1][s, :, :4], a_mods["v_proj"][1])
+
+
+def test_new_module_keys_repack_or_raise_for_released_adapters():
+    """A pool that grows a module key needs new banks: an adapter that still
+    has its tensors is repacked; one whose tensors were released raises."""
+    only_q = {"a": adapter(1, 2, keys=("q_proj",)), "b": adapter(2, 2, keys=("q_proj",))}
+    both = {"c": adapter(3, 2)}
+    pool = LoRAMemoryPool(2, 4, torch.device("cpu"), torch.float32)
+    pool.buffers.release_modules = False
+    pool.prepare_lora_batch(["a"], weight_store=only_q)
+    pool.prepare_lora_batch(["c"], weight_store=both)      # adds v_proj
+    pool.prepare_lora_batch(["b", "c"], weight_store={**only_q, **both})   # evicts "a"
+    pool.prepare_lora_batch(["a", "c"], weight_store={**only_q, **both})   # repacked for q|v
+    s = pool.get_slot_id("a")
+    assert torch.equal(pool.get_module_buffers("q_proj")[0][s, :2], only_q["a"].modules["q_proj"][0])
+    assert not pool.get_module_buffers("v_proj")[0][s].any()
+
+    released = {"a": adapter(1, 2, keys=("q_proj",)), "b": adapter(2, 2, keys=("q_proj",))}
+    pool = LoRAMemoryPool(2, 4, torch.device("cpu"), torch.float32)
+    pool.prepare_lora_batch(["a"], weight_store=released)
+    pool.prepare_lora_batch(["c"], weight_store=both)
+    pool.prepare_lora_batch(["b", "c"], weight_store={**released, **both})
+    with pytest.raises(RuntimeError, match="cannot be rebuilt"):
+        pool.prepare_lora_batch(["a", "c"], weight_store={**released, **both})

@@ -40,7 +40,8 @@ struct ShrinkArgs {
   int m_tiles;      // row tiles per segment (ceil(max_len / bm)); bounds the grid
   int ks;           // K splits per row tile
   int k_per_split;  // reduction elements per split (multiple of KSTEP)
-  float* partials;  // ks > 1: [ks][rows][n_slices * r_max] fp32 split sums
+  float* partials;  // ks > 1: [ks][rows][part_cols] fp32 split sums (this launch's columns first)
+  int part_cols;    // row width of the split sums: n_slices * r_max of the whole call
   int skip_reduce;  // ks > 1: leave the split sums for the expand (no reduce launch)
 };
 
@@ -49,7 +50,8 @@ struct ShrinkPlan {
   int m_tiles;
   int ks;
   int k_per_split;
-  int nbt;    // compiled bound on 16-row blocks of A over all slices
+  int nbt;    // compiled bound on 16-row blocks of A over the slices of one launch
+  int spg;    // slices per launch: calls over 8 A blocks run one launch per group of slices
   size_t ws_bytes;
 };
 

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void shrink_kernel(ShrinkArgs a) {
 
   const int t = row0 + wm * 16 + r16;
   if (wk == 0 && t < end) {
-    const int ncols = a.n_slices * a.r_max;
+    const int ncols = a.part_cols;
     raw* mrow = static_cast<raw*>(a.mid) + static_cast<int64_t>(t) * a.mid_stride;
     float* prow = a.partials + (static_cast<int64_t>(kz) * a.rows + t) * ncols;
 #pragma unroll
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void shrink_rows_kernel(ShrinkArgs a) {
     }
   }
 
-  const int ncols = a.n_slices * a.r_max;
+  const int ncols = a.part_cols;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int t = wrow0 + rb * 16 + r16;
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
     __syncthreads();
   }
 
-  const int ncols = a.n_slices * a.r_max;
+  const int ncols = a.part_cols;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int t = row0 + wave * RB * 16 + rb * 16 + r16;
@@ -597,7 +597,7 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
     }
   }
 
-  const int ncols = a.n_slices * a.r_max;
+  const int ncols = a.part_cols;
   const int t = row0 + wave * 16 + r16;
   if (t < end) {
     raw* mrow = static_cast<raw*>(a.mid) + static_cast<int64_t>(t) * a.mid_stride;
@@ -641,7 +641,7 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a) {
   const int rank = slot_rank_of(a.meta, tr.slot, a.r_max, a.rank_mult);
   if (rank == 0) return;
   const int live = min(((rank + 15) >> 4) * 16, a.r_max);
-  const int ncols = a.n_slices * a.r_max;
+  const int ncols = a.part_cols;
   const int per_row = a.n_slices * live;
   const int64_t zs = static_cast<int64_t>(a.rows) * ncols;
   raw* mid = static_cast<raw*>(a.mid);
@@ -689,6 +689,16 @@ __global__ __launch_bounds__(256) void shrink_reduce_kernel(ShrinkArgs a) {
   }
 }
 
+// The in-order reduction of the split sums into mid, over dense row tiles.
+template <class T>
+hipError_t launch_reduce(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+  const int64_t r_tiles = dense_tiles(args.meta.bs, p.m_tiles * (p.bm / kReduceRows), args.rows, kReduceRows);
+  if (r_tiles <= 0) return hipSuccess;
+  if (!grid_fits(r_tiles)) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(r_tiles)), dim3(256), 0, stream, args);
+  return hipGetLastError();
+}
+
 // The short kernel (bm 16) runs one workgroup per segment and split; the
 // long kernels and the reduction run over dense row tiles.
 template <class T>
@@ -700,10 +710,7 @@ hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const Shri
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * p.ks)), dim3(256), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1 || args.skip_reduce) return e;
-  const int64_t r_tiles = dense_tiles(args.meta.bs, p.m_tiles * (p.bm / kReduceRows), args.rows, kReduceRows);
-  if (!grid_fits(r_tiles)) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((shrink_reduce_kernel<T>), dim3(static_cast<unsigned>(r_tiles)), dim3(256), 0, stream, args);
-  return hipGetLastError();
+  return launch_reduce<T>(p, args, stream);
 }
 
 template <class T, int NBT, bool AL>
@@ -738,7 +745,24 @@ hipError_t launch_al(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t st
 
 template <class T>
 hipError_t launch_dtype(const ShrinkPlan& p, const ShrinkArgs& args, bool aligned, hipStream_t stream) {
-  return aligned ? launch_al<T, true>(p, args, stream) : launch_al<T, false>(p, args, stream);
+  if (p.spg >= args.n_slices)
+    return aligned ? launch_al<T, true>(p, args, stream) : launch_al<T, false>(p, args, stream);
+  // One launch per group of slices, each writing its own columns of mid and
+  // of the split sums (same values as one launch over all slices), then one
+  // reduction over every column.
+  using raw = typename T::raw_t;
+  for (int s0 = 0; s0 < args.n_slices; s0 += p.spg) {
+    ShrinkArgs g = args;
+    g.n_slices = min(p.spg, args.n_slices - s0);
+    for (int i = 0; i < g.n_slices; ++i) g.slices[i] = args.slices[s0 + i];
+    g.mid = static_cast<raw*>(args.mid) + static_cast<int64_t>(s0) * args.r_max;
+    g.partials = args.partials ? args.partials + static_cast<int64_t>(s0) * args.r_max : nullptr;
+    g.skip_reduce = 1;
+    const hipError_t e = aligned ? launch_al<T, true>(p, g, stream) : launch_al<T, false>(p, g, stream);
+    if (e != hipSuccess) return e;
+  }
+  if (p.ks == 1 || args.skip_reduce) return hipSuccess;
+  return launch_reduce<T>(p, args, stream);
 }
 
 }  // namespace
@@ -748,8 +772,13 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
   if (in_dim <= 0 || r_max <= 0 || n_slices < 1 || n_slices > kMaxSlices || bs < 0 || max_len < 0 || rows < 0)
     return false;
   const int kstep = (dtype == MLORA_F32) ? F32::KSTEP : BF16::KSTEP;
-  const int blocks = n_slices * cdiv(r_max, 16);
+  // Over 8 blocks of A the slices run in groups of at most 8 blocks, one
+  // launch each (3 slices at r_max 64: q|k, then v), rather than one
+  // 16-block instance at occupancy 1.
+  const int per_slice = cdiv(r_max, 16);
   ShrinkPlan p{};
+  p.spg = (n_slices * per_slice > 8 && per_slice <= 8) ? 8 / per_slice : n_slices;
+  const int blocks = p.spg * per_slice;
   p.nbt = 1;
   while (p.nbt < blocks) p.nbt *= 2;
   if (p.nbt > 16) return false;
@@ -804,6 +833,7 @@ hipError_t launch_shrink(const ShrinkPlan& plan, ShrinkArgs args, int dtype, boo
   args.m_tiles = plan.m_tiles;
   args.ks = plan.ks;
   args.k_per_split = plan.k_per_split;
+  args.part_cols = args.n_slices * args.r_max;
   switch (dtype) {
     case MLORA_BF16: return launch_dtype<BF16>(plan, args, aligned, stream);
     case MLORA_F16: return launch_dtype<F16>(plan, args, aligned, stream);

@@ -308,6 +308,8 @@ def test_mixed_long_and_one_row_segments(dev, n_short):
     (2, 16, [16, 5, 0, 12]),     # two blocks
     (3, 16, [16, 16, 0, 7]),     # three blocks, compiled as four
     (2, 64, [64, 40, 0, 17]),    # eight blocks
+    (3, 64, [64, 40, 0, 17]),    # twelve blocks: q|k, then v, one launch each
+    (4, 48, [48, 33, 0, 7]),     # twelve blocks of three per slice: two launches of two slices
 ])
 def test_streamed_lds_shrink_block_counts(dev, n_slices, r_max, ranks):
     """Long segments with K a multiple of 64 take the shrink that streams x

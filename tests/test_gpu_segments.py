@@ -49,6 +49,13 @@ def case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, seed):
     ("rmax12_split", [1] * 30, [i % 6 for i in range(30)], [12, 12, 7, 0, 12, 5], 4096, [640], 12, torch.float16),
     ("rmax12_mixed_bf16", [40] + [1] * 20 + [33], [0] + [i % 4 for i in range(20)] + [2], [12, 9, 12, 4], 4096,
      [512, 256], 12, torch.bfloat16),
+    # q|k|v at r_max 64 (twelve A blocks): the shrink runs once per group of
+    # slices (q|k, then v), each writing its columns of mid / the split sums
+    ("qkv_r64_mixed", [90, 1, 1, 3, 40, 1], [0, 1, 2, 0, 3, 1], [64, 33, 0, 48], 4096, [512, 128, 128], 64,
+     torch.bfloat16),
+    ("qkv_r64_decode", [1] * 24 + [5], [i % 6 for i in range(25)], [64, 17, 64, 0, 40, 64], 4096, [512, 128, 128],
+     64, torch.bfloat16),
+    ("qkv_r64_long", [150, 200, 130], [0, 1, 0], [64, 40], 4096, [512, 128, 128], 64, torch.float16),
 ])
 def test_one_call_equals_two_calls(dev, name, lens, slots, ranks, in_dim, outs, r_max, dtype):
     x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, len(name))

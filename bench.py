@@ -67,46 +67,56 @@ OTHER_WORKLOADS = {
                          "rank-16 adapters, tokens drawn over 32 of them",
     "pool_upload": "pool upload scatter, Llama-3-8B 32 layers x 7 projections (224 keys), rank 16, "
                    "4 staged adapters (84 MB each) into an 8-slot pool",
-    "c5_step": "Llama-3-8B 32-layer LoRA step: 7 projections per layer at rank 16 (q|k|v and gate|up fused), "
+    "c5_step": "Llama-3-8B-shaped 32-layer model step (random init): 7 projections per layer LoRA-ed at rank 16, "
                "mixed batch of 2 x 512 prefill + 64 decode tokens, 128-slot pool (10.7 GB), adapters Zipf(1.1) over 512",
 }
 
 
 def bench_c5_step(args) -> int:
-    """Per-step latency of the 32-layer Llama-3-8B LoRA stack serving a mixed
+    """Per-step latency of a 32-layer Llama-3-8B-shaped model serving a mixed
     batch, with the slot pool in the loop.
 
-    Every step draws 66 requests (2 prefill of 512 tokens, 64 decode) from
-    Zipf(1.1) over 512 adapters, makes them resident in the 128-slot pool
-    (LRU eviction; misses are uploaded from pinned host banks by the copy
-    stream and the scatter kernel), rewrites the resident segment table and
-    replays one HIP graph holding every LoRA call of the step: per layer
-    q|k|v (3 slices, x read once), o, gate|up (2 slices) and down.  The base
-    GEMMs and attention are not part of the path.  Requests are not merged
-    (one segment each), so the captured launch shapes hold for every step.
-    Host banks: 512 adapter names share 16 distinct weight sets, so host
-    memory stays at 1.3 GB while every miss still moves its 84 MB over PCIe.
+    The model is ``decoder.Decoder(DecoderConfig.llama3_8b())``, random-init
+    on the GPU, bf16, all 7 projections of every layer wrapped by the
+    manager (``LinearWithLoRA``, HIP backend) and its RMSNorms on the HIP
+    kernel.  A step is one packed forward (``Decoder.forward_mixed``) of 2
+    prompts of 512 tokens and 64 decode rows (position 512 over their own
+    KV caches): base GEMMs, attention, norms, every LoRA delta, LM head on
+    the 66 next-token rows.  Every step draws 66 requests from Zipf(1.1)
+    over 512 adapters, makes them resident in the 128-slot pool (LRU
+    eviction; misses are uploaded from pinned host banks by the copy stream
+    and the scatter kernel), rewrites the resident segment table (66
+    segments, one per request, in row order) and replays the captured
+    forward.  Host banks: the 512 adapter names share 16 distinct weight
+    sets, so host memory stays at 1.3 GB while every miss still moves its
+    84 MB over PCIe.
     """
     import statistics
 
     import torch
 
-    from multi_lora_amd import AdapterWeights, HipLoRABackend, LoRAMemoryPool, write_kernel_input_metadata
-    from multi_lora_amd.batch_info import empty_kernel_input_metadata
+    from multi_lora_amd import AdapterWeights, MultiLoRAManager, set_lora_enabled, write_kernel_input_metadata
+    from multi_lora_amd.decoder import Decoder, DecoderConfig, StaticKV
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    H, I, KV, L, K, R, N_AD = 4096, 14336, 1024, 32, 128, 16, 512
-    proj = {"q": (H, H), "k": (H, KV), "v": (H, KV), "o": (H, H), "gate": (H, I), "up": (H, I), "down": (I, H)}
+    cfg = DecoderConfig.llama3_8b()
+    L, R, K, N_AD, SETS = cfg.num_hidden_layers, 16, 128, 512, 16
+    torch.manual_seed(4)
+    with torch.device(dev):
+        model = Decoder(cfg)
+    model = model.to(torch.bfloat16).eval()
+    names7 = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+              "mlp.up_proj", "mlp.down_proj")
+    dims = {f"layers.{l}.{n}": (model.get_submodule(f"layers.{l}.{n}").in_features,
+                                model.get_submodule(f"layers.{l}.{n}").out_features) for l in range(L) for n in names7}
     g = torch.Generator().manual_seed(4)
-    sets = []
-    for _ in range(16):
-        sets.append({f"layers.{l}.{n}": ((torch.randn(R, i, generator=g) * i ** -0.5).bfloat16(),
-                                         (torch.randn(o, R, generator=g) * 0.02).bfloat16())
-                     for l in range(L) for n, (i, o) in proj.items()})
-    shared = [AdapterWeights(rank=R, scaling=2.0, modules=m) for m in sets]
-    store = {f"a{i}": shared[i % len(shared)] for i in range(N_AD)}
-    pool = LoRAMemoryPool(K, R, dev, torch.bfloat16)
+    shared = [AdapterWeights(rank=R, scaling=2.0, modules={
+        k: ((torch.randn(R, i, generator=g) * i ** -0.5).bfloat16(), (torch.randn(o, R, generator=g) * 0.02).bfloat16())
+        for k, (i, o) in dims.items()}) for _ in range(SETS)]
+    store = {f"a{i}": shared[i % SETS] for i in range(N_AD)}
+    mgr = MultiLoRAManager.from_adapters(model, store, max_loras_per_batch=K, max_lora_rank=R)
+    pool, be = mgr.pool, mgr._lora_backend
     zipf = torch.tensor([(i + 1) ** -1.1 for i in range(N_AD)])
     lens = [512, 512] + [1] * 64
     rows = sum(lens)
@@ -114,99 +124,94 @@ def bench_c5_step(args) -> int:
     def draw():
         return [f"a{i}" for i in torch.multinomial(zipf, len(lens), replacement=True, generator=g).tolist()]
 
-    names = draw()
-    pool.prepare_lora_batch(list(dict.fromkeys(names)), weight_store=store)
-    meta = write_kernel_input_metadata(empty_kernel_input_metadata(device=dev, dtype=torch.bfloat16),
-                                       pool.build_batch_info(names), device=dev, dtype=torch.bfloat16, seq_lens=lens)
-    be = HipLoRABackend()
+    def setup(names):
+        """The manager's per-step setup, one segment per request (no merging of
+        neighbours, so the captured launch shapes hold for every step)."""
+        pool.prepare_lora_batch(list(dict.fromkeys(names)), weight_store=mgr._weight_store)
+        return write_kernel_input_metadata(mgr._resident_meta, pool.build_batch_info(names), device=dev,
+                                           dtype=torch.bfloat16, seq_lens=lens)
+
+    mgr._resident_meta = setup(draw())
+    meta = mgr._resident_meta
     be.set_kernel_input_metadata(meta)
-    bufs = [{n: pool.get_module_buffers(f"layers.{l}.{n}") for n in proj} for l in range(L)]
-    x_h = torch.randn(rows, H, device=dev).bfloat16()
-    x_i = torch.randn(rows, I, device=dev).bfloat16()
-    out_qkv = torch.zeros(rows, H + 2 * KV, device=dev, dtype=torch.bfloat16)
-    out_o = torch.zeros(rows, H, device=dev, dtype=torch.bfloat16)
-    out_gu = torch.zeros(rows, 2 * I, device=dev, dtype=torch.bfloat16)
-    out_down = torch.zeros(rows, H, device=dev, dtype=torch.bfloat16)
+    for key, wrapper in mgr.lora_wrappers.items():
+        wrapper.set_lora_info(be, *pool.get_module_buffers(key))
+    prompts = torch.randint(0, cfg.vocab_size, (2, 512), device=dev)
+    decode_ids = torch.randint(0, cfg.vocab_size, (64, 1), device=dev)
+    kv = StaticKV(cfg, 64, 520, dev, torch.bfloat16)
+    pos = torch.tensor([512], device=dev)
     stream = torch.cuda.current_stream(dev)
+    out = {}
 
-    def qkv(i):
-        p = bufs[i % L]
-        be.apply_lora_multi(x_h, [p["q"][0], p["k"][0], p["v"][0]], [p["q"][1], p["k"][1], p["v"][1]], out_qkv,
-                            [0, H, H + KV])
+    def forward(_):
+        out["logits"] = model.forward_mixed(prompts, decode_ids, kv, pos)
 
-    def o(i):
-        be.apply_lora(x_h, bufs[i % L]["o"][0], bufs[i % L]["o"][1], out_o)
+    with torch.inference_mode():
+        g_fwd = capture(torch, forward, 1)
+        set_lora_enabled(False)
+        try:
+            g_base = capture(torch, forward, 1)
+        finally:
+            set_lora_enabled(True)
 
-    def gate_up(i):
-        p = bufs[i % L]
-        be.apply_lora_multi(x_h, [p["gate"][0], p["up"][0]], [p["gate"][1], p["up"][1]], out_gu, [0, I])
+        # Serving loop: warm the pool to its steady state, then time steps.
+        warm, timed = 96, max(20, min(args.steps // 20, 60))
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(timed)]
+        step_ms, misses = [], []
+        bank_bytes = pool.buffers.layout(R).total * 2
+        for it in range(warm + timed):
+            names = draw()
+            before = set(pool.name_to_slot)
+            k = it - warm
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            if k >= 0:
+                ev[k][0].record(stream)
+            assert setup(names) is meta
+            if k >= 0:
+                ev[k][1].record(stream)
+            g_fwd.replay()
+            if k >= 0:
+                ev[k][2].record(stream)
+            torch.cuda.synchronize()
+            if k >= 0:
+                step_ms.append((time.perf_counter() - t0) * 1e3)
+                misses.append(sum(1 for n in dict.fromkeys(names) if n not in before))
+        finite = bool(torch.isfinite(out["logits"]).all())
+        upload_ms = [a[0].elapsed_time(a[1]) for a in ev]
+        fwd_ms = [a[1].elapsed_time(a[2]) for a in ev]
+        miss_steps = [(u, m) for u, m in zip(upload_ms, misses) if m > 0]
+        h2d = (sum(m for _, m in miss_steps) * bank_bytes / (sum(u for u, _ in miss_steps) * 1e-3) / 1e9
+               if miss_steps else None)
 
-    def down(i):
-        be.apply_lora(x_i, bufs[i % L]["down"][0], bufs[i % L]["down"][1], out_down)
+        # The forward alone (adapters resident), with and without the LoRA deltas.
+        reps = max(10, min(args.steps // 20, 50))
+        t_fwd = time_graph(torch, g_fwd, reps, 1, stream)
+        t_base = time_graph(torch, g_base, reps, 1, stream)
 
-    def step(i):
-        for fn in (qkv, o, gate_up, down):
-            fn(i)
+        # Per-projection LoRA calls at this batch's shapes, 32 layers each.
+        used = len({int(s) for s in meta.weight_indices[: meta.bs].tolist()})
+        xs = {4096: torch.randn(rows, 4096, device=dev).bfloat16(), 14336: torch.randn(rows, 14336, device=dev).bfloat16()}
+        e = 2
+        kernels = {}
+        for n in names7:
+            i, o = dims[f"layers.0.{n}"]
+            y = torch.zeros(rows, o, device=dev, dtype=torch.bfloat16)
+            bufs = [pool.get_module_buffers(f"layers.{l}.{n}") for l in range(L)]
 
-    for i in range(2 * L):
-        step(i)
-    torch.cuda.synchronize()
-    g_step = capture(torch, step, L)  # one graph = every LoRA call of one step
+            def call(l, x=xs[i], y=y, bufs=bufs):
+                be.apply_lora(x, bufs[l % L][0], bufs[l % L][1], y)
 
-    # Serving loop: warm the pool to its steady state, then time steps.
-    warm, timed = 96, max(20, min(args.steps // 20, 60))
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(timed)]
-    step_ms, misses, host_ms = [], [], []
-    bank_bytes = pool.buffers.layout(R).total * 2
-    for it in range(warm + timed):
-        names = draw()
-        wanted = list(dict.fromkeys(names))
-        before = set(pool.name_to_slot)
-        t0 = time.perf_counter()
-        k = it - warm
-        if k >= 0:
-            ev[k][0].record(stream)
-        pool.prepare_lora_batch(wanted, weight_store=store)
-        if k >= 0:
-            ev[k][1].record(stream)
-        write_kernel_input_metadata(meta, pool.build_batch_info(names), device=dev, dtype=torch.bfloat16,
-                                    seq_lens=lens)
-        g_step.replay()
-        if k >= 0:
-            ev[k][2].record(stream)
-        th = time.perf_counter()
-        torch.cuda.synchronize()
-        if k >= 0:
-            step_ms.append((time.perf_counter() - t0) * 1e3)
-            host_ms.append((th - t0) * 1e3)
-            misses.append(sum(1 for n in wanted if n not in before))
-    upload_ms = [a[0].elapsed_time(a[1]) for a in ev]
-    lora_ms = [a[1].elapsed_time(a[2]) for a in ev]
-    miss_steps = [(u, m) for u, m in zip(upload_ms, misses) if m > 0]
-    h2d = (sum(m for _, m in miss_steps) * bank_bytes / (sum(u for u, _ in miss_steps) * 1e-3) / 1e9
-           if miss_steps else None)
-
-    # Kernel-time breakdown of the LoRA part (same batch shape, resident adapters).
-    reps = max(2, min(args.steps // 200, 20))
-    lora_step_ms = time_graph(torch, g_step, reps * L, L, stream) * L
-    used = len({int(s) for s in meta.weight_indices[: meta.bs].tolist()})
-    e = 2
-
-    def call_bytes(in_dim, outs):
-        return rows * in_dim * e + sum(used * R * in_dim * e + used * od * R * e + 2 * rows * od * e for od in outs)
-
-    per_layer = {"q|k|v": call_bytes(H, [H, KV, KV]), "o": call_bytes(H, [H]), "gate|up": call_bytes(H, [I, I]),
-                 "down": call_bytes(I, [H])}
-    kernels = {}
-    for name, fn in (("q|k|v", qkv), ("o", o), ("gate|up", gate_up), ("down", down)):
-        ms = time_graph(torch, capture(torch, fn, L), reps * L, L, stream)
-        kernels[name] = {"us_per_layer": round(ms * 1e3, 2), "us_per_step": round(ms * 1e3 * L, 1),
-                         "bytes_per_layer": per_layer[name], "GB/s": round(per_layer[name] / (ms * 1e-3) / 1e9, 1)}
-    step_bytes = L * sum(per_layer.values())
+            ms = time_graph(torch, capture(torch, call, L), reps * L, L, stream)
+            nbytes = rows * i * e + used * R * (i + o) * e + 2 * rows * o * e
+            kernels[n.split(".")[1]] = {"us_per_layer": round(ms * 1e3, 2), "us_per_step": round(ms * 1e3 * L, 1),
+                                        "bytes_per_layer": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    lora_calls_ms = sum(k["us_per_step"] for k in kernels.values()) / 1e3
+    step_bytes = L * sum(k["bytes_per_layer"] for k in kernels.values())
     dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
     med = statistics.median
     result = {
-        "metric": "c5 per-step latency (pool upload + every LoRA call of a 32-layer step)",
+        "metric": "c5 per-step latency (pool upload + 32-layer forward of the mixed batch)",
         "value": round(med(step_ms), 3),
         "unit": "ms",
         "n_gpus": 1,
@@ -217,22 +222,29 @@ def bench_c5_step(args) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
+        "data": "synthetic (random-init weights, random token ids)",
         "config": {"workload": OTHER_WORKLOADS["c5_step"], "rows": rows, "segments": len(lens),
-                   "timing": "wall clock per step (synchronised), events around the upload and the graph replay"},
-        "breakdown": {"upload_ms_median": round(med(upload_ms), 3), "lora_ms_median": round(med(lora_ms), 3),
-                      "host_enqueue_ms_median": round(med(host_ms), 3),
+                   "model": "decoder.Decoder(DecoderConfig.llama3_8b()): base GEMMs, fp32 attention, HIP RMSNorm, "
+                            "LoRA on q/k/v/o/gate/up/down, LM head on the 66 next-token rows",
+                   "timing": "wall clock per step (synchronised); events around the upload and the graph replay"},
+        "breakdown": {"upload_ms_median": round(med(upload_ms), 3), "forward_ms_median": round(med(fwd_ms), 3),
+                      "upload_share": round(med(upload_ms) / med(step_ms), 3),
                       "misses_per_step_mean": round(statistics.mean(misses), 2),
                       "miss_bytes_per_adapter": bank_bytes,
                       "h2d_GB/s_on_miss_steps": round(h2d, 1) if h2d else None},
-        "lora_only": {"ms_per_step": round(lora_step_ms, 3), "distinct_adapters": used,
-                      "algorithmic_bytes_per_step": step_bytes,
-                      "GB/s": round(step_bytes / (lora_step_ms * 1e-3) / 1e9, 1), "kernels": kernels},
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": kernels[dom]["GB/s"], "peak": HBM_PEAK_GBS,
+        "forward_resident": {"with_lora_ms": round(t_fwd, 3), "base_only_ms": round(t_base, 3),
+                             "lora_ms": round(t_fwd - t_base, 3),
+                             "lora_share_of_forward": round((t_fwd - t_base) / t_fwd, 3),
+                             "logits_finite": finite},
+        "lora_calls": {"ms_per_step": round(lora_calls_ms, 3), "distinct_adapters": used,
+                       "algorithmic_bytes_per_step": step_bytes,
+                       "GB/s": round(step_bytes / (lora_calls_ms * 1e-3) / 1e9, 1), "kernels": kernels},
+        "roofline": {"kernel": f"LoRA {dom}", "bound": "hbm", "achieved": kernels[dom]["GB/s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernels[dom]["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None},
     }
     print(json.dumps(result), flush=True)
     return 0
+
 
 def bench_pool_upload(args) -> int:
     """mlora_pool_scatter from device-resident stage rows (the kernel's own

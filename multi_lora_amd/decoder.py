@@ -11,7 +11,9 @@ projection is a plain ``nn.Linear`` named like Llama's
 manager wraps them with ``LinearWithLoRA`` exactly as it wraps a Hugging Face
 model, and ``fuse_rmsnorm`` routes the norms through the HIP RMSNorm.
 
-Attention is computed in fp32 from contiguous operands.  The KV cache is
+Attention runs its two products in the model dtype (fp32 accumulation,
+contiguous operands) with the softmax in fp32; the query heads that share a
+key head are stacked as rows, so keys are never repeated.  The KV cache is
 written in place at ``cache_position`` and read whole under a boolean mask,
 so a decode step touches fixed addresses and can be captured in a HIP graph.
 ``forward`` accepts the keyword arguments the reference passes to its model
@@ -95,26 +97,54 @@ class Attention(nn.Module):
         self.o_proj = nn.Linear(c.num_attention_heads * d, c.hidden_size, bias=False)
 
     def forward(self, x, cos, sin, mask, kv: Optional[StaticKV], layer: int, cache_position):
-        c = self.c
         b, t, _ = x.shape
+        out = self._attend(self.q_proj(x), self.k_proj(x), self.v_proj(x), b, t, cos, sin, mask, kv, layer,
+                           cache_position)
+        return self.o_proj(out.to(x.dtype))
+
+    def _attend(self, q, k, v, b, t, cos, sin, mask, kv: Optional[StaticKV], layer: int, cache_position):
+        """Rotary attention of ``b`` sequences of ``t`` rows (projections given
+        row-major, ``[b*t, heads*d]`` or ``[b, t, heads*d]``); writes this
+        step's keys and values into ``kv`` at ``cache_position`` and attends
+        over the whole cache under ``mask``.  Returns ``[b, t, heads*d]`` fp32."""
+        c = self.c
         h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
-        q = self.q_proj(x).view(b, t, h, d).transpose(1, 2).float()
-        k = self.k_proj(x).view(b, t, kvh, d).transpose(1, 2).float()
-        v = self.v_proj(x).view(b, t, kvh, d).transpose(1, 2)
-        q, k = _rotate(q, cos, sin), _rotate(k, cos, sin)
+        rep = h // kvh
+        dt = q.dtype
+        q = q.reshape(b, t, h, d).transpose(1, 2).float()
+        k = k.reshape(b, t, kvh, d).transpose(1, 2).float()
+        v = v.reshape(b, t, kvh, d).transpose(1, 2)
+        q, k = _rotate(q, cos, sin).to(dt), _rotate(k, cos, sin).to(dt)
         if kv is not None:
             kv.keys[layer].index_copy_(2, cache_position, k.to(kv.keys[layer].dtype))
             kv.values[layer].index_copy_(2, cache_position, v.to(kv.values[layer].dtype))
             k, v = kv.keys[layer], kv.values[layer]
-        rep = h // kvh
-        keys = k.float().repeat_interleave(rep, dim=1)                       # [b, h, L, d]
-        vals = v.float().repeat_interleave(rep, dim=1)
-        scores = torch.matmul(q, keys.transpose(-1, -2).contiguous()) / math.sqrt(d)   # [b, h, t, L]
-        scores = scores.masked_fill(~mask, float("-inf"))
-        probs = torch.softmax(scores, dim=-1)
-        out = torch.matmul(probs, vals)                                       # [b, h, t, d]
-        out = out.transpose(1, 2).reshape(b, t, h * d).to(x.dtype)
-        return self.o_proj(out)
+        length = k.shape[2]
+        # The query heads sharing a key head are stacked as rows, so keys and
+        # values are read once per key head, never repeated.
+        qg = q.reshape(b, kvh, rep * t, d)
+        keys_t = k.to(dt).transpose(-1, -2).contiguous()                     # [b, kvh, d, L]
+        scores = torch.matmul(qg, keys_t).float() / math.sqrt(d)              # [b, kvh, rep*t, L]
+        scores = scores.view(b, kvh, rep, t, length).masked_fill(~mask[:, :, None], float("-inf"))
+        probs = torch.softmax(scores, dim=-1).to(dt).view(b, kvh, rep * t, length)
+        out = torch.matmul(probs, v.to(dt).contiguous())                      # [b, kvh, rep*t, d]
+        return out.view(b, h, t, d).transpose(1, 2).reshape(b, t, h * d)
+
+    def forward_mixed(self, x, pre: "Packed", dec: "Packed", layer: int):
+        """Packed rows ``x [R, hidden]``: ``pre.n`` prompts of ``pre.t`` tokens,
+        then ``dec.n`` decode rows.  The projections (and their LoRA deltas)
+        run once over all rows; attention runs per part, prompts causally
+        over themselves, decode rows over their own KV caches."""
+        q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        outs = []
+        for part in (pre, dec):
+            if part.n == 0:
+                continue
+            rows = slice(part.row0, part.row0 + part.n * part.t)
+            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.cos, part.sin, part.mask, part.kv,
+                             layer, part.cache_position)
+            outs.append(o.reshape(part.n * part.t, -1))
+        return self.o_proj(torch.cat(outs).to(x.dtype))
 
 
 class MLP(nn.Module):
@@ -139,6 +169,24 @@ class Block(nn.Module):
     def forward(self, x, cos, sin, mask, kv, layer, cache_position):
         x = x + self.self_attn(self.input_layernorm(x), cos, sin, mask, kv, layer, cache_position)
         return x + self.mlp(self.post_attention_layernorm(x))
+
+    def forward_mixed(self, x, pre, dec, layer):
+        x = x + self.self_attn.forward_mixed(self.input_layernorm(x), pre, dec, layer)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+@dataclass
+class Packed:
+    """One part of a packed mixed batch: ``n`` sequences of ``t`` rows from row ``row0``."""
+
+    n: int
+    t: int
+    row0: int
+    cos: torch.Tensor
+    sin: torch.Tensor
+    mask: torch.Tensor
+    kv: Optional[StaticKV]
+    cache_position: Optional[torch.Tensor]
 
 
 class Decoder(nn.Module):
@@ -172,6 +220,40 @@ class Decoder(nn.Module):
         for i, layer in enumerate(self.layers):
             x = layer(x, cos, sin, mask, kv, i, cache_position)
         return SimpleNamespace(logits=self.lm_head(self.norm(x)))
+
+    def _rope(self, positions: torch.Tensor):
+        """cos, sin ``[b, 1, t, head_dim]`` for integer positions ``[b, t]``."""
+        ang = positions.float()[..., None] * self.inv_freq
+        ang = torch.cat((ang, ang), dim=-1)[:, None]
+        return ang.cos(), ang.sin()
+
+    def forward_mixed(self, prompt_ids: torch.Tensor, decode_ids: torch.Tensor, decode_kv: StaticKV,
+                      decode_pos: torch.Tensor):
+        """One serving step over a mixed batch, rows packed as the segment table
+        lists them: every prompt's tokens (``prompt_ids [p, t]``, positions
+        0..t-1, causal within the prompt), then one row per decode sequence
+        (``decode_ids [d, 1]``) at position ``decode_pos`` (a 1-element device
+        tensor), attending over its KV cache ``decode_kv`` (written there).
+        Returns logits ``[p + d, vocab]`` for each prompt's last token and each
+        decode row.  Every shape is fixed by the arguments' shapes, so the
+        step can be captured in a graph and replayed with new ids and a new
+        ``decode_pos``."""
+        dev = prompt_ids.device
+        p, t = prompt_ids.shape
+        d = decode_ids.shape[0]
+        x = torch.cat((self.embed_tokens(prompt_ids).reshape(p * t, -1),
+                       self.embed_tokens(decode_ids).reshape(d, -1)))
+        pos = torch.arange(t, device=dev)
+        cos, sin = self._rope(pos.view(1, t))
+        causal = (pos[None, :] <= pos[:, None]).view(1, 1, t, t)
+        pre = Packed(p, t, 0, cos, sin, causal, None, None)
+        cos_d, sin_d = self._rope(decode_pos.view(1, 1))
+        seen = (torch.arange(decode_kv.max_len, device=dev) <= decode_pos).view(1, 1, 1, -1)
+        dec = Packed(d, 1, p * t, cos_d, sin_d, seen, decode_kv, decode_pos)
+        for i, layer in enumerate(self.layers):
+            x = layer.forward_mixed(x, pre, dec, i)
+        last = torch.cat((torch.arange(t - 1, p * t, t, device=dev), torch.arange(p * t, p * t + d, device=dev)))
+        return self.lm_head(self.norm(x[last]))
 
     @staticmethod
     def _mask(attention_mask, b, t, length, cache_position, dev) -> torch.Tensor:

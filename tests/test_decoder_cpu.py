@@ -41,3 +41,34 @@ def test_padding_mask_hides_positions():
     ids2[:, 1] = (ids2[:, 1] + 5) % 97
     b = m(input_ids=ids2, attention_mask=mask, use_cache=False).logits[:, -1]
     torch.testing.assert_close(a, b)
+
+
+@torch.inference_mode()
+def test_mixed_step_equals_separate_prefill_and_decode():
+    """One packed step (2 prompts of 7 tokens, then 3 decode rows at position
+    5 over their own caches) gives the logits of running the prompts and the
+    decode rows through the ordinary forward separately, and writes the same
+    KV entries."""
+    m = model()
+    g = torch.Generator().manual_seed(3)
+    prompts = torch.randint(0, 97, (2, 7), generator=g)
+    history = torch.randint(0, 97, (3, 5), generator=g)
+    nxt = torch.randint(0, 97, (3, 1), generator=g)
+    want_p = m(input_ids=prompts, use_cache=False).logits[:, -1]
+    kv_ref = StaticKV(m.config, 3, 12, "cpu", torch.float32)
+    m(input_ids=history, past_key_values=kv_ref, cache_position=torch.arange(5))
+    kv = StaticKV(m.config, 3, 12, "cpu", torch.float32)
+    for layer in range(m.config.num_hidden_layers):
+        kv.keys[layer].copy_(kv_ref.keys[layer])
+        kv.values[layer].copy_(kv_ref.values[layer])
+    pos = torch.tensor([5])
+    mask = (torch.arange(12) <= pos).view(1, 1, 1, -1).expand(3, 1, 1, 12)
+    want_d = m(input_ids=nxt, attention_mask=mask, position_ids=pos.view(1, 1).expand(3, 1), past_key_values=kv_ref,
+               cache_position=pos).logits[:, 0]
+    got = m.forward_mixed(prompts, nxt, kv, pos)
+    assert got.shape == (5, 97)
+    torch.testing.assert_close(got[:2], want_p, atol=2e-5, rtol=2e-5)
+    torch.testing.assert_close(got[2:], want_d, atol=2e-5, rtol=2e-5)
+    for layer in range(m.config.num_hidden_layers):
+        torch.testing.assert_close(kv.keys[layer], kv_ref.keys[layer], atol=1e-6, rtol=1e-6)
+        torch.testing.assert_close(kv.values[layer], kv_ref.values[layer], atol=1e-6, rtol=1e-6)

@@ -95,3 +95,38 @@ def test_adapters_change_the_decode(dev):
         lg = out.logits[:, -1].float()
         assert torch.allclose(lg[0], lg[2], atol=1e-5)
         assert (lg[0] - lg[1]).abs().max() > 1e-3 and (lg[0] - lg[3]).abs().max() > 1e-3
+
+
+def test_mixed_step_with_adapters_equals_separate_runs(dev):
+    """The packed serving step of the 32-layer benchmark, on the small model:
+    2 prompts and 3 decode rows in one forward, each row with its adapter
+    (HIP kernels, one segment table over the packed rows), give the logits of
+    running the prompts and the decode rows through the manager separately."""
+    from multi_lora_amd.decoder import StaticKV
+
+    mgr, cfg = build(torch.float32)
+    g = torch.Generator().manual_seed(7)
+    prompts = torch.randint(0, cfg.vocab_size, (2, 6), generator=g).to("cuda")
+    history = torch.randint(0, cfg.vocab_size, (3, 4), generator=g).to("cuda")
+    nxt = torch.randint(0, cfg.vocab_size, (3, 1), generator=g).to("cuda")
+    names_p, names_d = ["a", "b"], ["b", None, "a"]
+    with torch.inference_mode():
+        want_p = mgr.forward_with_lora(input_ids=prompts, lora_names=names_p, seq_lens=[6, 6],
+                                       use_cache=False).logits[:, -1]
+        kv_ref = StaticKV(cfg, 3, 8, "cuda", torch.float32)
+        mgr.forward_with_lora(input_ids=history, lora_names=names_d, seq_lens=[4] * 3, past_key_values=kv_ref,
+                              cache_position=torch.arange(4, device="cuda"))
+        kv = StaticKV(cfg, 3, 8, "cuda", torch.float32)
+        for layer in range(cfg.num_hidden_layers):
+            kv.keys[layer].copy_(kv_ref.keys[layer])
+            kv.values[layer].copy_(kv_ref.values[layer])
+        pos = torch.tensor([4], device="cuda")
+        mask = (torch.arange(8, device="cuda") <= pos).view(1, 1, 1, -1).expand(3, 1, 1, 8)
+        want_d = mgr.forward_with_lora(input_ids=nxt, lora_names=names_d, seq_lens=[1] * 3, attention_mask=mask,
+                                       position_ids=pos.view(1, 1).expand(3, 1), past_key_values=kv_ref,
+                                       cache_position=pos).logits[:, 0]
+        mgr._setup_forward_batch(names_p + names_d, seq_lens=[6, 6, 1, 1, 1])
+        got = mgr.model.forward_mixed(prompts, nxt, kv, pos)
+    torch.testing.assert_close(got[:2], want_p, atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(got[2:], want_d, atol=1e-4, rtol=1e-4)
+    assert (want_d[0] - want_d[1]).abs().max() > 1e-3  # the adapters matter

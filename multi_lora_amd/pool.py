@@ -84,6 +84,7 @@ class _GpuBuffers:
         self._stage: Optional[torch.Tensor] = None
         self._copy_stream = None
         self._load_event = None
+        self._last_read: Dict[int, "torch.cuda.Event"] = {}
         # Release the per-module host tensors once an adapter is packed into
         # its bank, so host memory holds one copy of the weights.
         self.release_modules = True
@@ -117,11 +118,28 @@ class _GpuBuffers:
         if self._copy_stream is None:
             self._copy_stream = torch.cuda.Stream(device=self.device)
             self._load_event = torch.cuda.Event()
-        # Slots being overwritten may still be read by queued compute work.
-        self._copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+        # A slot being overwritten may still be read by queued compute work:
+        # wait for the last compute that read it, and nothing else, so an
+        # upload overlaps compute on the other slots.
+        waited = set()
+        for slot, _ in pairs:
+            ev = self._last_read.get(slot)
+            if ev is not None and id(ev) not in waited:
+                self._copy_stream.wait_event(ev)
+                waited.add(id(ev))
         with torch.cuda.stream(self._copy_stream):
             self._load(pairs, non_blocking=True)
         self._load_event.record(self._copy_stream)
+
+    def mark_read(self, slots: Iterable[int]) -> None:
+        """Record that compute enqueued so far on the current stream reads ``slots``."""
+        slots = list(slots)
+        if self.device.type != "cuda" or not slots:
+            return
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        for slot in slots:
+            self._last_read[slot] = ev
 
     def wait_load(self) -> None:
         """Make the compute stream wait for the last upload."""
@@ -219,7 +237,8 @@ class _GpuBuffers:
     def _scatter_staged(self, stage: torch.Tensor, slots: List[int], plan: _RankPlan) -> None:
         """One launch: staged rows [0, len(slots)) into their slots, every key."""
         table = self._key_table(plan)
-        slots_dev = torch.tensor(slots, dtype=torch.int32, device=self.device)
+        # From pinned memory, so the host does not wait for the copies queued before it.
+        slots_dev = torch.tensor(slots, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
         rc = _ffi.lib().mlora_pool_scatter(
             stage.data_ptr(), stage.stride(0), len(slots), slots_dev.data_ptr(), table.data_ptr(), len(plan.keys),
             plan.rank, self.max_loras_per_batch, plan.max_numel, _ffi.dtype_code(self.dtype),
@@ -257,6 +276,7 @@ class LoRAMemoryPool:
         self.slot_names: Dict[int, LoraName] = {}
         self._slot_rank_scaling: Dict[int, Tuple[int, float]] = {}
         self.buffers = _GpuBuffers(max_loras_per_batch, max_lora_rank, self.device, dtype)
+        self._batch_slots: List[int] = []
 
     def get_slot_id(self, name: LoraName) -> int:
         if name not in self.name_to_slot:
@@ -280,9 +300,18 @@ class LoRAMemoryPool:
 
         Adapters are visited in the iteration order of ``lora_names`` (pass an
         ordered, de-duplicated list for a reproducible slot assignment).  All
-        uploads of the batch are issued together, then the compute stream is
-        ordered after them.
+        uploads of the batch are issued together on the copy stream, then the
+        current (compute) stream is ordered after them.
+
+        Ordering against compute: a batch's slots count as read by all compute
+        enqueued on the current stream until the next call; an upload into an
+        evicted slot waits for the compute that last read that slot and for
+        nothing else.  So the next batch can be prepared while this batch's
+        forward is still running, and its uploads overlap that forward
+        unless they evict one of its adapters.
         """
+        # The previous batch's slots are read by the compute enqueued since it was prepared.
+        self.buffers.mark_read(self._batch_slots)
         wanted = list(dict.fromkeys(lora_names))
         keep = set(wanted)
         for name in wanted:
@@ -305,6 +334,7 @@ class LoRAMemoryPool:
             pairs.append((slot, weights))
         self.buffers.write_many(pairs)
         self.buffers.wait_load()
+        self._batch_slots = [self.name_to_slot[n] for n in wanted]
 
     def build_batch_info(self, lora_names: List[LoraName]) -> BatchLoRAInfo:
         """Slot per segment; rank and scaling per slot (empty slots: 0, 0.0)."""

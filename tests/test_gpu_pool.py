@@ -91,3 +91,25 @@ def test_scatter_entry_point_direct(dev):
     want_b[1, :, :rank] = row[b_off:b_off + out_dim * rank].view(out_dim, rank)
     assert torch.equal(a.cpu(), want_a) and torch.equal(b.cpu(), want_b)
     assert ctypes.sizeof(_ffi.PoolKey) == 64
+
+
+def test_upload_into_an_evicted_slot_waits_for_the_compute_reading_it(dev):
+    """Compute enqueued after a batch was prepared reads that batch's slots;
+    preparing the next batch evicts one of them, and its upload (on the copy
+    stream) must not land before that compute has read the slot."""
+    dims = {"q_proj": (256, 128)}
+    st = {"a": adapter(1, 8, dims, torch.float32), "b": adapter(2, 8, dims, torch.float32)}
+    a_rows = st["a"].modules["q_proj"][0].clone()
+    b_rows = st["b"].modules["q_proj"][0].clone()
+    pool = LoRAMemoryPool(1, 8, dev, torch.float32)
+    pool.prepare_lora_batch(["a"], weight_store=st)
+    slot_a = pool.get_module_buffers("q_proj")[0][0]
+    busy = torch.randn(2048, 2048, device=dev)
+    for _ in range(30):  # keeps the compute stream busy for a while before the read below
+        busy = torch.tanh(busy @ busy * 1e-3)
+    seen = slot_a.clone()  # reads the slot after the long work
+    pool.prepare_lora_batch(["b"], weight_store=st)  # evicts "a": slot 0 gets b's rows
+    torch.cuda.synchronize()
+    assert torch.equal(seen.cpu(), a_rows)
+    assert torch.equal(pool.get_module_buffers("q_proj")[0][0].cpu(), b_rows)
+    assert pool.get_slot_id("b") == 0 and "a" not in pool.name_to_slot

@@ -95,7 +95,8 @@ def bench_c5_step(args) -> int:
 
     import torch
 
-    from multi_lora_amd import AdapterWeights, MultiLoRAManager, set_lora_enabled, write_kernel_input_metadata
+    from multi_lora_amd import (AdapterWeights, MultiLoRAManager, fuse_gate_up_projections, fuse_qkv_projections,
+                                set_lora_enabled, write_kernel_input_metadata)
     from multi_lora_amd.decoder import Decoder, DecoderConfig, StaticKV
 
     dev = torch.device("cuda", 0)
@@ -116,6 +117,10 @@ def bench_c5_step(args) -> int:
         for k, (i, o) in dims.items()}) for _ in range(SETS)]
     store = {f"a{i}": shared[i % SETS] for i in range(N_AD)}
     mgr = MultiLoRAManager.from_adapters(model, store, max_loras_per_batch=K, max_lora_rank=R)
+    # q|k|v and gate|up as one base GEMM and one multi-slice LoRA call each,
+    # for every input shape (the mixed batch included).
+    assert fuse_qkv_projections(mgr.lora_wrappers, all_shapes=True) == L
+    assert fuse_gate_up_projections(mgr.lora_wrappers) == L
     pool, be = mgr.pool, mgr._lora_backend
     zipf = torch.tensor([(i + 1) ** -1.1 for i in range(N_AD)])
     lens = [512, 512] + [1] * 64
@@ -204,23 +209,28 @@ def bench_c5_step(args) -> int:
         t_fwd = time_graph(torch, g_fwd, reps, 1, stream)
         t_base = time_graph(torch, g_base, reps, 1, stream)
 
-        # Per-projection LoRA calls at this batch's shapes, 32 layers each.
+        # The LoRA calls of one layer at this batch's shapes, as the fused
+        # model makes them (q|k|v and gate|up multi-slice), 32 layers each.
         used = len({int(s) for s in meta.weight_indices[: meta.bs].tolist()})
         xs = {4096: torch.randn(rows, 4096, device=dev).bfloat16(), 14336: torch.randn(rows, 14336, device=dev).bfloat16()}
         e = 2
         kernels = {}
-        for n in names7:
-            i, o = dims[f"layers.0.{n}"]
-            y = torch.zeros(rows, o, device=dev, dtype=torch.bfloat16)
-            bufs = [pool.get_module_buffers(f"layers.{l}.{n}") for l in range(L)]
+        groups = {"q|k|v": names7[0:3], "o": names7[3:4], "gate|up": names7[4:6], "down": names7[6:7]}
+        for gname, projs in groups.items():
+            i = dims[f"layers.0.{projs[0]}"][0]
+            outs = [dims[f"layers.0.{p}"][1] for p in projs]
+            cols = [sum(outs[:k]) for k in range(len(outs))]
+            y = torch.zeros(rows, sum(outs), device=dev, dtype=torch.bfloat16)
+            bufs = [[pool.get_module_buffers(f"layers.{l}.{p}") for p in projs] for l in range(L)]
 
-            def call(l, x=xs[i], y=y, bufs=bufs):
-                be.apply_lora(x, bufs[l % L][0], bufs[l % L][1], y)
+            def call(l, x=xs[i], y=y, bufs=bufs, cols=cols):
+                ab = bufs[l % L]
+                be.apply_lora_multi(x, [t[0] for t in ab], [t[1] for t in ab], y, cols)
 
             ms = time_graph(torch, capture(torch, call, L), reps * L, L, stream)
-            nbytes = rows * i * e + used * R * (i + o) * e + 2 * rows * o * e
-            kernels[n.split(".")[1]] = {"us_per_layer": round(ms * 1e3, 2), "us_per_step": round(ms * 1e3 * L, 1),
-                                        "bytes_per_layer": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+            nbytes = rows * i * e + sum(used * R * (i + o) * e + 2 * rows * o * e for o in outs)
+            kernels[gname] = {"us_per_layer": round(ms * 1e3, 2), "us_per_step": round(ms * 1e3 * L, 1),
+                              "bytes_per_layer": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     lora_calls_ms = sum(k["us_per_step"] for k in kernels.values()) / 1e3
     step_bytes = L * sum(k["bytes_per_layer"] for k in kernels.values())
     dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
@@ -239,8 +249,9 @@ def bench_c5_step(args) -> int:
         "dtype": "bf16",
         "data": "synthetic (random-init weights, random token ids)",
         "config": {"workload": OTHER_WORKLOADS["c5_step"], "rows": rows, "segments": len(lens),
-                   "model": "decoder.Decoder(DecoderConfig.llama3_8b()): base GEMMs, fp32 attention, HIP RMSNorm, "
-                            "LoRA on q/k/v/o/gate/up/down, LM head on the 66 next-token rows",
+                   "model": "decoder.Decoder(DecoderConfig.llama3_8b()): base GEMMs (q|k|v and gate|up fused), "
+                            "attention, HIP RMSNorm, LoRA on q/k/v/o/gate/up/down (q|k|v and gate|up as multi-slice "
+                            "calls), LM head on the 66 next-token rows",
                    "timing": "wall clock per step (synchronised); events around the upload and the graph replay"},
         "breakdown": {"upload_ms_median": round(med(upload_ms), 3), "forward_ms_median": round(med(fwd_ms), 3),
                       "upload_share": round(med(upload_ms) / med(step_ms), 3),

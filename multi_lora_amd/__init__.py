@@ -14,7 +14,8 @@ from .batch_info import (
     write_kernel_input_metadata,
 )
 from .eviction import EvictionPolicy
-from .layers import LinearWithLoRA, QKVProjGroup, fuse_qkv_projections, lora_delta, set_lora_enabled
+from .layers import (LinearWithLoRA, QKVProjGroup, fuse_gate_up_projections, fuse_qkv_projections, lora_delta,
+                     set_lora_enabled)
 from .manager import MultiLoRAManager
 from .pool import LoRAMemoryPool
 from .weights import AdapterWeights
@@ -32,6 +33,7 @@ __all__ = [
     "QKVProjGroup",
     "empty_kernel_input_metadata",
     "fill_column",
+    "fuse_gate_up_projections",
     "fuse_qkv_projections",
     "get_lora_backend",
     "group_rows",

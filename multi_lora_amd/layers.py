@@ -73,9 +73,16 @@ class LinearWithLoRA(nn.Module):
 
 
 class QKVProjGroup:
-    """One base GEMM for q/k/v of an attention block (decode only; bias-free)."""
+    """One base GEMM and one multi-slice LoRA call for sibling projections
+    that read the same input: q/k/v of an attention block
+    (multi_lora/layers.py:91-142), or gate/up of an MLP.  Bias-free.
 
-    def __init__(self, wrappers: List[LinearWithLoRA]) -> None:
+    Decode-shaped inputs (one row per sequence) always take the fused path,
+    as in the reference.  With ``all_shapes`` every input does: prefill and
+    mixed batches then read x once for all slices, in one library call.
+    """
+
+    def __init__(self, wrappers: List[LinearWithLoRA], all_shapes: bool = False) -> None:
         if any(w.base_layer.bias is not None for w in wrappers):
             raise RuntimeError("QKV fusion requires bias=None")
         self.wrappers = list(wrappers)
@@ -91,6 +98,7 @@ class QKVProjGroup:
         self._cached_x: Optional[torch.Tensor] = None
         self._cached_out: Optional[torch.Tensor] = None
         self._delta_done = False
+        self.all_shapes = all_shapes
 
     def _multi_ready(self) -> bool:
         first = self.wrappers[0]
@@ -102,7 +110,7 @@ class QKVProjGroup:
         )
 
     def forward(self, wrapper: LinearWithLoRA, x: torch.Tensor) -> torch.Tensor:
-        if x.shape[-2] != 1:
+        if x.shape[-2] != 1 and not self.all_shapes:
             return wrapper.add_delta(x, wrapper.base_layer(x))
         if self._cached_x is not x:
             self._cached_x = x
@@ -128,19 +136,32 @@ class QKVProjGroup:
 
 
 QKV_LEAVES = ("q_proj", "k_proj", "v_proj")
+GATE_UP_LEAVES = ("gate_proj", "up_proj")
 
 
-def fuse_qkv_projections(wrappers: Dict[str, LinearWithLoRA]) -> int:
+def _fuse_siblings(wrappers: Dict[str, LinearWithLoRA], leaves, all_shapes: bool) -> int:
+    """Group the wrappers named ``<parent>.<leaf>`` by parent; every parent
+    holding all of ``leaves`` becomes one group, in ``leaves`` order."""
+    blocks: Dict[str, Dict[str, LinearWithLoRA]] = {}
+    for name, wrapper in wrappers.items():
+        parent, dot, leaf = name.rpartition(".")
+        if dot and leaf in leaves and wrapper.qkv_group is None:
+            blocks.setdefault(parent, {})[leaf] = wrapper
+    complete = [block for block in blocks.values() if len(block) == len(leaves)]
+    for block in complete:
+        QKVProjGroup([block[leaf] for leaf in leaves], all_shapes=all_shapes)
+    return len(complete)
+
+
+def fuse_qkv_projections(wrappers: Dict[str, LinearWithLoRA], all_shapes: bool = False) -> int:
     """Fuse the base GEMMs of every attention block whose q, k and v
     projections are all wrapped (multi_lora/layers.py:128-142); returns the
     number of blocks fused.  Wrappers are matched by their parent module's
     name, so ``...self_attn.q_proj`` joins ``...self_attn.k_proj``."""
-    blocks: Dict[str, Dict[str, LinearWithLoRA]] = {}
-    for name, wrapper in wrappers.items():
-        parent, dot, leaf = name.rpartition(".")
-        if dot and leaf in QKV_LEAVES:
-            blocks.setdefault(parent, {})[leaf] = wrapper
-    complete = [block for block in blocks.values() if len(block) == len(QKV_LEAVES)]
-    for block in complete:
-        QKVProjGroup([block[leaf] for leaf in QKV_LEAVES])
-    return len(complete)
+    return _fuse_siblings(wrappers, QKV_LEAVES, all_shapes)
+
+
+def fuse_gate_up_projections(wrappers: Dict[str, LinearWithLoRA], all_shapes: bool = True) -> int:
+    """The same for every MLP whose gate and up projections are both wrapped:
+    one base GEMM and one two-slice LoRA call over their shared input."""
+    return _fuse_siblings(wrappers, GATE_UP_LEAVES, all_shapes)

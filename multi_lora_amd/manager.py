@@ -33,7 +33,7 @@ from .batch_info import (
     group_rows,
     write_kernel_input_metadata,
 )
-from .layers import LinearWithLoRA, fuse_qkv_projections
+from .layers import LinearWithLoRA, fuse_gate_up_projections, fuse_qkv_projections
 from .pool import LoRAMemoryPool, LoraName
 from .weights import AdapterWeights
 
@@ -111,8 +111,13 @@ class MultiLoRAManager:
                 wrapper = LinearWithLoRA(module)
                 setattr(parent, child, wrapper)
                 self.lora_wrappers[name] = wrapper
-        if os.environ.get("MULTI_LORA_FUSED_QKV", "0") == "1":
-            fuse_qkv_projections(self.lora_wrappers)
+        # "1": q/k/v fused for decode-shaped inputs (the reference's switch);
+        # "all": for every input.  Gate/up: "1" or "all" fuses every input.
+        fused_qkv = os.environ.get("MULTI_LORA_FUSED_QKV", "0")
+        if fused_qkv in ("1", "all"):
+            fuse_qkv_projections(self.lora_wrappers, all_shapes=fused_qkv == "all")
+        if os.environ.get("MULTI_LORA_FUSED_GATE_UP", "0") in ("1", "all"):
+            fuse_gate_up_projections(self.lora_wrappers)
         if os.environ.get("MULTI_LORA_FUSED_NORM", "1") == "1" and self.pool.device.type == "cuda":
             from .kernels.rmsnorm import fuse_rmsnorm
 

@@ -132,3 +132,42 @@ def test_no_cpu_fallback():
     hip.set_kernel_input_metadata(wl.meta)
     with pytest.raises(RuntimeError):
         hip.apply_lora(wl.x, wl.a_stacks[0], wl.b_stacks[0], wl.clone_base())
+
+
+@pytest.mark.parametrize("leaves,lens", [
+    (("q_proj", "k_proj", "v_proj"), [20, 20, 20]),       # prefill: 3 sequences of 20 tokens
+    (("gate_proj", "up_proj"), [40, 1, 1, 1, 17]),        # mixed: prefill rows and decode rows
+])
+def test_fused_groups_on_every_shape_equal_separate_layers(dev, leaves, lens):
+    """With all_shapes, prefill and mixed batches take the fused base GEMM and
+    one multi-slice LoRA call; each layer's output equals its separate
+    forward (the LoRA part bit for bit in the kernels' order, the base GEMM to
+    bf16 rounding)."""
+    from multi_lora_amd.layers import _fuse_siblings
+    from multi_lora_amd.synthetic import make_meta
+
+    prefix = "model.layers.0.blk."
+    dims = dict(zip(leaves, (256, 64, 64)[: len(leaves)] if len(leaves) == 3 else (192, 192)))
+    torch.manual_seed(1)
+    wrappers = {prefix + n: LinearWithLoRA(nn.Linear(128, d, bias=False).to(dev, torch.bfloat16))
+                for n, d in dims.items()}
+    rows = sum(lens)
+    slots = [i % 3 for i in range(len(lens))]
+    meta = make_meta(lens, slots, [8, 8, 0, 8], [2.0, 1.0, 0.0, 0.5], dev, torch.bfloat16)
+    hip = HipLoRABackend()
+    hip.set_kernel_input_metadata(meta)
+    g = torch.Generator().manual_seed(5)
+    for n, d in dims.items():
+        a = (torch.randn(4, 8, 128, generator=g) * 0.1).to(dev, torch.bfloat16)
+        b = (torch.randn(4, d, 8, generator=g) * 0.1).to(dev, torch.bfloat16)
+        wrappers[prefix + n].set_lora_info(hip, a, b)
+    x = torch.randn(rows, 128, device=dev, dtype=torch.bfloat16)
+    order = [prefix + n for n in leaves]
+    ref = [wrappers[k](x).clone() for k in order]
+    assert _fuse_siblings(wrappers, leaves, all_shapes=True) == 1
+    got = [wrappers[k](x) for k in order]
+    torch.cuda.synchronize()
+    grp = wrappers[order[0]].qkv_group
+    assert grp._delta_done and grp._cached_x is x
+    for g_, r_ in zip(got, ref):
+        torch.testing.assert_close(g_, r_, atol=2e-2, rtol=1e-2)

@@ -52,3 +52,25 @@ def test_fused_weights_are_views_in_q_k_v_order_and_outputs_hold():
     # prefill shapes (more than one token) take each layer's own GEMM
     xs = torch.randn(2, 5, 32)
     torch.testing.assert_close(ws[p + "k_proj"](xs), xs @ ws[p + "k_proj"].base_layer.weight.T)
+
+
+def test_gate_up_groups_and_all_shape_fusion():
+    """gate/up siblings fuse like q/k/v; with all_shapes a prefill-shaped input
+    takes the fused GEMM too, and outputs still equal the separate layers."""
+    from multi_lora_amd import fuse_gate_up_projections
+
+    p = "model.layers.0.mlp."
+    ws = _wrap([(p + "gate_proj", 48), (p + "up_proj", 48), (p + "down_proj", 32),
+                ("model.layers.1.mlp.gate_proj", 48)])
+    xs = torch.randn(2, 5, 32)
+    before = {n: w(xs).clone() for n, w in ws.items() if "layers.0" in n}
+    assert fuse_gate_up_projections(ws) == 1
+    grp = ws[p + "gate_proj"].qkv_group
+    assert grp is ws[p + "up_proj"].qkv_group and grp.all_shapes
+    assert ws[p + "down_proj"].qkv_group is None and ws["model.layers.1.mlp.gate_proj"].qkv_group is None
+    for n in before:
+        out = ws[n](xs)
+        torch.testing.assert_close(out, before[n], rtol=1e-6, atol=1e-6)
+    assert grp._cached_x is xs  # the fused GEMM ran for the prefill shape
+    # already grouped wrappers are left alone
+    assert fuse_gate_up_projections(ws) == 0

@@ -65,6 +65,10 @@ OTHER_WORKLOADS = {
                   "128 rank-32 adapters",
     "decode_q_resident": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool holding 64 resident "
                          "rank-16 adapters, tokens drawn over 32 of them",
+    "c5_gate_up": "the 32-layer step's gate|up LoRA call: 4096->2x14336, mixed batch of 2 x 512 prefill + 64 decode "
+                  "rows (66 segments), 128-slot pool holding 35 rank-16 adapters",
+    "c5_qkv": "the 32-layer step's q|k|v LoRA call: 4096->[4096,1024,1024], mixed batch of 2 x 512 prefill + 64 "
+              "decode rows (66 segments), 128-slot pool holding 35 rank-16 adapters",
     "pool_upload": "pool upload scatter, Llama-3-8B 32 layers x 7 projections (224 keys), rank 16, "
                    "4 staged adapters (84 MB each) into an 8-slot pool",
     "c5_step": "Llama-3-8B-shaped 32-layer model step (random init): 7 projections per layer LoRA-ed at rank 16, "
@@ -434,8 +438,7 @@ def bench_other(args) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     name = args.workload
-    host = grouped_host(name) if name in GROUPED_WORKLOADS else synthetic.prefill_mlp(
-        device="cpu", part=name.split("_", 1)[1])
+    host = workload_host(name)
     meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
     e = host.x.element_size()
     rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + 2 * host.base.numel()) * e
@@ -549,7 +552,9 @@ def bench_other(args) -> int:
 
         total_bytes = lora_bytes
         parts = {"shrink": (sh, a_bytes), "expand": (ex, b_bytes)}
-        path = "HipLoRABackend.apply_lora_multi (segment shrink, then expand)"
+        path = ("HipLoRABackend.apply_lora_multi (one mlora_apply_segments call: segment shrink, then the "
+                "mixed-batch expand; the parts are the two-call path)" if name.startswith("c5_") else
+                "HipLoRABackend.apply_lora_multi (segment shrink, then expand)")
 
     for i in range(max(args.warmup // 10, 2 * n_rep)):
         step(i)
@@ -644,7 +649,7 @@ def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> di
 COPY_ELEMS = 32 << 20
 PROFILE_CALLS = 64
 GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_qkv")
-PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down")
+PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down", "c5_gate_up", "c5_qkv")
 MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
 
@@ -663,6 +668,8 @@ def workload_host(name: str):
 
     if name in GROUPED_WORKLOADS:
         return grouped_host(name)
+    if name.startswith("c5_"):
+        return synthetic.mixed_c5(device="cpu", part=name.split("_", 1)[1])
     return synthetic.prefill_mlp(device="cpu", part=name.split("_", 1)[1])
 
 

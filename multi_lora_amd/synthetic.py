@@ -209,6 +209,28 @@ def decode_qkv(device="cpu", dtype=torch.bfloat16, tokens: int = 256, hidden: in
     return wl
 
 
+def mixed_c5(device="cpu", dtype=torch.bfloat16, part: str = "gate_up", hidden: int = 4096, inter: int = 14336,
+             kv: int = 1024, n_slots: int = 128, n_adapters: int = 35, rank: int = 16, seed: int = 4) -> LoRAWorkload:
+    """One LoRA call of the 32-layer step's mixed batch: 2 prompts of 512 tokens, then 64 decode rows, one
+    segment each; a 128-slot pool holding ``n_adapters`` rank-16 adapters, slot per segment uniform over
+    them.  ``part`` is ``gate_up`` (4096 -> 2 x 14336), ``qkv`` (4096 -> [4096, 1024, 1024]), ``o``
+    (4096 -> 4096) or ``down`` (14336 -> 4096)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    seg_lens = [512, 512] + [1] * 64
+    seg_slots = torch.randint(0, n_adapters, (len(seg_lens),), generator=g).tolist()
+    ranks = [rank] * n_adapters + [0] * (n_slots - n_adapters)
+    in_dim, outs = {"gate_up": (hidden, [inter, inter]), "qkv": (hidden, [hidden, kv, kv]), "o": (hidden, [hidden]),
+                    "down": (inter, [hidden])}[part]
+    x = _normal(g, (sum(seg_lens), in_dim), 1.0)
+    a, b = _stacks(g, n_slots, ranks, rank, in_dim, outs, in_dim ** -0.5, 0.02)
+    cols, c = [], 0
+    for o in outs:
+        cols.append(c)
+        c += o
+    return _finish(f"c5_{part}", g, seg_lens, seg_slots, ranks, [2.0] * n_slots, x, a, b, sum(outs), dtype, device,
+                   cols)
+
+
 def algorithmic_bytes(wl: LoRAWorkload, include_x: bool = True) -> int:
     """HBM bytes a perfect shrink+expand moves: x once, each referenced slot's live A rows and
     B columns once per slice, and the residual read plus write."""

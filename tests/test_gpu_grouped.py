@@ -428,3 +428,25 @@ def test_slices_not_multiples_of_the_expand_tile(dev, mode):
 
 def test_abi_version(dev):
     assert _ffi.lib().mlora_abi_version() == _ffi.ABI_VERSION == 5
+
+
+def test_largest_supported_shape(dev):
+    """The decode path's limits together: in_dim 16384 (64 K chunks, one flag
+    per lane of the polling wave), four slices at r_max 64 (shrink items split
+    per slice), full and partial ranks, a rank-0 slot, segments of up to 16
+    rows.  All schedules, and the single launch with every wait given up,
+    agree bit for bit and match the oracle."""
+    assert _ffi.lib().mlora_grouped_workspace_bytes(16384, 64, 4, 64, 8, _ffi.MLORA_BF16, 0) > 0
+    g = torch.Generator().manual_seed(77)
+    n_slots = 8
+    lens = [1, 16, 3, 1, 7, 1, 1, 16, 2, 1, 1, 1, 5, 1, 1, 1]
+    slots = torch.randint(0, n_slots, (len(lens),), generator=g).tolist()
+    ranks = [64, 40, 0, 64, 17, 64, 64, 33]
+    wl = workload("largest", dev, lens, slots, ranks, [0.75] * n_slots, 16384, [512, 256, 264, 1024], 64, 77)
+    lws = LinkedWorkspace()
+    one = check(wl, mode=1, lws=lws)
+    assert_clean(lws)
+    assert torch.equal(grouped(wl, mode=2), one)
+    lws.set_wait_ticks(-1)
+    assert torch.equal(grouped(wl, mode=1, lws=lws), one)
+    assert counters(lws)[0] > 0

@@ -113,3 +113,50 @@ def test_upload_into_an_evicted_slot_waits_for_the_compute_reading_it(dev):
     assert torch.equal(seen.cpu(), a_rows)
     assert torch.equal(pool.get_module_buffers("q_proj")[0][0].cpu(), b_rows)
     assert pool.get_slot_id("b") == 0 and "a" not in pool.name_to_slot
+
+
+def test_pipelined_serving_equals_serialised(dev):
+    """A serving loop that never synchronises between steps (the next batch is
+    prepared, evicting and uploading, while the previous forward may still
+    run) gives, step for step, the logits of the same batches run with a
+    synchronisation after every step.  Three slots for six adapters, so
+    nearly every step evicts."""
+    from multi_lora_amd import MultiLoRAManager
+    from multi_lora_amd.decoder import Decoder, DecoderConfig
+
+    cfg = DecoderConfig()
+    proj = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+            "mlp.up_proj", "mlp.down_proj")
+
+    def run(sync_each_step):
+        torch.manual_seed(0)
+        model = Decoder(cfg).to(dev, torch.float32).eval()
+        adapters = {}
+        for j in range(6):
+            g = torch.Generator().manual_seed(100 + j)
+            mods = {}
+            for layer in range(cfg.num_hidden_layers):
+                for p in proj:
+                    lin = model.get_submodule(f"layers.{layer}.{p}")
+                    mods[f"layers.{layer}.{p}"] = (torch.randn(8, lin.in_features, generator=g) * 0.05,
+                                                   torch.randn(lin.out_features, 8, generator=g) * 0.05)
+            adapters[f"a{j}"] = AdapterWeights(rank=8, scaling=2.0, modules=mods)
+        mgr = MultiLoRAManager.from_adapters(model, adapters, max_loras_per_batch=3, max_lora_rank=8)
+        rng = random.Random(7)
+        ids = torch.randint(0, cfg.vocab_size, (4, 6), generator=torch.Generator().manual_seed(3)).to(dev)
+        outs = []
+        with torch.inference_mode():
+            for _ in range(12):
+                names = [f"a{rng.randrange(6)}" for _ in range(4)]
+                while len(set(names)) > 3:
+                    names[rng.randrange(4)] = names[0]
+                out = mgr.forward_with_lora(input_ids=ids, lora_names=names, seq_lens=[6] * 4, use_cache=False)
+                outs.append(out.logits.clone())
+                if sync_each_step:
+                    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        return [o.cpu() for o in outs]
+
+    piped, serial = run(False), run(True)
+    for k, (p_, s_) in enumerate(zip(piped, serial)):
+        assert torch.equal(p_, s_), f"step {k} differs"

@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
                     help="FETCH_SIZE and WRITE_SIZE run directories of --profile-traffic (and optionally an MFMA "
                          "counter run's) -> the workload's counter summary under profiles/")
+    ap.add_argument("--sweep", choices=("decode",),
+                    help="decode: one JSON line per decode shape (tokens, adapters, rank, slices), graph-timed "
+                         "over cold replicas, with the schedule the library picks")
     ap.add_argument("--regions", type=int, default=0,
                     help="timed regions of exactly --steps steps each (default: enough for ~2000 steps, 5..101); "
                          "the step time is their median")
@@ -602,6 +605,60 @@ def bench_other(args) -> int:
     return 0
 
 
+def sweep_decode(args) -> int:
+    """The planned decode path over decode shapes around the headline: token
+    counts, adapter counts and ranks at q_proj 4096->4096, and q|k|v at
+    4096->[4096,1024,1024].  Each shape: the backend's call, graph-timed over
+    cold replicas (at least 600 MB), and both schedules for comparison."""
+    import torch
+
+    from multi_lora_amd import synthetic
+    from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, apply_grouped
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    shapes = [dict(tokens=t, n_adapters=32, rank=16) for t in (16, 32, 64, 128, 256, 512)]
+    shapes += [dict(tokens=128, n_adapters=a, rank=16) for a in (1, 8, 64)]
+    shapes += [dict(tokens=128, n_adapters=32, rank=r) for r in (8, 32, 64)]
+    shapes += [dict(tokens=t, n_adapters=64, rank=16, qkv=True) for t in (64, 256)]
+    for sh in shapes:
+        qkv = sh.pop("qkv", False)
+        n_slots = max(64, 2 * sh["n_adapters"])
+        if qkv:
+            host = synthetic.decode_qkv(device="cpu", tokens=sh["tokens"], n_slots=n_slots, n_adapters=sh["n_adapters"],
+                                        rank=sh["rank"], seed=5)
+        else:
+            host = synthetic.decode_q(device="cpu", n_slots=n_slots, seed=5, **sh)
+        meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+        e = host.x.element_size()
+        rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + host.base.numel()) * e
+        n_rep = max(2, -(-600_000_000 // rep_bytes))
+        reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
+                 host.base.to(dev)) for _ in range(n_rep)]
+        lws = LinkedWorkspace()
+        nbytes = synthetic.algorithmic_bytes(host)
+        res = {}
+        for mode in (0, 1, 2):
+            def call(i, mode=mode):
+                x, a, b, out = reps[i % n_rep]
+                assert apply_grouped(x, a, b, meta, out, host.col_offsets, lws, mode=mode)
+            per_graph = max(32, n_rep)
+            res[mode] = time_calls(torch, call, max(args.kernel_steps, 2 * per_graph), per_graph, stream) * 1e3
+        fb, pe = lws.counters()
+        if pe:
+            raise RuntimeError(f"{pe} plan errors; timings are void")
+        us = res[0]
+        print(json.dumps({
+            "shape": ("q|k|v 4096->[4096,1024,1024]" if qkv else "q_proj 4096->4096"), **sh,
+            "slots": n_slots, "entries": meta.plan_entries, "us": round(us, 2),
+            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": nbytes, "one_launch_us": round(res[1], 2), "two_launches_us": round(res[2], 2),
+            "library_pick": "one launch" if abs(res[0] - res[1]) <= abs(res[0] - res[2]) else "two launches",
+            "handoff_fallback_chunks": fb}), flush=True)
+    return 0
+
+
 def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> dict:
     """The oracle's per-segment PyTorch path (plus its RMSNorm for decode_qkv)
     on the host cores, bf16, same inputs; at least 3 timed steps."""
@@ -871,6 +928,8 @@ def main() -> int:
 
     if args.profile_traffic:
         return profile_traffic(args.workload)
+    if args.sweep == "decode":
+        return sweep_decode(args)
     if args.workload == "pool_upload":
         return bench_pool_upload(args)
     if args.workload == "c5_step":

@@ -46,12 +46,14 @@ struct ShrinkArgs {
 };
 
 struct ShrinkPlan {
-  int bm;     // 16 or 64 token rows per tile
+  int bm;         // 16 or 64 token rows per tile
   int m_tiles;
   int ks;
   int k_per_split;
-  int nbt;    // compiled bound on 16-row blocks of A over the slices of one launch
-  int spg;    // slices per launch: calls over 8 A blocks run one launch per group of slices
+  int nbt;        // compiled bound on 16-row blocks of A over the slices of one launch
+  int spg;        // slices per launch: calls over 8 A blocks run one launch per group of slices
+  int kt;         // streamed kernel: reduction elements per stage (0: not planned)
+  int stages;     // streamed kernel: stages in flight
   size_t ws_bytes;
 };
 

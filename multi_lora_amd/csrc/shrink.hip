@@ -447,16 +447,26 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
 // Long segments, 16-bit types, aligned rows, K split in multiples of the
 // stage width KT: x and A stages go from HBM straight to LDS
 // (global_load_lds_dwordx4: lane l of a wave instruction fills LDS bytes
-// [16 l, 16 l + 16) above the instruction's base), kDmaStages stages in
-// flight, so loads hold no VGPRs and occupancy is set by LDS alone.  A stage
-// is 64 x rows and NAL A rows of KT elements (2 KT bytes, KT / 8 chunks of 16
-// bytes); rows are not padded:
-// the chunk c of LDS row r holds source chunk c ^ dma_swz(r), which makes the
-// MFMA fragment reads (16 rows, one chunk each) hit 16 different bank groups.
-// Per stage: wait for this wave's loads of the stage (vmcnt), one barrier
-// (all waves' loads landed, the buffer of stage st - 1 is free), request
-// stage st + kDmaStages - 1 into that buffer, MFMAs from LDS.
+// [16 l, 16 l + 16) above the instruction's base), S stages in flight, so
+// loads hold no VGPRs and occupancy is set by LDS alone.  A workgroup is BM
+// token rows (BM / 16 waves of 16 rows each) against the NAL A rows of the
+// slices' live rank blocks.  A stage is the BM x rows and the NAL A rows, KT
+// elements each (2 KT bytes, KT / 8 chunks of 16 bytes); rows are not
+// padded: the chunk c of LDS row r holds source chunk c ^ dma_swz(r), which
+// makes the MFMA fragment reads (16 rows, one chunk each) hit 16 different
+// bank groups.  A stage is (BM + NAL) / (64 / CPR) load instructions, dealt
+// to the waves round-robin.  Per stage: wait for this wave's loads of the
+// stage (vmcnt), one barrier (all waves' loads landed, the buffer of stage
+// st - 1 is free), request stage st + S - 1 into that buffer, MFMAs from LDS.
+// The planned instance is BM 64, KT 64, S 3: 128-row tiles (eight waves)
+// and 4 to 9 stages of 32 or 64 elements measured no faster at prefill
+// gate|up and down, and neither did the same loads without the MFMAs or
+// the A fragment reads (the kernel is bound by its loads).  All row tiles of
+// a split walk K in step, so the A rows in flight at any time are few and
+// stay in the L2; a stream-K grid (equal runs of (tile, stage) units per
+// workgroup) loses that and measured slower (gate|up 23.0 vs 18.2 us).
 constexpr int kDmaKt = 64;  // reduction elements per stage
+constexpr int kCpolNt = 2;  // cache-policy operand of a load: non-temporal
 constexpr int kDmaStages = 3;
 
 // Swizzle of LDS row r for rows of CPR 16-byte chunks: the 16 rows of one
@@ -467,26 +477,55 @@ __device__ __forceinline__ int dma_swz(int r) { return (r / (16 / CPR)) & (CPR -
 typedef __attribute__((address_space(1))) void gvoid_t;
 typedef __attribute__((address_space(3))) void lvoid_t;
 
-template <class T, int NBT, int KT>
-__global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, MAX] (larger n: MAX).
+template <int MAX, int N = 0>
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+  if constexpr (N >= MAX) {
+    wait_vmcnt<MAX>();
+  } else {
+    if (n == N) {
+      wait_vmcnt<N>();
+      return;
+    }
+    wait_vmcnt_upto<MAX, N + 1>(n);
+  }
+}
+
+// s_waitcnt vmcnt(A * live) for a wave-uniform live in [0, L].
+template <int A, int L, int N = 0>
+__device__ __forceinline__ void wait_vmcnt_times(int live) {
+  if constexpr (N >= L) {
+    wait_vmcnt<A * L>();
+  } else {
+    if (live == N) {
+      wait_vmcnt<A * N>();
+      return;
+    }
+    wait_vmcnt_times<A, L, N + 1>(live);
+  }
+}
+
+template <class T, int NBT, int KT, int BM = 64, int S = kDmaStages>
+__global__ __launch_bounds__(BM * 4) void shrink_dma_kernel(ShrinkArgs a) {
   using raw = typename T::raw_t;
   static_assert(sizeof(raw) == 2, "16-bit types only");
-  constexpr int BM = 64;
-  constexpr int NAL = 16 * (NBT < 2 ? 2 : NBT);  // A rows loaded per stage (a whole instruction per wave)
+  constexpr int W = BM / 16;                      // waves
+  constexpr int NAL = 16 * (NBT < 2 ? 2 : NBT);  // A rows loaded per stage
   constexpr int ROWS = BM + NAL;
   constexpr int ROW_BYTES = KT * 2;               // 128 or 64
   constexpr int CPR = KT / 8;                     // 16-byte chunks per row per stage
   constexpr int RPI = 64 / CPR;                   // rows per wave instruction
+  constexpr int NX = BM / RPI;                    // x instructions per stage
+  constexpr int NI = ROWS / RPI;                  // instructions per stage
+  constexpr int L = (NI + W - 1) / W;             // most instructions of one wave per stage
   constexpr int STAGE_BYTES = ROWS * ROW_BYTES;
-  constexpr int XI = BM * CPR / 256;              // x instructions per wave per stage
-  constexpr int AI = NAL * CPR / 256;             // A instructions per wave per stage
-  constexpr int L = XI + AI;                      // loads per wave per stage
-  static_assert((BM * CPR) % 256 == 0 && (NAL * CPR) % 256 == 0, "whole instructions per wave");
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[kDmaStages * STAGE_BYTES];
+  static_assert(BM % RPI == 0 && NAL % RPI == 0, "whole instructions");
+  static_assert(S >= 3 && (S - 2) * L < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[S * STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15;
   const int g = lane >> 4;
 
@@ -506,63 +545,62 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   const int nb_act = (rank + 15) >> 4;
   const int nbt = a.n_slices * nb_act;
 
-  // Source of this lane's chunk in each of its load instructions: LDS row r
-  // (stage-local), LDS chunk lane % CPR, source chunk (lane % CPR) ^ swz(r).
+  // Load instruction j of this wave is stage instruction i = wave + W j:
+  // x rows [i RPI, i RPI + RPI) for i < NX, else A rows [(i - NX) RPI, ...).
+  // Lane l fills LDS row (stage-local) i RPI + l / CPR, chunk l % CPR, from
+  // source chunk (l % CPR) ^ swz(row).  Instructions whose rows are all past
+  // the segment (x) or past the live rank blocks (A) are skipped: they would
+  // only fetch a clamped row again, and the products of their LDS rows are
+  // discarded.  The same instructions are live in every stage.  An A
+  // instruction's rows lie in one 16-row block, so its slice is uniform and
+  // the slice's pointers come by scalar loads.
   const int c8 = lane & (CPR - 1);
   const raw* src[L];
-  int lds_off[L];  // byte offset of the instruction's first chunk within a stage
+  uint32_t live_mask = 0;
+  int live = 0;
 #pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int first = (wave * XI + i) * 64;       // chunk index within the x region
-    const int r = (first + lane) / CPR;           // x row of the tile, 0..63
-    src[i] = static_cast<const raw*>(a.x) + static_cast<int64_t>(min(row0 + r, end - 1)) * a.x_stride +
-             ((c8 ^ dma_swz<CPR>(r)) << 3);
-    lds_off[i] = first * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < AI; ++i) {
-    const int first = (wave * AI + i) * 64;       // chunk index within the A region
-    const int ra = (first + lane) / CPR;          // A row of the stage, 0..NAL-1
-    const int j = min(ra >> 4, nbt - 1);
-    const int s = j / nb_act;
-    const raw* arow = slice_a<raw>(a.slices, s, slot, min((j - s * nb_act) * 16 + (ra & 15), rank - 1));
-    src[XI + i] = arow + ((c8 ^ dma_swz<CPR>(BM + ra)) << 3);
-    lds_off[XI + i] = BM * ROW_BYTES + first * 16;
+  for (int j = 0; j < L; ++j) {
+    const int i = wave + W * j;
+    const int r = i * RPI + lane / CPR;  // stage-local LDS row
+    if (i < NX) {
+      src[j] = static_cast<const raw*>(a.x) + static_cast<int64_t>(min(row0 + r, end - 1)) * a.x_stride +
+               ((c8 ^ dma_swz<CPR>(r)) << 3);
+    } else {
+      const int ra = min(r - BM, NAL - 1);
+      const int jb = min(min((i - NX) * RPI, NAL - 1) >> 4, nbt - 1);  // the block of all the instruction's rows
+      const int s = jb / nb_act;
+      const raw* arow = slice_a<raw>(a.slices, s, slot, min((jb - s * nb_act) * 16 + (ra & 15), rank - 1));
+      src[j] = arow + ((c8 ^ dma_swz<CPR>(r)) << 3);
+    }
+    const bool on = i < NI && (i < NX ? i * RPI < rows_here : (i - NX) * RPI < nbt * 16);
+    if (on) {
+      live_mask |= 1u << j;
+      ++live;
+    }
   }
 
   const int kbeg = kz * a.k_per_split;
   const int kend = min(a.in_dim, kbeg + a.k_per_split);
   const int nst = (kend - kbeg) / KT;  // the dispatch makes the split a multiple of KT
 
-  // Instructions of this wave that hold live rows (8 rows each): x rows of
-  // the segment and A rows of the live rank blocks.  The others would only
-  // fetch a clamped row again; they are skipped and their LDS rows, whose
-  // products are discarded, left as they are.  The counts are the same for
-  // every stage.
-  const int xi_live = min(max((rows_here - wave * XI * RPI + RPI - 1) / RPI, 0), XI);
-  const int ai_live = min(max((nbt * 16 - wave * AI * RPI + RPI - 1) / RPI, 0), AI);
+  // Instructions j < XJ of every wave are x loads (W XJ = NX).  x is read
+  // once, so those loads carry the non-temporal hint (nt): the L2 keeps the
+  // A rows, which every row tile of the segment reads again, in preference.
+  constexpr int XJ = NX / W;
+  static_assert(XJ * W == NX, "x instructions split evenly over the waves");
   auto issue = [&](int st) {
-    unsigned char* base = lds + (st % kDmaStages) * STAGE_BYTES;
+    unsigned char* base = lds + (st % S) * STAGE_BYTES;
     const int k0 = kbeg + st * KT;
 #pragma unroll
-    for (int i = 0; i < L; ++i)
-      if (i < XI ? i < xi_live : i - XI < ai_live)
-        __builtin_amdgcn_global_load_lds((gvoid_t*)(src[i] + k0), (lvoid_t*)(base + lds_off[i]), 16, 0, 0);
-  };
-  // vmcnt allowing one stage of this wave's loads still in flight.
-  const int live = xi_live + ai_live;
-  auto wait_one_stage_ahead = [&]() {
-    static_assert(L <= 6, "one case per live load count");
-    constexpr int A = kDmaStages - 2;  // stages still in flight
-    switch (live) {
-      case 0: wait_vmcnt<0>(); break;
-      case 1: wait_vmcnt<A * 1>(); break;
-      case 2: wait_vmcnt<A * 2>(); break;
-      case 3: wait_vmcnt<A * 3>(); break;
-      case 4: wait_vmcnt<A * 4>(); break;
-      case 5: wait_vmcnt<A * 5>(); break;
-      default: wait_vmcnt<A * 6>(); break;
-    }
+    for (int j = 0; j < L; ++j)
+      if (live_mask & (1u << j)) {
+        gvoid_t* gp = (gvoid_t*)(src[j] + k0);
+        lvoid_t* lp = (lvoid_t*)(base + (wave + W * j) * 1024);
+        if (j < XJ)
+          __builtin_amdgcn_global_load_lds(gp, lp, 16, 0, kCpolNt);
+        else
+          __builtin_amdgcn_global_load_lds(gp, lp, 16, 0, 0);
+      }
   };
 
   f32x4 acc[NBT];
@@ -570,19 +608,21 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
   for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-  for (int st = 0; st < kDmaStages - 1; ++st)
+  for (int st = 0; st < S - 1; ++st)
     if (st < nst) issue(st);
   for (int st = 0; st < nst; ++st) {
-    if (st + kDmaStages - 2 < nst)
-      wait_one_stage_ahead();
+    // This wave's loads of stage st have landed once at most those of the
+    // stages issued after it are still in flight.
+    const int ahead = min(S - 2, nst - 1 - st);
+    if (ahead == S - 2)
+      wait_vmcnt_times<S - 2, L>(live);
     else
-      wait_vmcnt<0>();
+      wait_vmcnt_upto<(S - 2) * L>(ahead * live);
     // A bare barrier: a fenced one would also wait for the stages still in
-    // flight.  This wave's loads of stage st have landed (vmcnt above), and
-    // the barrier makes that true of every wave.
+    // flight.  The barrier makes the wait above true of every wave.
     __builtin_amdgcn_s_barrier();
-    if (st + kDmaStages - 1 < nst) issue(st + kDmaStages - 1);
-    const unsigned char* base = lds + (st % kDmaStages) * STAGE_BYTES;
+    if (st + S - 1 < nst) issue(st + S - 1);
+    const unsigned char* base = lds + (st % S) * STAGE_BYTES;
 #pragma unroll
     for (int ks = 0; ks < KT / 32; ++ks) {
       const int c = ks * 4 + g;
@@ -615,6 +655,10 @@ __global__ __launch_bounds__(256) void shrink_dma_kernel(ShrinkArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (n + q < a.r_max) mrow[col + q] = T::from_f32(v[q]);
+      } else if ((a.r_max & 3) == 0 && (reinterpret_cast<uintptr_t>(a.partials) & 15) == 0) {
+        // n is a multiple of 4 below r_max, so all four columns exist and the
+        // store is 16-byte aligned (rows of n_slices * r_max floats).
+        if (n < a.r_max) *reinterpret_cast<f32x4*>(prow + col) = v;
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -702,33 +746,41 @@ hipError_t launch_reduce(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_
 // The short kernel (bm 16) runs one workgroup per segment and split; the
 // long kernels and the reduction run over dense row tiles.
 template <class T>
-hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+hipError_t launch_with(void (*kern)(ShrinkArgs), const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream,
+                       int threads = 256) {
   const int64_t tiles = p.bm == 16 ? static_cast<int64_t>(args.meta.bs) * p.m_tiles
                                    : dense_tiles(args.meta.bs, p.m_tiles, args.rows, p.bm);
   if (tiles <= 0) return hipSuccess;
   if (!grid_fits(tiles * p.ks)) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * p.ks)), dim3(256), 0, stream, args);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * p.ks)), dim3(threads), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1 || args.skip_reduce) return e;
   return launch_reduce<T>(p, args, stream);
+}
+
+// The streamed kernel's instance for the plan's (rows, stage width, stages).
+template <class T, int NBT>
+hipError_t launch_dma(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
+  if (p.bm == 64 && p.kt == 64 && p.stages == 3)
+    return launch_with<T>(shrink_dma_kernel<T, NBT, 64, 64, 3>, p, args, stream, 256);
+  return hipErrorInvalidValue;
 }
 
 template <class T, int NBT, bool AL>
 hipError_t launch_nbt_al(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
   constexpr int RB = kShrinkRb<NBT>;
   if (p.bm == 16) return launch_with<T>(shrink_kernel<T, 1, NBT, AL>, p, args, stream);
-  if (p.bm != 64 * RB) return hipErrorInvalidValue;
   if constexpr (AL && sizeof(typename T::raw_t) == 2 && NBT <= 8) {
     // Direct-to-LDS stages when every split is a whole number of them
     // (measured at prefill gate|up 25.3 vs 33.7 us, down 39.5 vs 43.5 us).
     // 64-element stages for every block count: with eight A blocks, 32-element
     // stages (36 KB of LDS, twice the occupancy) measured slower at prefill
     // gate|up, 30.8 vs 26 us.
-    constexpr int KT = kDmaKt;
-    if (args.in_dim % KT == 0 && p.k_per_split % KT == 0)
-      return launch_with<T>(shrink_dma_kernel<T, NBT, KT>, p, args, stream);
-    return launch_with<T>(shrink_lds_kernel<T, NBT, RB>, p, args, stream);
+    if (p.kt > 0 && args.in_dim % p.kt == 0 && p.k_per_split % p.kt == 0) return launch_dma<T, NBT>(p, args, stream);
   }
+  if (p.bm != 64 * RB) return hipErrorInvalidValue;
+  if constexpr (AL && sizeof(typename T::raw_t) == 2 && NBT <= 8)
+    return launch_with<T>(shrink_lds_kernel<T, NBT, RB>, p, args, stream);
   return launch_with<T>(shrink_rows_kernel<T, NBT, RB, AL>, p, args, stream);
 }
 
@@ -806,6 +858,10 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
     // 8 bytes per column and split) cost at most the x bytes (at gate|up, six
     // splits move 0.75 of the x bytes in sums and still beat four).
     const bool streamed = dtype != MLORA_F32 && p.nbt <= 8 && in_dim % kDmaKt == 0;
+    if (streamed) {
+      p.kt = kDmaKt;
+      p.stages = kDmaStages;
+    }
     const int unit = streamed ? kDmaKt : kstep;
     const int units = cdiv(in_dim, unit);
     const int ncols = n_slices * r_max;

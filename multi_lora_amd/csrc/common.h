@@ -37,6 +37,12 @@ struct BF16 {
   __device__ static __forceinline__ raw_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
   }
+  // from_f32(lo) | from_f32(hi) << 16, in one conversion instruction.
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+  }
   __device__ static __forceinline__ f32x4 mma(f32x4 acc, u32x4 a, u32x4 b) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
@@ -52,6 +58,9 @@ struct F16 {
   }
   __device__ static __forceinline__ raw_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(from_f32(lo)) | (static_cast<uint32_t>(from_f32(hi)) << 16);
   }
   __device__ static __forceinline__ f32x4 mma(f32x4 acc, u32x4 a, u32x4 b) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),

@@ -80,8 +80,6 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
   const int end = tr.end;
   const int row0 = tr.start + tr.mt * BM;
   const int slot = tr.slot;
-  const int rank = slot_rank_of(a.meta, slot, a.r_max, 1);
-  if (rank == 0) return;
 
   int s = 0;
   while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
@@ -89,8 +87,10 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
   const int out_dim = a.slices[s].out_dim;
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
 
-  const float scale = load_scaling_uniform(a.meta.scalings, slot, a.meta.scal_dtype);
-  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
+  // Clamped to the pool: an out-of-pool slot has rank 0, and its loads are
+  // discarded.
+  const int pslot = min(max(slot, 0), a.meta.num_slots - 1);
+  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(pslot) * a.slices[s].b_slot_stride;
   const int64_t brs = a.slices[s].b_row_stride;
   const raw* brow[4];
 #pragma unroll
@@ -102,13 +102,25 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
     mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
                static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
 
+  // The slot's rank and scaling word go out first, as vector loads (lane0 is
+  // 0 in every lane, but not known to be uniform), and are waited for
+  // together with the first fragments: as scalar loads they were waited for
+  // before any request below went out (scalar loads return out of order, so
+  // a wait for one waits for all), a round trip of about 1.3 us under load.
+  const int lane0 = static_cast<int>(__builtin_amdgcn_mbcnt_lo(0u, 0u));
+  const int rank_word = a.meta.ranks[pslot + lane0];
+  const bool scal16 = a.meta.scal_dtype == MLORA_BF16 || a.meta.scal_dtype == MLORA_F16;
+  const char* scal_byte = static_cast<const char*>(a.meta.scalings) + (scal16 ? 2 : 4) * static_cast<int64_t>(pslot);
+  const int scal_hi = scal16 ? static_cast<int>(reinterpret_cast<uintptr_t>(scal_byte) & 3) : 0;
+  const uint32_t scal_word = reinterpret_cast<const uint32_t*>(scal_byte - scal_hi)[lane0];
+
   // The first K-step's mid and B fragments go out before the output tile,
   // unmasked (masked at the MFMA): loads complete in issue order, so waiting
   // for them leaves the tile's loads in flight.
   u32x4 yv0[TB], bv0[4];
   {
     const int kk = g * VEC;
-    const int off = kk < rank ? kk : 0;
+    const int off = kk < a.r_max ? kk : 0;
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) yv0[tb] = ld_chunk(mrow[tb] + off);
 #pragma unroll
@@ -128,10 +140,24 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
     const raw* src = out + static_cast<int64_t>(min(row0 + r, end - 1)) * a.out_stride + n;
     __builtin_amdgcn_global_load_lds((gvoid_t*)src, (lvoid_t*)(tile + ins * 64 * 16), 16, 0, 0);
   }
-  // The fragments have landed; the scheduling barrier keeps their MFMAs
-  // (and the wait) below the tile's loads.
+  // The rank, scaling and fragments have landed; the scheduling barrier
+  // keeps their uses (and the wait) below the tile's loads.
   wait_vmcnt<IPW>();
   __builtin_amdgcn_sched_barrier(0);
+  const int rank = (slot >= 0 && slot < a.meta.num_slots)
+                       ? min(max(__builtin_amdgcn_readfirstlane(rank_word), 0), a.r_max) : 0;
+  float scale;
+  {
+    const uint32_t w = __builtin_amdgcn_readfirstlane(scal_word);
+    const uint16_t h = static_cast<uint16_t>(scal_hi ? (w >> 16) : (w & 0xffffu));
+    scale = !scal16 ? __uint_as_float(w) : (a.meta.scal_dtype == MLORA_BF16 ? BF16::to_f32(h) : F16::to_f32(h));
+  }
+  // A rank-0 (or out-of-pool) slot leaves the output as it is; the tile's
+  // loads into LDS must land before the waves leave.
+  if (rank == 0) {
+    wait_vmcnt<0>();
+    return;
+  }
 
   f32x4 acc[4][TB];
 #pragma unroll
@@ -174,13 +200,13 @@ __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
       const f32x4 v = acc[nb][tb];
       uint2* p = reinterpret_cast<uint2*>(tile + t * ROWB + (((nl / VEC) ^ (t & 15)) << 4) + (nl % VEC) * 2);
       const uint2 o = *p;
-      const float d0 = T::to_f32(T::from_f32(v[0] * scale)), d1 = T::to_f32(T::from_f32(v[1] * scale));
-      const float d2 = T::to_f32(T::from_f32(v[2] * scale)), d3 = T::to_f32(T::from_f32(v[3] * scale));
+      // Two elements a conversion (the same rounding as one at a time).
+      const uint32_t dlo = T::pack2(v[0] * scale, v[1] * scale), dhi = T::pack2(v[2] * scale, v[3] * scale);
+      auto lo = [](uint32_t u) { return T::to_f32(static_cast<raw>(u & 0xffffu)); };
+      auto hi = [](uint32_t u) { return T::to_f32(static_cast<raw>(u >> 16)); };
       uint2 w;
-      w.x = static_cast<uint32_t>(T::from_f32(T::to_f32(static_cast<raw>(o.x & 0xffffu)) + d0)) |
-            (static_cast<uint32_t>(T::from_f32(T::to_f32(static_cast<raw>(o.x >> 16)) + d1)) << 16);
-      w.y = static_cast<uint32_t>(T::from_f32(T::to_f32(static_cast<raw>(o.y & 0xffffu)) + d2)) |
-            (static_cast<uint32_t>(T::from_f32(T::to_f32(static_cast<raw>(o.y >> 16)) + d3)) << 16);
+      w.x = T::pack2(lo(o.x) + lo(dlo), hi(o.x) + hi(dlo));
+      w.y = T::pack2(lo(o.y) + lo(dhi), hi(o.y) + hi(dhi));
       *p = w;
     }
   }

@@ -49,21 +49,32 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
   const int r16 = lane & 15;
   const int g = lane >> 4;
 
+  // Aligned y from mid (kEarly): the first K-step's mid and B fragments are
+  // requested before the output tile, and the slot's rank and scaling with
+  // them (see below); otherwise the rank comes first.
+  constexpr bool kEarly = AL && !FUSED;
   const int end = tr.end;
   const int row0 = tr.start + tr.mt * BM;
   const int slot = tr.slot;
-  const int rank = slot_rank_of(a.meta, slot, a.r_max, 1);
-  if (rank == 0) return;
+  int rank = 0;
+  float scale = 0.f;
+  if constexpr (!kEarly) {
+    rank = slot_rank_of(a.meta, slot, a.r_max, 1);
+    if (rank == 0) return;
+  }
 
   int s = 0;
   while (s + 1 < a.n_slices && nt_g >= a.tile_base[s + 1]) ++s;
   const int n0 = (nt_g - a.tile_base[s]) * BN;
   const int out_dim = a.slices[s].out_dim;
-  const float scale = load_scaling_uniform(a.meta.scalings, slot, a.meta.scal_dtype);
+  if constexpr (!kEarly) scale = load_scaling_uniform(a.meta.scalings, slot, a.meta.scal_dtype);
 
   raw* out = static_cast<raw*>(a.out) + a.slices[s].out_col;
 
-  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(slot) * a.slices[s].b_slot_stride;
+  // Clamped to the pool: an out-of-pool slot has rank 0 (its loads, made
+  // before the rank is known, are discarded).
+  const int pslot = min(max(slot, 0), a.meta.num_slots - 1);
+  const raw* B = static_cast<const raw*>(a.slices[s].b) + static_cast<int64_t>(pslot) * a.slices[s].b_slot_stride;
   const int64_t brs = a.slices[s].b_row_stride;
   const raw* brow[4];
 #pragma unroll
@@ -75,15 +86,25 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
     mrow[tb] = static_cast<const raw*>(a.mid) + s * a.r_max +
                static_cast<int64_t>(min(row0 + tb * 16 + r16, end - 1)) * a.mid_stride;
 
-  // Aligned y from mid: the first K-step's mid and B fragments are requested
-  // before the output tile, unmasked (masked at the MFMA).  Loads complete in
-  // issue order, so the first MFMAs wait for them only, with the tile's loads
-  // still in flight.
-  constexpr bool kEarly = AL && !FUSED;
+  // kEarly: the slot's rank and scaling word are vector loads (lane0 is 0
+  // in every lane, but not known to be uniform), then the first K-step's mid
+  // and B fragments, unmasked (masked at the MFMA), all before the output
+  // tile.  Loads complete in issue order, so the first MFMAs wait for these
+  // only, with the tile's loads still in flight.  (As scalar loads the rank
+  // and scaling were waited for before any request went out: scalar loads
+  // return out of order, so a wait for one waits for all.)
   u32x4 yv0[TB], bv0[4];
+  int rank_word = 0, scal_hi = 0;
+  uint32_t scal_word = 0;
+  const bool scal16 = a.meta.scal_dtype == MLORA_BF16 || a.meta.scal_dtype == MLORA_F16;
   if constexpr (kEarly) {
+    const int lane0 = static_cast<int>(__builtin_amdgcn_mbcnt_lo(0u, 0u));
+    rank_word = a.meta.ranks[pslot + lane0];
+    const char* scal_byte = static_cast<const char*>(a.meta.scalings) + (scal16 ? 2 : 4) * static_cast<int64_t>(pslot);
+    scal_hi = scal16 ? static_cast<int>(reinterpret_cast<uintptr_t>(scal_byte) & 3) : 0;
+    scal_word = reinterpret_cast<const uint32_t*>(scal_byte - scal_hi)[lane0];
     const int kk = g * VEC;
-    const int off = kk < rank ? kk : 0;
+    const int off = kk < a.r_max ? kk : 0;
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) yv0[tb] = ld_chunk(mrow[tb] + off);
 #pragma unroll
@@ -141,9 +162,19 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
 
   int k_first = 0;
   if constexpr (kEarly) {
-    // The scheduling barrier keeps these MFMAs (and their wait) below the
+    // The scheduling barrier keeps these MFMAs (and their waits) below the
     // output tile's loads.
     __builtin_amdgcn_sched_barrier(0);
+    rank = (slot >= 0 && slot < a.meta.num_slots) ? min(max(__builtin_amdgcn_readfirstlane(rank_word), 0), a.r_max)
+                                                   : 0;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(scal_word);
+    const uint16_t h = static_cast<uint16_t>(scal_hi ? (w >> 16) : (w & 0xffffu));
+    scale = !scal16 ? __uint_as_float(w) : (a.meta.scal_dtype == MLORA_BF16 ? BF16::to_f32(h) : F16::to_f32(h));
+    // A rank-0 (or out-of-pool) slot leaves the output as it is.
+    if (rank == 0) {
+      wait_vmcnt<0>();
+      return;
+    }
     const u32x4 m = keep_mask<T>(rank - g * VEC);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
@@ -185,10 +216,8 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
       raw* p = delta + tl * LDS_STRIDE + nl;
       if constexpr (sizeof(raw) == 2) {
         uint2 w;
-        w.x = static_cast<uint32_t>(T::from_f32(v[0] * scale)) |
-              (static_cast<uint32_t>(T::from_f32(v[1] * scale)) << 16);
-        w.y = static_cast<uint32_t>(T::from_f32(v[2] * scale)) |
-              (static_cast<uint32_t>(T::from_f32(v[3] * scale)) << 16);
+        w.x = T::pack2(v[0] * scale, v[1] * scale);
+        w.y = T::pack2(v[2] * scale, v[3] * scale);
         *reinterpret_cast<uint2*>(p) = w;
       } else {
         *reinterpret_cast<f32x4*>(p) = v * scale;

@@ -17,6 +17,7 @@ from multi_lora_amd.kernels import (
     sgemm_lora_b_fwd,
     sgemm_lora_b_multi_fwd,
 )
+from multi_lora_amd.kernels.lora_ops import apply_segments
 from multi_lora_amd.synthetic import make_meta
 from oracle.lora_ref import TorchLoRABackend, apply_f64, apply_kernel_numerics
 from tests.gpu_helpers import assert_tol_f64, assert_ulp_close
@@ -335,6 +336,47 @@ def test_streamed_lds_shrink_block_counts(dev, n_slices, r_max, ranks):
     assert_tol_f64(out, want)
     assert_ulp_close(out, kout, what="out")
     assert_ulp_close(mid, kmid, what="mid")
+
+
+@pytest.mark.parametrize("scal_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_streamed_paths_skip_out_of_pool_and_rank0_slots(dev, scal_dtype):
+    """Long segments take the streamed shrink and expand; the streamed
+    expand requests a tile's B and output rows before the slot's rank has
+    arrived (B through the slot clamped to the pool).  Slots outside the
+    pool on both sides and a rank-0 slot leave their rows as they were;
+    slots of both parities read a 16-bit scaling from either half of its
+    32-bit word.  Two calls and the one-call path agree bit for bit."""
+    g = torch.Generator().manual_seed(77)
+    in_dim, out_dim, r_max = 4096, 512, 32
+    lens = [130, 70, 96, 64, 150, 90]
+    slots = [1, -1, 0, 5, 3, 2]  # pool of 4: -1 and 5 lie outside it; slot 0 has rank 0
+    ranks = [0, 32, 16, 8]
+    scal = [0.75, 1.5, 2.0, 0.5]
+    rows = sum(lens)
+    assert rows >= 64 * len(lens)  # the streamed (long-segment) kernels
+    x = torch.randn(rows, in_dim, generator=g).bfloat16()
+    a = (torch.randn(len(ranks), r_max, in_dim, generator=g) * in_dim ** -0.5).bfloat16()
+    b = (torch.randn(len(ranks), out_dim, r_max, generator=g) * 0.05).bfloat16()
+    base = torch.randn(rows, out_dim, generator=g).bfloat16()
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", scal_dtype)
+    want = apply_f64(x, [a], [b], meta_cpu, base)
+    kmid, kout = apply_kernel_numerics(x, [a], [b], meta_cpu, base)
+    meta = make_meta(lens, slots, ranks, scal, dev, scal_dtype)
+    mid, out = run_hip(x.to(dev), [a.to(dev)], [b.to(dev)], meta, base.to(dev))
+    assert_tol_f64(out, want)
+    assert_ulp_close(out, kout, what="out")
+    one = base.to(dev)
+    apply_segments(x.to(dev), [a.to(dev)], [b.to(dev)], meta, one, [0])
+    torch.cuda.synchronize()
+    assert torch.equal(one.cpu(), out)
+    st = 0
+    for n, slot in zip(lens, slots):
+        if not 0 <= slot < len(ranks) or ranks[slot] == 0:
+            assert torch.equal(out[st:st + n], base[st:st + n]), (slot, st)
+            assert torch.count_nonzero(mid[st:st + n]) == 0, (slot, st)
+        else:
+            assert not torch.equal(out[st:st + n], base[st:st + n]), (slot, st)
+        st += n
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

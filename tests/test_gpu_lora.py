@@ -17,7 +17,7 @@ from multi_lora_amd.kernels import (
     sgemm_lora_b_fwd,
     sgemm_lora_b_multi_fwd,
 )
-from multi_lora_amd.kernels.lora_ops import apply_segments
+from multi_lora_amd.kernels.lora_ops import apply_segments, shrink
 from multi_lora_amd.synthetic import make_meta
 from oracle.lora_ref import TorchLoRABackend, apply_f64, apply_kernel_numerics
 from tests.gpu_helpers import assert_tol_f64, assert_ulp_close
@@ -311,6 +311,7 @@ def test_mixed_long_and_one_row_segments(dev, n_short):
     (2, 64, [64, 40, 0, 17]),    # eight blocks
     (3, 64, [64, 40, 0, 17]),    # twelve blocks: q|k, then v, one launch each
     (4, 48, [48, 33, 0, 7]),     # twelve blocks of three per slice: two launches of two slices
+    (1, 18, [18, 5, 0, 11]),     # r_max not a multiple of 4: split sums stored a column at a time
 ])
 def test_streamed_lds_shrink_block_counts(dev, n_slices, r_max, ranks):
     """Long segments with K a multiple of 64 take the shrink that streams x
@@ -336,6 +337,39 @@ def test_streamed_lds_shrink_block_counts(dev, n_slices, r_max, ranks):
     assert_tol_f64(out, want)
     assert_ulp_close(out, kout, what="out")
     assert_ulp_close(mid, kmid, what="mid")
+
+
+class _OffsetWorkspace:
+    """A workspace whose pointer is `offset` bytes past a fresh allocation."""
+
+    def __init__(self, offset):
+        self.offset, self.buf = offset, None
+
+    def get(self, need, dev):
+        self.buf = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        return self.buf.data_ptr() + self.offset, need
+
+
+def test_streamed_shrink_split_sums_in_an_unaligned_workspace(dev):
+    """The streamed shrink stores its split sums 16 bytes at a time when the
+    workspace allows it, and a column at a time when the caller's workspace
+    is only 4-byte aligned: the results are the same bit for bit."""
+    wl = synthetic.prefill_mlp(device=dev, part="gate_up", n_seg=4, min_len=64, max_len=200, hidden=4096,
+                               inter=1024, seed=11)
+    r_max = wl.a_stacks[0].shape[1]
+    outs = []
+    for ws in (None, _OffsetWorkspace(4), _OffsetWorkspace(8)):
+        mid = torch.full((wl.x.shape[0], len(wl.a_stacks) * r_max), float("nan"), dtype=wl.x.dtype, device=dev)
+        if ws is None:
+            sgemm_lora_a_multi_fwd(wl.x, wl.a_stacks, wl.meta, mid)
+        else:
+            shrink(wl.x, wl.a_stacks, wl.meta, mid, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(mid.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    kmid, _ = apply_kernel_numerics(wl.x.cpu(), [a.cpu() for a in wl.a_stacks], [b.cpu() for b in wl.b_stacks],
+                                    cpu_meta(wl.meta), wl.base.cpu(), wl.col_offsets)
+    assert_ulp_close(outs[0], kmid, what="mid")
 
 
 @pytest.mark.parametrize("scal_dtype", [torch.bfloat16, torch.float16, torch.float32])

@@ -92,14 +92,16 @@ def test_decode_qkv_multi_slice(dev):
     check_workload(synthetic.decode_qkv(device=dev))
 
 
-def test_prefill_gate_up_reduced(dev):
-    wl = synthetic.prefill_mlp(device=dev, part="gate_up", n_seg=4, min_len=17, max_len=200, hidden=1024,
-                               inter=2816, seed=21)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_gate_up_reduced(dev, dtype):
+    wl = synthetic.prefill_mlp(device=dev, dtype=dtype, part="gate_up", n_seg=4, min_len=17, max_len=200,
+                               hidden=1024, inter=2816, seed=21)
     check_workload(wl)
 
 
-def test_prefill_down_reduced(dev):
-    wl = synthetic.prefill_mlp(device=dev, part="down", n_seg=5, min_len=1, max_len=150, hidden=768,
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_down_reduced(dev, dtype):
+    wl = synthetic.prefill_mlp(device=dev, dtype=dtype, part="down", n_seg=5, min_len=1, max_len=150, hidden=768,
                                inter=3584, seed=22)
     check_workload(wl)
 

@@ -55,14 +55,18 @@ class DecoderConfig:
 
 
 class StaticKV:
-    """Per-layer K and V buffers ``[batch, kv_heads, max_len, head_dim]``, allocated once."""
+    """Per-layer key and value buffers, allocated once: keys
+    ``[batch, kv_heads, head_dim, max_len]`` (stored transposed, so the score
+    product reads them in place as its contiguous right operand) and values
+    ``[batch, kv_heads, max_len, head_dim]``."""
 
     def __init__(self, config: DecoderConfig, batch: int, max_len: int, device, dtype) -> None:
-        shape = (batch, config.num_key_value_heads, max_len, config.head_dim)
+        kshape = (batch, config.num_key_value_heads, config.head_dim, max_len)
+        vshape = (batch, config.num_key_value_heads, max_len, config.head_dim)
         self.max_len = max_len
-        self.keys: List[torch.Tensor] = [torch.zeros(shape, device=device, dtype=dtype)
+        self.keys: List[torch.Tensor] = [torch.zeros(kshape, device=device, dtype=dtype)
                                          for _ in range(config.num_hidden_layers)]
-        self.values: List[torch.Tensor] = [torch.zeros(shape, device=device, dtype=dtype)
+        self.values: List[torch.Tensor] = [torch.zeros(vshape, device=device, dtype=dtype)
                                            for _ in range(config.num_hidden_layers)]
 
 
@@ -106,7 +110,8 @@ class Attention(nn.Module):
         """Rotary attention of ``b`` sequences of ``t`` rows (projections given
         row-major, ``[b*t, heads*d]`` or ``[b, t, heads*d]``); writes this
         step's keys and values into ``kv`` at ``cache_position`` and attends
-        over the whole cache under ``mask``.  Returns ``[b, t, heads*d]`` fp32."""
+        over the whole cache under ``mask``.  Returns ``[b, t, heads*d]`` in
+        the model dtype."""
         c = self.c
         h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         rep = h // kvh
@@ -114,19 +119,23 @@ class Attention(nn.Module):
         q = q.reshape(b, t, h, d).transpose(1, 2).float()
         k = k.reshape(b, t, kvh, d).transpose(1, 2).float()
         v = v.reshape(b, t, kvh, d).transpose(1, 2)
-        q, k = _rotate(q, cos, sin).to(dt), _rotate(k, cos, sin).to(dt)
+        # The score scale is applied to q in fp32, before its one rounding.
+        q, k = (_rotate(q, cos, sin) * (1.0 / math.sqrt(d))).to(dt), _rotate(k, cos, sin).to(dt)
         if kv is not None:
-            kv.keys[layer].index_copy_(2, cache_position, k.to(kv.keys[layer].dtype))
+            kv.keys[layer].index_copy_(3, cache_position, k.transpose(-1, -2).to(kv.keys[layer].dtype))
             kv.values[layer].index_copy_(2, cache_position, v.to(kv.values[layer].dtype))
-            k, v = kv.keys[layer], kv.values[layer]
-        length = k.shape[2]
+            keys_t, v = kv.keys[layer].to(dt), kv.values[layer]                  # keys_t [b, kvh, d, L]
+        else:
+            keys_t = k.transpose(-1, -2).contiguous()
+        length = keys_t.shape[-1]
         # The query heads sharing a key head are stacked as rows, so keys and
-        # values are read once per key head, never repeated.
+        # values are read once per key head, never repeated.  Scores stay in
+        # the model dtype, masked in place; softmax computes a 16-bit input
+        # in fp32 and rounds its output once.
         qg = q.reshape(b, kvh, rep * t, d)
-        keys_t = k.to(dt).transpose(-1, -2).contiguous()                     # [b, kvh, d, L]
-        scores = torch.matmul(qg, keys_t).float() / math.sqrt(d)              # [b, kvh, rep*t, L]
-        scores = scores.view(b, kvh, rep, t, length).masked_fill(~mask[:, :, None], float("-inf"))
-        probs = torch.softmax(scores, dim=-1).to(dt).view(b, kvh, rep * t, length)
+        scores = torch.matmul(qg, keys_t)                                     # [b, kvh, rep*t, L]
+        scores.view(b, kvh, rep, t, length).masked_fill_(~mask[:, :, None], float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
         out = torch.matmul(probs, v.to(dt).contiguous())                      # [b, kvh, rep*t, d]
         return out.view(b, h, t, d).transpose(1, 2).reshape(b, t, h * d)
 

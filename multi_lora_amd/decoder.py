@@ -84,10 +84,33 @@ class DecoderRMSNorm(nn.Module):
         return h.to(x.dtype)
 
 
+@dataclass
+class Rotary:
+    """Rotary tables for rows ``[b, t]`` in the model dtype, shaped
+    ``[b, t, 1, head_dim]`` to broadcast over a projection's output viewed as
+    ``[b, t, heads, head_dim]``: ``cos`` and the signed ``sin`` (``-sin`` on
+    the first half), so that ``rotate(x) = x * cos + roll(x, d/2) * sin``.
+    q's tables also carry the score scale ``1/sqrt(head_dim)``."""
+
+    cos_q: torch.Tensor
+    sin_q: torch.Tensor
+    cos_k: torch.Tensor
+    sin_k: torch.Tensor
+
+    @staticmethod
+    def make(positions: torch.Tensor, inv_freq: torch.Tensor, dtype) -> "Rotary":
+        ang = positions.float()[..., None] * inv_freq                    # [b, t, d/2]
+        c, s = ang.cos(), ang.sin()
+        cos = torch.cat((c, c), dim=-1)[:, :, None]                      # [b, t, 1, d]
+        sin = torch.cat((-s, s), dim=-1)[:, :, None]
+        scale = 1.0 / math.sqrt(2 * inv_freq.numel())
+        return Rotary((cos * scale).to(dtype), (sin * scale).to(dtype), cos.to(dtype), sin.to(dtype))
+
+
 def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    half = x.shape[-1] // 2
-    x1, x2 = x[..., :half], x[..., half:]
-    return x * cos + torch.cat((-x2, x1), dim=-1) * sin
+    """``x * cos + rotate_half(x) * sin`` with the sign of rotate_half folded
+    into ``sin``: three element-wise kernels in the model dtype."""
+    return torch.addcmul(x * cos, x.roll(x.shape[-1] // 2, dims=-1), sin)
 
 
 class Attention(nn.Module):
@@ -100,13 +123,13 @@ class Attention(nn.Module):
         self.v_proj = nn.Linear(c.hidden_size, c.num_key_value_heads * d, bias=False)
         self.o_proj = nn.Linear(c.num_attention_heads * d, c.hidden_size, bias=False)
 
-    def forward(self, x, cos, sin, mask, kv: Optional[StaticKV], layer: int, cache_position):
+    def forward(self, x, rot: Rotary, mask, kv: Optional[StaticKV], layer: int, cache_position):
         b, t, _ = x.shape
-        out = self._attend(self.q_proj(x), self.k_proj(x), self.v_proj(x), b, t, cos, sin, mask, kv, layer,
+        out = self._attend(self.q_proj(x), self.k_proj(x), self.v_proj(x), b, t, rot, mask, kv, layer,
                            cache_position)
         return self.o_proj(out.to(x.dtype))
 
-    def _attend(self, q, k, v, b, t, cos, sin, mask, kv: Optional[StaticKV], layer: int, cache_position):
+    def _attend(self, q, k, v, b, t, rot: Rotary, mask, kv: Optional[StaticKV], layer: int, cache_position):
         """Rotary attention of ``b`` sequences of ``t`` rows (projections given
         row-major, ``[b*t, heads*d]`` or ``[b, t, heads*d]``); writes this
         step's keys and values into ``kv`` at ``cache_position`` and attends
@@ -116,11 +139,11 @@ class Attention(nn.Module):
         h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         rep = h // kvh
         dt = q.dtype
-        q = q.reshape(b, t, h, d).transpose(1, 2).float()
-        k = k.reshape(b, t, kvh, d).transpose(1, 2).float()
+        # Rotated in the projections' own layout, then laid out per head:
+        # q [b, h, t, d] (scaled for the scores), k [b, kvh, t, d].
+        q = _rotate(q.reshape(b, t, h, d), rot.cos_q, rot.sin_q).transpose(1, 2).contiguous()
+        k = _rotate(k.reshape(b, t, kvh, d), rot.cos_k, rot.sin_k).transpose(1, 2)
         v = v.reshape(b, t, kvh, d).transpose(1, 2)
-        # The score scale is applied to q in fp32, before its one rounding.
-        q, k = (_rotate(q, cos, sin) * (1.0 / math.sqrt(d))).to(dt), _rotate(k, cos, sin).to(dt)
         if kv is not None:
             kv.keys[layer].index_copy_(3, cache_position, k.transpose(-1, -2).to(kv.keys[layer].dtype))
             kv.values[layer].index_copy_(2, cache_position, v.to(kv.values[layer].dtype))
@@ -150,7 +173,7 @@ class Attention(nn.Module):
             if part.n == 0:
                 continue
             rows = slice(part.row0, part.row0 + part.n * part.t)
-            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.cos, part.sin, part.mask, part.kv,
+            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.rot, part.mask, part.kv,
                              layer, part.cache_position)
             outs.append(o.reshape(part.n * part.t, -1))
         return self.o_proj(torch.cat(outs).to(x.dtype))
@@ -175,8 +198,8 @@ class Block(nn.Module):
         self.post_attention_layernorm = DecoderRMSNorm(c.hidden_size, c.rms_norm_eps)
         self.mlp = MLP(c)
 
-    def forward(self, x, cos, sin, mask, kv, layer, cache_position):
-        x = x + self.self_attn(self.input_layernorm(x), cos, sin, mask, kv, layer, cache_position)
+    def forward(self, x, rot: Rotary, mask, kv, layer, cache_position):
+        x = x + self.self_attn(self.input_layernorm(x), rot, mask, kv, layer, cache_position)
         return x + self.mlp(self.post_attention_layernorm(x))
 
     def forward_mixed(self, x, pre, dec, layer):
@@ -191,8 +214,7 @@ class Packed:
     n: int
     t: int
     row0: int
-    cos: torch.Tensor
-    sin: torch.Tensor
+    rot: Rotary
     mask: torch.Tensor
     kv: Optional[StaticKV]
     cache_position: Optional[torch.Tensor]
@@ -220,21 +242,13 @@ class Decoder(nn.Module):
             cache_position = torch.arange(t, device=dev)
         if position_ids is None:
             position_ids = cache_position.view(1, t).expand(b, t)
-        ang = position_ids.float()[..., None] * self.inv_freq            # [b, t, d/2]
-        ang = torch.cat((ang, ang), dim=-1)[:, None]                     # [b, 1, t, d]
-        cos, sin = ang.cos(), ang.sin()
+        x = self.embed_tokens(input_ids)
+        rot = Rotary.make(position_ids.expand(b, t), self.inv_freq, x.dtype)
         length = kv.max_len if kv is not None else t
         mask = self._mask(attention_mask, b, t, length, cache_position, dev)
-        x = self.embed_tokens(input_ids)
         for i, layer in enumerate(self.layers):
-            x = layer(x, cos, sin, mask, kv, i, cache_position)
+            x = layer(x, rot, mask, kv, i, cache_position)
         return SimpleNamespace(logits=self.lm_head(self.norm(x)))
-
-    def _rope(self, positions: torch.Tensor):
-        """cos, sin ``[b, 1, t, head_dim]`` for integer positions ``[b, t]``."""
-        ang = positions.float()[..., None] * self.inv_freq
-        ang = torch.cat((ang, ang), dim=-1)[:, None]
-        return ang.cos(), ang.sin()
 
     def forward_mixed(self, prompt_ids: torch.Tensor, decode_ids: torch.Tensor, decode_kv: StaticKV,
                       decode_pos: torch.Tensor):
@@ -253,12 +267,11 @@ class Decoder(nn.Module):
         x = torch.cat((self.embed_tokens(prompt_ids).reshape(p * t, -1),
                        self.embed_tokens(decode_ids).reshape(d, -1)))
         pos = torch.arange(t, device=dev)
-        cos, sin = self._rope(pos.view(1, t))
         causal = (pos[None, :] <= pos[:, None]).view(1, 1, t, t)
-        pre = Packed(p, t, 0, cos, sin, causal, None, None)
-        cos_d, sin_d = self._rope(decode_pos.view(1, 1))
+        pre = Packed(p, t, 0, Rotary.make(pos.view(1, t), self.inv_freq, x.dtype), causal, None, None)
         seen = (torch.arange(decode_kv.max_len, device=dev) <= decode_pos).view(1, 1, 1, -1)
-        dec = Packed(d, 1, p * t, cos_d, sin_d, seen, decode_kv, decode_pos)
+        dec = Packed(d, 1, p * t, Rotary.make(decode_pos.view(1, 1), self.inv_freq, x.dtype), seen, decode_kv,
+                     decode_pos)
         for i, layer in enumerate(self.layers):
             x = layer.forward_mixed(x, pre, dec, i)
         last = torch.cat((torch.arange(t - 1, p * t, t, device=dev), torch.arange(p * t, p * t + d, device=dev)))

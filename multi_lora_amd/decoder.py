@@ -123,17 +123,18 @@ class Attention(nn.Module):
         self.v_proj = nn.Linear(c.hidden_size, c.num_key_value_heads * d, bias=False)
         self.o_proj = nn.Linear(c.num_attention_heads * d, c.hidden_size, bias=False)
 
-    def forward(self, x, rot: Rotary, mask, kv: Optional[StaticKV], layer: int, cache_position):
+    def forward(self, x, rot: Rotary, hide, kv: Optional[StaticKV], layer: int, cache_position):
         b, t, _ = x.shape
-        out = self._attend(self.q_proj(x), self.k_proj(x), self.v_proj(x), b, t, rot, mask, kv, layer,
+        out = self._attend(self.q_proj(x), self.k_proj(x), self.v_proj(x), b, t, rot, hide, kv, layer,
                            cache_position)
         return self.o_proj(out.to(x.dtype))
 
-    def _attend(self, q, k, v, b, t, rot: Rotary, mask, kv: Optional[StaticKV], layer: int, cache_position):
+    def _attend(self, q, k, v, b, t, rot: Rotary, hide, kv: Optional[StaticKV], layer: int, cache_position):
         """Rotary attention of ``b`` sequences of ``t`` rows (projections given
         row-major, ``[b*t, heads*d]`` or ``[b, t, heads*d]``); writes this
         step's keys and values into ``kv`` at ``cache_position`` and attends
-        over the whole cache under ``mask``.  Returns ``[b, t, heads*d]`` in
+        over the whole cache, except the key positions ``hide`` marks
+        (boolean ``[b, 1, t, L]``, True = not attended).  Returns ``[b, t, heads*d]`` in
         the model dtype."""
         c = self.c
         h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
@@ -157,7 +158,7 @@ class Attention(nn.Module):
         # in fp32 and rounds its output once.
         qg = q.reshape(b, kvh, rep * t, d)
         scores = torch.matmul(qg, keys_t)                                     # [b, kvh, rep*t, L]
-        scores.view(b, kvh, rep, t, length).masked_fill_(~mask[:, :, None], float("-inf"))
+        scores.view(b, kvh, rep, t, length).masked_fill_(hide[:, :, None], float("-inf"))
         probs = torch.softmax(scores, dim=-1)
         out = torch.matmul(probs, v.to(dt).contiguous())                      # [b, kvh, rep*t, d]
         return out.view(b, h, t, d).transpose(1, 2).reshape(b, t, h * d)
@@ -173,7 +174,7 @@ class Attention(nn.Module):
             if part.n == 0:
                 continue
             rows = slice(part.row0, part.row0 + part.n * part.t)
-            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.rot, part.mask, part.kv,
+            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.rot, part.hide, part.kv,
                              layer, part.cache_position)
             outs.append(o.reshape(part.n * part.t, -1))
         return self.o_proj(torch.cat(outs).to(x.dtype))
@@ -198,8 +199,8 @@ class Block(nn.Module):
         self.post_attention_layernorm = DecoderRMSNorm(c.hidden_size, c.rms_norm_eps)
         self.mlp = MLP(c)
 
-    def forward(self, x, rot: Rotary, mask, kv, layer, cache_position):
-        x = x + self.self_attn(self.input_layernorm(x), rot, mask, kv, layer, cache_position)
+    def forward(self, x, rot: Rotary, hide, kv, layer, cache_position):
+        x = x + self.self_attn(self.input_layernorm(x), rot, hide, kv, layer, cache_position)
         return x + self.mlp(self.post_attention_layernorm(x))
 
     def forward_mixed(self, x, pre, dec, layer):
@@ -215,7 +216,7 @@ class Packed:
     t: int
     row0: int
     rot: Rotary
-    mask: torch.Tensor
+    hide: torch.Tensor  # True: key position not attended
     kv: Optional[StaticKV]
     cache_position: Optional[torch.Tensor]
 
@@ -245,9 +246,9 @@ class Decoder(nn.Module):
         x = self.embed_tokens(input_ids)
         rot = Rotary.make(position_ids.expand(b, t), self.inv_freq, x.dtype)
         length = kv.max_len if kv is not None else t
-        mask = self._mask(attention_mask, b, t, length, cache_position, dev)
+        hide = ~self._mask(attention_mask, b, t, length, cache_position, dev)  # once for every layer
         for i, layer in enumerate(self.layers):
-            x = layer(x, rot, mask, kv, i, cache_position)
+            x = layer(x, rot, hide, kv, i, cache_position)
         return SimpleNamespace(logits=self.lm_head(self.norm(x)))
 
     def forward_mixed(self, prompt_ids: torch.Tensor, decode_ids: torch.Tensor, decode_kv: StaticKV,
@@ -267,10 +268,10 @@ class Decoder(nn.Module):
         x = torch.cat((self.embed_tokens(prompt_ids).reshape(p * t, -1),
                        self.embed_tokens(decode_ids).reshape(d, -1)))
         pos = torch.arange(t, device=dev)
-        causal = (pos[None, :] <= pos[:, None]).view(1, 1, t, t)
-        pre = Packed(p, t, 0, Rotary.make(pos.view(1, t), self.inv_freq, x.dtype), causal, None, None)
-        seen = (torch.arange(decode_kv.max_len, device=dev) <= decode_pos).view(1, 1, 1, -1)
-        dec = Packed(d, 1, p * t, Rotary.make(decode_pos.view(1, 1), self.inv_freq, x.dtype), seen, decode_kv,
+        later = (pos[None, :] > pos[:, None]).view(1, 1, t, t)
+        pre = Packed(p, t, 0, Rotary.make(pos.view(1, t), self.inv_freq, x.dtype), later, None, None)
+        unseen = (torch.arange(decode_kv.max_len, device=dev) > decode_pos).view(1, 1, 1, -1)
+        dec = Packed(d, 1, p * t, Rotary.make(decode_pos.view(1, 1), self.inv_freq, x.dtype), unseen, decode_kv,
                      decode_pos)
         for i, layer in enumerate(self.layers):
             x = layer.forward_mixed(x, pre, dec, i)

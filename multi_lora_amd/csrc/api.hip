@@ -210,13 +210,7 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
   args.ks = ks;
   hipError_t e;
   if (mixed) {
-    // Tiles of 32 rows over the long segments: at most (rows + 31 * segs) / 32.
-    // At least one unit, which loops over every long tile should the summary
-    // have none (max_len > 16 says there is one).
-    const int64_t long_units = std::max<int64_t>(
-        1, (static_cast<int64_t>(meta->long_rows) + static_cast<int64_t>(mlora::kExpandLongBM - 1) * meta->long_segs) /
-               mlora::kExpandLongBM);
-    e = mlora::launch_mixed(args, dtype, static_cast<int>(long_units), meta->short_slots,
+    e = mlora::launch_mixed(args, dtype, meta->long_rows, meta->long_segs, meta->short_slots, num_cus(),
                             static_cast<hipStream_t>(stream));
   } else {
     e = mlora::launch_expand(bm, args, dtype, aligned, static_cast<hipStream_t>(stream));

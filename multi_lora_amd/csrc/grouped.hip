@@ -12,6 +12,7 @@
 // MFMA, scales and rounds (sgemm_lora_b.py:84-89), and adds into the output
 // rows through an LDS transpose.  The long segments' row tiles follow in the
 // same launch (expand_tile.h).
+#include "expand_dma.h"
 #include "expand_tile.h"
 #include "kernels.h"
 #include "loads.h"
@@ -281,18 +282,27 @@ __device__ int short_slot(const unsigned* bits, const int* offs, int nwords, int
 
 // One launch over a mixed batch: slot-grouped items for the short segments,
 // then tiled units for the long ones (see launch_mixed).  FUSED: y from
-// the shrink's split sums (ea.partials, ea.ks splits), else from mid.
-template <class T, bool FUSED, int RS>
+// the shrink's split sums (ea.partials, ea.ks splits), else from mid.  LBM:
+// rows of a long-segment tile, 32 (expand_kernel's register-prefetched
+// tile) or 64 (expand_dma_kernel's tile streamed through LDS; y from mid
+// only).  A workgroup runs units of one kind, so the kinds share one LDS
+// area.
+template <class T, bool FUSED, int RS, int LBM>
 __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, GroupedArgs ga, int long_units,
                                                               int short_units) {
-  __shared__ __attribute__((aligned(16))) ExpandTileLds<T, kExpandLongBM, FUSED> tl;
-  __shared__ __attribute__((aligned(16))) ExpandLds<T, 1> gl;
+  constexpr bool STREAMED = LBM == kExpandStreamBM;
+  static_assert(LBM == kExpandLongBM || (STREAMED && !FUSED), "32-row tiles, or 64-row streamed ones from mid");
+  using TileLds = ExpandTileLds<T, kExpandLongBM, FUSED>;
+  constexpr int kLongBytes = STREAMED ? expand_dma_lds_bytes<LBM>() : static_cast<int>(sizeof(TileLds));
+  constexpr int kShortBytes = static_cast<int>(sizeof(ExpandLds<T, 1>));
+  __shared__ __attribute__((aligned(1024))) unsigned char area[kLongBytes > kShortBytes ? kLongBytes : kShortBytes];
   __shared__ unsigned bits[kMixedMaxSlots / 32];
   __shared__ int offs[kMixedMaxSlots / 32];
   __shared__ int pick;
   const int nt = ea.n_tiles;
   const int b = blockIdx.x;
   if (b < short_units * nt) {
+    auto& gl = *reinterpret_cast<ExpandLds<T, 1>*>(area);
     const int j = b / nt;
     const int nt_g = b - j * nt;
     const int n_short = short_slot_map(ga, bits, offs, gl.tmp);
@@ -312,35 +322,80 @@ __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, Gro
   const int nt_g = (b - short_units * nt) - u * nt;
   TileRef tr;
   bool found;
-  const int total = long_tile(ea.meta, ea.rows, u, kExpandLongBM, kShortSegRows, &tr, &found);
-  if (found) expand_tile<T, kExpandLongBM, true, FUSED>(ea, tr, nt_g, tl);
+  const int total = long_tile(ea.meta, ea.rows, u, LBM, kShortSegRows, &tr, &found);
+  if (found) {
+    if constexpr (STREAMED)
+      expand_dma_tile<T, LBM>(ea, tr, nt_g, area);
+    else
+      expand_tile<T, LBM, true, FUSED>(ea, tr, nt_g, *reinterpret_cast<TileLds*>(area));
+  }
   // More long tiles than the launch has units for: this unit also takes
-  // tiles u + long_units, u + 2 long_units, ...
+  // tiles u + long_units, u + 2 long_units, ...  Streamed tiles go as two
+  // halves of 32 rows here: the 64-row body inside a loop does not fit the
+  // registers (values hoisted out of the loop stay live across it).
   for (int t = u + long_units; t < total; t += long_units) {
     __syncthreads();
-    long_tile(ea.meta, ea.rows, t, kExpandLongBM, kShortSegRows, &tr, &found);
-    if (found) expand_tile<T, kExpandLongBM, true, FUSED>(ea, tr, nt_g, tl);
+    long_tile(ea.meta, ea.rows, t, LBM, kShortSegRows, &tr, &found);
+    if (!found) continue;
+    if constexpr (STREAMED) {
+      constexpr int HBM = LBM / 2;
+      TileRef h = tr;
+      h.mt = 2 * tr.mt;
+      expand_dma_tile<T, HBM>(ea, h, nt_g, area);
+      h.mt += 1;
+      if (h.start + h.mt * HBM < h.end) {
+        __syncthreads();
+        expand_dma_tile<T, HBM>(ea, h, nt_g, area);
+      }
+    } else {
+      expand_tile<T, LBM, true, FUSED>(ea, tr, nt_g, *reinterpret_cast<TileLds*>(area));
+    }
   }
 }
 
-template <class T, bool FUSED>
-hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int long_units, int short_units,
-                          hipStream_t stream) {
+// Long-segment tiles of LBM rows: at most (rows + (LBM - 1) segs) / LBM.
+// At least one unit, which loops over every long tile should the summary
+// have none.
+template <int LBM>
+int64_t mixed_long_units(int64_t long_rows, int long_segs) {
+  return std::max<int64_t>(1, (long_rows + static_cast<int64_t>(LBM - 1) * long_segs) / LBM);
+}
+
+template <class T, bool FUSED, int LBM>
+hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int64_t long_rows, int long_segs,
+                          int short_units, hipStream_t stream) {
+  const int64_t lu = mixed_long_units<LBM>(long_rows, long_segs);
+  if (lu > INT32_MAX) return hipErrorInvalidConfiguration;
+  const int long_units = static_cast<int>(lu);
   const int64_t blocks = (static_cast<int64_t>(long_units) + short_units) * ea.n_tiles;
   if (blocks <= 0) return hipSuccess;
   if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   if (ga.r_max <= T::KSTEP)
-    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                       ea, ga, long_units, short_units);
+    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, ea, ga, long_units, short_units);
   else
-    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 2>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                       ea, ga, long_units, short_units);
+    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 2, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, ea, ga, long_units, short_units);
   return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_mixed_dt(const ExpandArgs& ea, const GroupedArgs& ga, bool fused, int64_t long_rows, int long_segs,
+                           int short_units, int cus, hipStream_t stream) {
+  if (fused) return launch_mixed_t<T, true, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, stream);
+  // Streamed 64-row tiles when they give every CU at least its four
+  // workgroups (c5 gate|up: 1792 of them, 39.4 vs 40.7 us); fewer, larger
+  // tiles leave CUs idle (c5 q|k|v: 384, 13.0 vs 12.1 us).
+  const int64_t streamed = mixed_long_units<kExpandStreamBM>(long_rows, long_segs) * ea.n_tiles;
+  if (streamed >= 4 * static_cast<int64_t>(cus))
+    return launch_mixed_t<T, false, kExpandStreamBM>(ea, ga, long_rows, long_segs, short_units, stream);
+  return launch_mixed_t<T, false, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, stream);
 }
 
 }  // namespace
 
-hipError_t launch_mixed(const ExpandArgs& args, int dtype, int long_units, int short_units, hipStream_t stream) {
+hipError_t launch_mixed(const ExpandArgs& args, int dtype, int64_t long_rows, int long_segs, int short_units,
+                        int cus, hipStream_t stream) {
   GroupedArgs ga{};
   ga.rows = args.rows;
   for (int s = 0; s < kMaxSlices; ++s) ga.slices[s] = args.slices[s];
@@ -358,11 +413,8 @@ hipError_t launch_mixed(const ExpandArgs& args, int dtype, int long_units, int s
   ga.mid = args.mid;
   ga.mid_stride = args.mid_stride;
   const bool fused = args.ks > 1 && args.partials != nullptr;
-  if (dtype == MLORA_BF16)
-    return fused ? launch_mixed_t<BF16, true>(args, ga, long_units, short_units, stream)
-                 : launch_mixed_t<BF16, false>(args, ga, long_units, short_units, stream);
-  return fused ? launch_mixed_t<F16, true>(args, ga, long_units, short_units, stream)
-               : launch_mixed_t<F16, false>(args, ga, long_units, short_units, stream);
+  return dtype == MLORA_BF16 ? launch_mixed_dt<BF16>(args, ga, fused, long_rows, long_segs, short_units, cus, stream)
+                             : launch_mixed_dt<F16>(args, ga, fused, long_rows, long_segs, short_units, cus, stream);
 }
 
 }  // namespace mlora

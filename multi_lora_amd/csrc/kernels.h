@@ -220,12 +220,15 @@ constexpr int kMixedMaxSlots = 2048;
 // One launch for a batch mixing long and short segments: units
 // [0, short_units * n_tiles) are slot-grouped items (distinct slot of the
 // short segments, in slot order; 256-column tile), which read each adapter's
-// B tile once for all of that slot's short rows; the next
-// long_units * n_tiles are (32-row tile of a long segment, 256-column tile),
-// as expand_kernel's.  The kernel recounts both from the table: a count
-// given too small is covered by looping, one too large leaves units that
-// exit.
-hipError_t launch_mixed(const ExpandArgs& args, int dtype, int long_units, int short_units, hipStream_t stream);
+// B tile once for all of that slot's short rows; the next units are (row
+// tile of a long segment, 256-column tile): 64 rows streamed through LDS as
+// expand_dma_kernel's when y comes from mid and such tiles give each of the
+// `cus` CUs four workgroups, else 32 rows as expand_kernel's.  The long
+// units are counted from the summary's long_rows and long_segs.  The kernel
+// recounts both kinds from the table: a count given too small is covered by
+// looping, one too large leaves units that exit.
+hipError_t launch_mixed(const ExpandArgs& args, int dtype, int64_t long_rows, int long_segs, int short_units,
+                        int cus, hipStream_t stream);
 
 
 // -------------------------------------------------------------- rmsnorm

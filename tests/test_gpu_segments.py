@@ -150,6 +150,18 @@ MIXED_CASES = [
     # rank-0, out-of-pool and empty short segments next to live ones
     ("odd_slots", [100, 1, 1, 4, 1, 0, 3, 1, 33], [0, 9, -1, 1, 2, 1, 1, 3, 2], [16, 16, 0, 16], 1024, [512], 16,
      torch.bfloat16),
+    # wide enough for 64-row long tiles streamed through LDS (17 row tiles x
+    # 112 column tiles, at least four workgroups a CU on a 256-CU GPU)
+    ("gate_up_streamed", [512, 512] + [1] * 64, None, [16] * 48 + [0] * 16, 1024, [14336, 14336], 16,
+     torch.bfloat16),
+    # streamed, fp16: ragged long segments (not multiples of 64 rows; ranks
+    # 32, 0, 24, 8), short ones of 1..16 rows, ranks below r_max
+    ("ragged_streamed_f16", [700, 333, 5, 70, 1, 16, 17, 2, 1, 9] + [1] * 30,
+     [0, 2, 5, 1, 3, 6, 4, 7, 9, 10] + [(7 * i) % 64 for i in range(30)],
+     [32, 24, 0, 32, 8, 16, 32, 24] * 8, 1024, [12288, 12288], 32, torch.float16),
+    # streamed at r_max 64 (two MFMA K-steps)
+    ("r64_streamed", [640, 384] + [1, 2, 3, 16] * 10, None, [64, 40, 16, 0] * 16, 1024, [14336, 14336], 64,
+     torch.bfloat16),
 ]
 
 
@@ -159,7 +171,9 @@ def test_mixed_batch_expand_equals_tiled(dev, name, lens, slots, ranks, in_dim, 
     the one-launch mixed expand (slot-grouped items for the short segments);
     without it, every segment is tiled.  Results are equal bit for bit, also
     when the summary is wrong (too small: units loop; too large: units exit),
-    and match the oracle."""
+    and match the oracle.  A summary of 5/8 of the long rows in one segment
+    keeps the streamed cases streamed, with too few units: the extra tiles
+    go as 32-row halves."""
     g = torch.Generator().manual_seed(len(name))
     if slots is None:
         slots = [0] * 2 + zipf_slots(g, len(lens) - 2, 512, len(ranks))
@@ -177,8 +191,8 @@ def test_mixed_batch_expand_equals_tiled(dev, name, lens, slots, ranks, in_dim, 
     long_segs, long_rows, short_slots = hinted.table_summary(len(ranks))
     assert long_segs > 0 and short_slots > 0, "the case must mix long and short segments"
     assert torch.equal(run(hinted), tiled), f"{name}: mixed expand differs from the tiled one"
-    for wrong in ((1, 1, 1), (long_segs, long_rows, max(1, short_slots // 3)), (long_segs + 5, long_rows + 900,
-                                                                               short_slots + 7)):
+    for wrong in ((1, 1, 1), (long_segs, long_rows, max(1, short_slots // 3)),
+                  (long_segs + 5, long_rows + 900, short_slots + 7), (1, max(1, long_rows * 5 // 8), short_slots)):
         bad = make_meta(lens, slots, ranks, scal, dev, dtype)
         bad.table_summary = lambda n, w=wrong: w
         assert torch.equal(run(bad), tiled), f"{name}: summary {wrong} changed the result"

@@ -286,10 +286,12 @@ __device__ int short_slot(const unsigned* bits, const int* offs, int nwords, int
 // rows of a long-segment tile, 32 (expand_kernel's register-prefetched
 // tile) or 64 (expand_dma_kernel's tile streamed through LDS; y from mid
 // only).  A workgroup runs units of one kind, so the kinds share one LDS
-// area.
+// area.  Unit order (each unit is n_tiles workgroups, the column tile
+// fastest): the short units first, or (interleave) long and short units
+// alternating while both last, then the rest.
 template <class T, bool FUSED, int RS, int LBM>
 __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, GroupedArgs ga, int long_units,
-                                                              int short_units) {
+                                                              int short_units, int interleave) {
   constexpr bool STREAMED = LBM == kExpandStreamBM;
   static_assert(LBM == kExpandLongBM || (STREAMED && !FUSED), "32-row tiles, or 64-row streamed ones from mid");
   using TileLds = ExpandTileLds<T, kExpandLongBM, FUSED>;
@@ -300,17 +302,29 @@ __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, Gro
   __shared__ int offs[kMixedMaxSlots / 32];
   __shared__ int pick;
   const int nt = ea.n_tiles;
-  const int b = blockIdx.x;
-  if (b < short_units * nt) {
+  const int v = blockIdx.x / nt;
+  const int nt_g = blockIdx.x - v * nt;
+  bool is_short;
+  int idx;
+  const int m = interleave ? min(long_units, short_units) : 0;
+  if (v < 2 * m) {
+    is_short = v & 1;
+    idx = v >> 1;
+  } else if (interleave) {
+    is_short = short_units > long_units;
+    idx = v - m;
+  } else {
+    is_short = v < short_units;
+    idx = is_short ? v : v - short_units;
+  }
+  if (is_short) {
     auto& gl = *reinterpret_cast<ExpandLds<T, 1>*>(area);
-    const int j = b / nt;
-    const int nt_g = b - j * nt;
+    const int j = idx;
     const int n_short = short_slot_map(ga, bits, offs, gl.tmp);
     const int nwords = (ga.meta.num_slots + 31) >> 5;
     // More short slots than the launch has units for (a summary from an
     // earlier table, e.g. in a replayed graph): this unit also takes slots
-    // j + short_units, j + 2 short_units, ...  These units come first in the
-    // grid, so such extra work overlaps the long tiles'.
+    // j + short_units, j + 2 short_units, ...
     for (int k = j; k < n_short; k += short_units) {
       const int slot = short_slot(bits, offs, nwords, k, &pick);
       expand_item<T, FUSED ? kSumF32 : kSumMid, 1, RS>(ga, slot, nt_g, gl);
@@ -318,8 +332,7 @@ __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, Gro
     }
     return;
   }
-  const int u = (b - short_units * nt) / nt;
-  const int nt_g = (b - short_units * nt) - u * nt;
+  const int u = idx;
   TileRef tr;
   bool found;
   const int total = long_tile(ea.meta, ea.rows, u, LBM, kShortSegRows, &tr, &found);
@@ -363,33 +376,40 @@ int64_t mixed_long_units(int64_t long_rows, int long_segs) {
 
 template <class T, bool FUSED, int LBM>
 hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int64_t long_rows, int long_segs,
-                          int short_units, hipStream_t stream) {
+                          int short_units, int cus, hipStream_t stream) {
   const int64_t lu = mixed_long_units<LBM>(long_rows, long_segs);
   if (lu > INT32_MAX) return hipErrorInvalidConfiguration;
   const int long_units = static_cast<int>(lu);
   const int64_t blocks = (static_cast<int64_t>(long_units) + short_units) * ea.n_tiles;
   if (blocks <= 0) return hipSuccess;
   if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
+  // Short items are latency-bound, long tiles bandwidth-bound.  Short items
+  // that fit in one round of workgroup slots (four a CU) go first, and the
+  // long tiles fill the other slots (c5 q|k|v: 672 short items, 24.6 vs 25.0
+  // us interleaved); more than that, and short-first would run rounds of
+  // short items alone before the first long tile, so the kinds alternate
+  // (c5 gate|up: 3136 short items, 49.7 vs 51.3 us).
+  const int interleave = static_cast<int64_t>(short_units) * ea.n_tiles > 4 * static_cast<int64_t>(cus) ? 1 : 0;
   if (ga.r_max <= T::KSTEP)
     hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, ea, ga, long_units, short_units);
+                       stream, ea, ga, long_units, short_units, interleave);
   else
     hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 2, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, ea, ga, long_units, short_units);
+                       stream, ea, ga, long_units, short_units, interleave);
   return hipGetLastError();
 }
 
 template <class T>
 hipError_t launch_mixed_dt(const ExpandArgs& ea, const GroupedArgs& ga, bool fused, int64_t long_rows, int long_segs,
                            int short_units, int cus, hipStream_t stream) {
-  if (fused) return launch_mixed_t<T, true, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, stream);
+  if (fused) return launch_mixed_t<T, true, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);
   // Streamed 64-row tiles when they give every CU at least its four
   // workgroups (c5 gate|up: 1792 of them, 39.4 vs 40.7 us); fewer, larger
   // tiles leave CUs idle (c5 q|k|v: 384, 13.0 vs 12.1 us).
   const int64_t streamed = mixed_long_units<kExpandStreamBM>(long_rows, long_segs) * ea.n_tiles;
   if (streamed >= 4 * static_cast<int64_t>(cus))
-    return launch_mixed_t<T, false, kExpandStreamBM>(ea, ga, long_rows, long_segs, short_units, stream);
-  return launch_mixed_t<T, false, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, stream);
+    return launch_mixed_t<T, false, kExpandStreamBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);
+  return launch_mixed_t<T, false, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);
 }
 
 }  // namespace

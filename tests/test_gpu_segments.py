@@ -199,6 +199,39 @@ def test_mixed_batch_expand_equals_tiled(dev, name, lens, slots, ranks, in_dim, 
     assert_tol_f64(tiled, apply_f64(x, As, Bs, meta_cpu, base, cols), name)
 
 
+@pytest.mark.parametrize("n_slots", [2048, 2049])
+def test_mixed_batch_expand_at_the_pool_size_limit(dev, n_slots):
+    """The mixed expand keeps the distinct short slots as a bitmap of 2048
+    slots in LDS: at 2048 slots it runs with short segments on slots at the
+    bitmap's word boundaries (31/32/33, 63/64, 1023/1024, 2047) and equals
+    the tiled result bit for bit; at 2049 slots the call takes the tiled
+    path.  Both match the oracle."""
+    short_slots = [0, 31, 32, 33, 63, 64, 1023, 1024, 2016, 2047, 32, 1024, 5, 2046]
+    lens = [100, 70] + [1, 3, 1, 16, 1, 2, 1, 1, 5, 1, 1, 9, 1, 1]
+    slots = [2047, 5] + short_slots
+    ranks = [16] * n_slots
+    ranks[33] = 0
+    ranks[1023] = 8
+    x, As, Bs, base, cols, _, _ = case(dev, lens, slots, ranks, 256, [512], 16, torch.bfloat16, 21)
+    # Scalings in the usual range (the helper's grow with the slot number).
+    scal = [0.5 + 0.25 * (i % 8) for i in range(n_slots)]
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", torch.bfloat16)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+
+    def run(meta):
+        out = base.to(dev).clone()
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=Workspace())
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    hinted = make_meta(lens, slots, ranks, scal, dev, torch.bfloat16)
+    long_segs, _, n_short = hinted.table_summary(n_slots)
+    assert long_segs == 2 and n_short == len(set(short_slots))
+    got = run(hinted)
+    assert torch.equal(got, run(make_meta(lens, slots, ranks, scal, dev, torch.bfloat16, host_copies=False)))
+    assert_tol_f64(got, apply_f64(x, As, Bs, meta_cpu, base, cols), f"{n_slots} slots")
+
+
 def test_mixed_batch_expand_in_a_replayed_graph_follows_table_rewrites(dev):
     """A captured mixed expand keeps the launch size of its capture; after an
     in-place rewrite that gives the short segments more distinct slots, the

@@ -322,9 +322,10 @@ __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, Gro
     const int j = idx;
     const int n_short = short_slot_map(ga, bits, offs, gl.tmp);
     const int nwords = (ga.meta.num_slots + 31) >> 5;
-    // More short slots than the launch has units for (a summary from an
-    // earlier table, e.g. in a replayed graph): this unit also takes slots
-    // j + short_units, j + 2 short_units, ...
+    // More short slots than the launch has units for (by design when the
+    // kinds are interleaved, or a summary from an earlier table, e.g. in a
+    // replayed graph): this unit also takes slots j + short_units,
+    // j + 2 short_units, ...
     for (int k = j; k < n_short; k += short_units) {
       const int slot = short_slot(bits, offs, nwords, k, &pick);
       expand_item<T, FUSED ? kSumF32 : kSumMid, 1, RS>(ga, slot, nt_g, gl);
@@ -380,16 +381,19 @@ hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int64_t l
   const int64_t lu = mixed_long_units<LBM>(long_rows, long_segs);
   if (lu > INT32_MAX) return hipErrorInvalidConfiguration;
   const int long_units = static_cast<int>(lu);
-  const int64_t blocks = (static_cast<int64_t>(long_units) + short_units) * ea.n_tiles;
-  if (blocks <= 0) return hipSuccess;
-  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   // Short items are latency-bound, long tiles bandwidth-bound.  Short items
   // that fit in one round of workgroup slots (four a CU) go first, and the
   // long tiles fill the other slots (c5 q|k|v: 672 short items, 24.6 vs 25.0
   // us interleaved); more than that, and short-first would run rounds of
   // short items alone before the first long tile, so the kinds alternate
-  // (c5 gate|up: 3136 short items, 49.7 vs 51.3 us).
+  // (c5 gate|up: 3136 short items, 49.7 vs 51.3 us), and each short unit
+  // takes two slots one after the other, which halves the workgroups that
+  // wait on their table scans (48.2 vs 49.4 us; three slots a unit: 48.5).
   const int interleave = static_cast<int64_t>(short_units) * ea.n_tiles > 4 * static_cast<int64_t>(cus) ? 1 : 0;
+  if (interleave) short_units = (short_units + 1) / 2;
+  const int64_t blocks = (static_cast<int64_t>(long_units) + short_units) * ea.n_tiles;
+  if (blocks <= 0) return hipSuccess;
+  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   if (ga.r_max <= T::KSTEP)
     hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        stream, ea, ga, long_units, short_units, interleave);

@@ -12,8 +12,12 @@ manager wraps them with ``LinearWithLoRA`` exactly as it wraps a Hugging Face
 model, and ``fuse_rmsnorm`` routes the norms through the HIP RMSNorm.
 
 Attention runs its two products in the model dtype (fp32 accumulation,
-contiguous operands) with the softmax in fp32; the query heads that share a
-key head are stacked as rows, so keys are never repeated.  The KV cache is
+contiguous operands, the score scale applied inside the first) with the
+softmax in fp32; the query heads that share a key head are stacked as rows,
+so keys are never repeated.  Rotary runs once per layer over q and k
+together when they are adjacent columns of one projection output (the fused
+q|k|v group's).  A block's residual adds travel to the next RMSNorm, which
+``fuse_rmsnorm`` turns into one fused add + RMSNorm kernel.  The KV cache is
 written in place at ``cache_position`` and read whole under a boolean mask,
 so a decode step touches fixed addresses and can be captured in a HIP graph.
 ``forward`` accepts the keyword arguments the reference passes to its model
@@ -83,28 +87,30 @@ class DecoderRMSNorm(nn.Module):
         h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.variance_epsilon) * self.weight.float()
         return h.to(x.dtype)
 
+    def add_forward(self, delta: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """``residual += delta`` (in place, rounded to the dtype), then the
+        norm of it; ``fuse_rmsnorm`` rebinds this to the fused HIP kernel."""
+        residual.add_(delta)
+        return self(residual)
+
 
 @dataclass
 class Rotary:
-    """Rotary tables for rows ``[b, t]`` in the model dtype, shaped
-    ``[b, t, 1, head_dim]`` to broadcast over a projection's output viewed as
-    ``[b, t, heads, head_dim]``: ``cos`` and the signed ``sin`` (``-sin`` on
-    the first half), so that ``rotate(x) = x * cos + roll(x, d/2) * sin``.
-    q's tables also carry the score scale ``1/sqrt(head_dim)``."""
+    """Rotary tables for ``R`` rows in the model dtype, shaped ``[R, 1, head_dim]``
+    to broadcast over rows viewed as ``[R, heads, head_dim]``: ``cos`` and the
+    signed ``sin`` (``-sin`` on the first half), so that
+    ``rotate(x) = x * cos + roll(x, d/2) * sin``."""
 
-    cos_q: torch.Tensor
-    sin_q: torch.Tensor
-    cos_k: torch.Tensor
-    sin_k: torch.Tensor
+    cos: torch.Tensor
+    sin: torch.Tensor
 
     @staticmethod
     def make(positions: torch.Tensor, inv_freq: torch.Tensor, dtype) -> "Rotary":
-        ang = positions.float()[..., None] * inv_freq                    # [b, t, d/2]
+        ang = positions.reshape(-1).float()[:, None] * inv_freq          # [R, d/2]
         c, s = ang.cos(), ang.sin()
-        cos = torch.cat((c, c), dim=-1)[:, :, None]                      # [b, t, 1, d]
-        sin = torch.cat((-s, s), dim=-1)[:, :, None]
-        scale = 1.0 / math.sqrt(2 * inv_freq.numel())
-        return Rotary((cos * scale).to(dtype), (sin * scale).to(dtype), cos.to(dtype), sin.to(dtype))
+        cos = torch.cat((c, c), dim=-1)[:, None]                          # [R, 1, d]
+        sin = torch.cat((-s, s), dim=-1)[:, None]
+        return Rotary(cos.to(dtype), sin.to(dtype))
 
 
 def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -118,6 +124,7 @@ class Attention(nn.Module):
         super().__init__()
         self.c = c
         d = c.head_dim
+        self.scale = 1.0 / math.sqrt(d)
         self.q_proj = nn.Linear(c.hidden_size, c.num_attention_heads * d, bias=False)
         self.k_proj = nn.Linear(c.hidden_size, c.num_key_value_heads * d, bias=False)
         self.v_proj = nn.Linear(c.hidden_size, c.num_key_value_heads * d, bias=False)
@@ -125,13 +132,28 @@ class Attention(nn.Module):
 
     def forward(self, x, rot: Rotary, hide, kv: Optional[StaticKV], layer: int, cache_position):
         b, t, _ = x.shape
-        out = self._attend(self.q_proj(x), self.k_proj(x), self.v_proj(x), b, t, rot, hide, kv, layer,
-                           cache_position)
+        q, k = self._rotate_qk(self.q_proj(x).reshape(b * t, -1), self.k_proj(x).reshape(b * t, -1), rot)
+        out = self._attend(q, k, self.v_proj(x), b, t, hide, kv, layer, cache_position)
         return self.o_proj(out.to(x.dtype))
 
-    def _attend(self, q, k, v, b, t, rot: Rotary, hide, kv: Optional[StaticKV], layer: int, cache_position):
-        """Rotary attention of ``b`` sequences of ``t`` rows (projections given
-        row-major, ``[b*t, heads*d]`` or ``[b, t, heads*d]``); writes this
+    def _rotate_qk(self, q: torch.Tensor, k: torch.Tensor, rot: Rotary):
+        """Rotary on rows ``q [R, h*d]`` and ``k [R, kvh*d]``; returns them as
+        ``[R, h, d]`` and ``[R, kvh, d]``.  When k's columns directly follow
+        q's in one tensor (the fused q|k|v output), both go through one set
+        of three kernels over the ``[R, h + kvh, d]`` view."""
+        c = self.c
+        h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        rows = q.shape[0]
+        if (q.stride(-1) == 1 and k.stride(-1) == 1 and q.stride(0) == k.stride(0) and q.dtype == k.dtype
+                and k.data_ptr() == q.data_ptr() + h * d * q.element_size()):
+            qk = torch.as_strided(q, (rows, h + kvh, d), (q.stride(0), d, 1))
+            r = _rotate(qk, rot.cos, rot.sin)
+            return r[:, :h], r[:, h:]
+        return (_rotate(q.reshape(rows, h, d), rot.cos, rot.sin), _rotate(k.reshape(rows, kvh, d), rot.cos, rot.sin))
+
+    def _attend(self, q, k, v, b, t, hide, kv: Optional[StaticKV], layer: int, cache_position):
+        """Attention of ``b`` sequences of ``t`` rows, given rotated ``q
+        [b*t, h, d]`` and ``k [b*t, kvh, d]`` and ``v`` row-major; writes this
         step's keys and values into ``kv`` at ``cache_position`` and attends
         over the whole cache, except the key positions ``hide`` marks
         (boolean ``[b, 1, t, L]``, True = not attended).  Returns ``[b, t, heads*d]`` in
@@ -140,42 +162,44 @@ class Attention(nn.Module):
         h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         rep = h // kvh
         dt = q.dtype
-        # Rotated in the projections' own layout, then laid out per head:
-        # q [b, h, t, d] (scaled for the scores), k [b, kvh, t, d].
-        q = _rotate(q.reshape(b, t, h, d), rot.cos_q, rot.sin_q).transpose(1, 2).contiguous()
-        k = _rotate(k.reshape(b, t, kvh, d), rot.cos_k, rot.sin_k).transpose(1, 2)
-        v = v.reshape(b, t, kvh, d).transpose(1, 2)
+        q = q.reshape(b, t, h, d).transpose(1, 2).contiguous()              # [b, h, t, d]
+        k = k.reshape(b, t, kvh, d)
+        v = v.reshape(b, t, kvh, d).transpose(1, 2)                           # [b, kvh, t, d]
         if kv is not None:
-            kv.keys[layer].index_copy_(3, cache_position, k.transpose(-1, -2).to(kv.keys[layer].dtype))
+            kv.keys[layer].index_copy_(3, cache_position, k.permute(0, 2, 3, 1).to(kv.keys[layer].dtype))
             kv.values[layer].index_copy_(2, cache_position, v.to(kv.values[layer].dtype))
             keys_t, v = kv.keys[layer].to(dt), kv.values[layer]                  # keys_t [b, kvh, d, L]
         else:
-            keys_t = k.transpose(-1, -2).contiguous()
+            keys_t = k.permute(0, 2, 3, 1).contiguous()
         length = keys_t.shape[-1]
         # The query heads sharing a key head are stacked as rows, so keys and
-        # values are read once per key head, never repeated.  Scores stay in
-        # the model dtype, masked in place; softmax computes a 16-bit input
-        # in fp32 and rounds its output once.
-        qg = q.reshape(b, kvh, rep * t, d)
-        scores = torch.matmul(qg, keys_t)                                     # [b, kvh, rep*t, L]
+        # values are read once per key head, never repeated.  The score scale
+        # is the product's alpha (beta 0: its input is not read).  Scores stay
+        # in the model dtype, masked in place; softmax computes a 16-bit
+        # input in fp32 and rounds its output once.
+        qg = q.view(b * kvh, rep * t, d)
+        unused = torch.empty((1, 1, 1), dtype=dt, device=q.device).expand(b * kvh, rep * t, length)
+        scores = torch.baddbmm(unused, qg, keys_t.reshape(b * kvh, d, length), beta=0.0, alpha=self.scale)
         scores.view(b, kvh, rep, t, length).masked_fill_(hide[:, :, None], float("-inf"))
         probs = torch.softmax(scores, dim=-1)
-        out = torch.matmul(probs, v.to(dt).contiguous())                      # [b, kvh, rep*t, d]
+        out = torch.bmm(probs, v.to(dt).contiguous().view(b * kvh, length, d))    # [b*kvh, rep*t, d]
         return out.view(b, h, t, d).transpose(1, 2).reshape(b, t, h * d)
 
-    def forward_mixed(self, x, pre: "Packed", dec: "Packed", layer: int):
+    def forward_mixed(self, x, rot: Rotary, pre: "Packed", dec: "Packed", layer: int):
         """Packed rows ``x [R, hidden]``: ``pre.n`` prompts of ``pre.t`` tokens,
-        then ``dec.n`` decode rows.  The projections (and their LoRA deltas)
-        run once over all rows; attention runs per part, prompts causally
-        over themselves, decode rows over their own KV caches."""
-        q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        then ``dec.n`` decode rows, with ``rot`` covering all R rows.  The
+        projections (and their LoRA deltas) and rotary run once over all
+        rows; attention runs per part, prompts causally over themselves,
+        decode rows over their own KV caches."""
+        q, k = self._rotate_qk(self.q_proj(x), self.k_proj(x), rot)
+        v = self.v_proj(x)
         outs = []
         for part in (pre, dec):
             if part.n == 0:
                 continue
             rows = slice(part.row0, part.row0 + part.n * part.t)
-            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.rot, part.hide, part.kv,
-                             layer, part.cache_position)
+            o = self._attend(q[rows], k[rows], v[rows], part.n, part.t, part.hide, part.kv, layer,
+                             part.cache_position)
             outs.append(o.reshape(part.n * part.t, -1))
         return self.o_proj(torch.cat(outs).to(x.dtype))
 
@@ -199,13 +223,19 @@ class Block(nn.Module):
         self.post_attention_layernorm = DecoderRMSNorm(c.hidden_size, c.rms_norm_eps)
         self.mlp = MLP(c)
 
-    def forward(self, x, rot: Rotary, hide, kv, layer, cache_position):
-        x = x + self.self_attn(self.input_layernorm(x), rot, hide, kv, layer, cache_position)
-        return x + self.mlp(self.post_attention_layernorm(x))
+    def forward(self, x, rot: Rotary, hide, kv, layer, cache_position, pending=None):
+        """Returns ``(x, delta)``: the residual stream after the attention half
+        and the MLP output still to be added to it.  ``pending``, the previous
+        block's such delta, is added in by this block's first RMSNorm (``x``
+        is updated in place)."""
+        h = self.input_layernorm(x) if pending is None else self.input_layernorm.add_forward(pending, x)
+        attn = self.self_attn(h, rot, hide, kv, layer, cache_position)
+        return x, self.mlp(self.post_attention_layernorm.add_forward(attn, x))
 
-    def forward_mixed(self, x, pre, dec, layer):
-        x = x + self.self_attn.forward_mixed(self.input_layernorm(x), pre, dec, layer)
-        return x + self.mlp(self.post_attention_layernorm(x))
+    def forward_mixed(self, x, rot, pre, dec, layer, pending=None):
+        h = self.input_layernorm(x) if pending is None else self.input_layernorm.add_forward(pending, x)
+        attn = self.self_attn.forward_mixed(h, rot, pre, dec, layer)
+        return x, self.mlp(self.post_attention_layernorm.add_forward(attn, x))
 
 
 @dataclass
@@ -215,7 +245,6 @@ class Packed:
     n: int
     t: int
     row0: int
-    rot: Rotary
     hide: torch.Tensor  # True: key position not attended
     kv: Optional[StaticKV]
     cache_position: Optional[torch.Tensor]
@@ -247,9 +276,10 @@ class Decoder(nn.Module):
         rot = Rotary.make(position_ids.expand(b, t), self.inv_freq, x.dtype)
         length = kv.max_len if kv is not None else t
         hide = ~self._mask(attention_mask, b, t, length, cache_position, dev)  # once for every layer
+        pending = None
         for i, layer in enumerate(self.layers):
-            x = layer(x, rot, hide, kv, i, cache_position)
-        return SimpleNamespace(logits=self.lm_head(self.norm(x)))
+            x, pending = layer(x, rot, hide, kv, i, cache_position, pending)
+        return SimpleNamespace(logits=self.lm_head(self.norm.add_forward(pending, x)))
 
     def forward_mixed(self, prompt_ids: torch.Tensor, decode_ids: torch.Tensor, decode_kv: StaticKV,
                       decode_pos: torch.Tensor):
@@ -269,14 +299,15 @@ class Decoder(nn.Module):
                        self.embed_tokens(decode_ids).reshape(d, -1)))
         pos = torch.arange(t, device=dev)
         later = (pos[None, :] > pos[:, None]).view(1, 1, t, t)
-        pre = Packed(p, t, 0, Rotary.make(pos.view(1, t), self.inv_freq, x.dtype), later, None, None)
+        pre = Packed(p, t, 0, later, None, None)
         unseen = (torch.arange(decode_kv.max_len, device=dev) > decode_pos).view(1, 1, 1, -1)
-        dec = Packed(d, 1, p * t, Rotary.make(decode_pos.view(1, 1), self.inv_freq, x.dtype), unseen, decode_kv,
-                     decode_pos)
+        dec = Packed(d, 1, p * t, unseen, decode_kv, decode_pos)
+        rot = Rotary.make(torch.cat((pos.repeat(p), decode_pos.reshape(1).expand(d))), self.inv_freq, x.dtype)
+        pending = None
         for i, layer in enumerate(self.layers):
-            x = layer.forward_mixed(x, pre, dec, i)
+            x, pending = layer.forward_mixed(x, rot, pre, dec, i, pending)
         last = torch.cat((torch.arange(t - 1, p * t, t, device=dev), torch.arange(p * t, p * t + d, device=dev)))
-        return self.lm_head(self.norm(x[last]))
+        return self.lm_head(self.norm(x[last] + pending[last]))
 
     @staticmethod
     def _mask(attention_mask, b, t, length, cache_position, dev) -> torch.Tensor:

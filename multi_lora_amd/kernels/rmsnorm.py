@@ -82,8 +82,10 @@ def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Ten
 def fuse_rmsnorm(model: torch.nn.Module) -> int:
     """Route every ``*RMSNorm`` module's forward through ``rmsnorm_fwd``; returns the count.
 
-    Only the instance's ``forward`` is rebound: parameters, the module tree
-    and ``state_dict`` are unchanged.
+    Only the instance's ``forward`` is rebound (and, for a module that has
+    one, its ``add_forward(delta, residual)`` -- residual add then norm --
+    through ``fused_add_rmsnorm``): parameters, the module tree and
+    ``state_dict`` are unchanged.
     """
     count = 0
     for module in model.modules():
@@ -94,6 +96,8 @@ def fuse_rmsnorm(model: torch.nn.Module) -> int:
         if eps is None or weight is None:
             continue
         module.forward = _bound_forward(weight, float(eps))
+        if callable(getattr(module, "add_forward", None)):
+            module.add_forward = _bound_add_forward(weight, float(eps))
         count += 1
     return count
 
@@ -103,3 +107,10 @@ def _bound_forward(weight: torch.Tensor, eps: float):
         return rmsnorm_fwd(hidden_states, weight, eps)
 
     return forward
+
+
+def _bound_add_forward(weight: torch.Tensor, eps: float):
+    def add_forward(delta: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        return fused_add_rmsnorm(delta, residual, weight, eps)
+
+    return add_forward

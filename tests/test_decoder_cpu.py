@@ -72,3 +72,33 @@ def test_mixed_step_equals_separate_prefill_and_decode():
     for layer in range(m.config.num_hidden_layers):
         torch.testing.assert_close(kv.keys[layer], kv_ref.keys[layer], atol=1e-6, rtol=1e-6)
         torch.testing.assert_close(kv.values[layer], kv_ref.values[layer], atol=1e-6, rtol=1e-6)
+
+
+@torch.inference_mode()
+def test_rotary_over_a_fused_qkv_output_equals_q_and_k_apart():
+    """When q and k are adjacent column views of one projection output (the
+    fused q|k|v group's), rotary runs once over both; the result equals
+    rotating q and k apart, and a reference rotate_half rotation."""
+    from multi_lora_amd.decoder import Rotary
+
+    m = model()
+    c = m.config
+    h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+    rows = 7
+    qkv = torch.randn(rows, (h + 2 * kvh) * d, generator=torch.Generator().manual_seed(3))
+    q, k = qkv[:, : h * d], qkv[:, h * d: (h + kvh) * d]
+    pos = torch.tensor([0, 1, 2, 5, 9, 40, 511])
+    rot = Rotary.make(pos, m.inv_freq, torch.float32)
+    attn = m.layers[0].self_attn
+    qj, kj = attn._rotate_qk(q, k, rot)
+    qa, ka = attn._rotate_qk(q.clone(), k.clone(), rot)  # separate tensors: rotated apart
+    torch.testing.assert_close(qj, qa, atol=0, rtol=0)
+    torch.testing.assert_close(kj, ka, atol=0, rtol=0)
+    ang = pos.float()[:, None] * m.inv_freq                                 # [rows, d/2]
+    cos, sin = torch.cat((ang.cos(), ang.cos()), -1)[:, None], torch.cat((ang.sin(), ang.sin()), -1)[:, None]
+
+    def rotate_half(x):
+        return torch.cat((-x[..., d // 2:], x[..., : d // 2]), -1)
+
+    qr = q.reshape(rows, h, d)
+    torch.testing.assert_close(qj, qr * cos + rotate_half(qr) * sin, atol=1e-6, rtol=1e-6)

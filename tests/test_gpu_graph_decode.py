@@ -130,3 +130,35 @@ def test_mixed_step_with_adapters_equals_separate_runs(dev):
     torch.testing.assert_close(got[:2], want_p, atol=1e-4, rtol=1e-4)
     torch.testing.assert_close(got[2:], want_d, atol=1e-4, rtol=1e-4)
     assert (want_d[0] - want_d[1]).abs().max() > 1e-3  # the adapters matter
+
+
+@pytest.mark.parametrize("dtype,atol", [(torch.float32, 1e-4), (torch.bfloat16, 6e-2)])
+def test_fused_norms_equal_the_torch_norms(dev, dtype, atol):
+    """``fuse_rmsnorm`` routes the decoder's norms, and its residual add +
+    norm (``add_forward``), through the HIP kernels; the logits of a prefill
+    and of a packed mixed step equal the model's own torch norms (the HIP
+    norm rounds once where the torch one rounds the fp32 result once too,
+    so fp32 agrees to rounding and bf16 within a few units)."""
+    from multi_lora_amd.decoder import StaticKV
+    from multi_lora_amd.kernels.rmsnorm import fuse_rmsnorm
+
+    torch.manual_seed(0)
+    cfg = DecoderConfig()
+    plain = Decoder(cfg).to("cuda", dtype).eval()
+    for mod in plain.modules():
+        if type(mod).__name__.endswith("RMSNorm"):
+            with torch.no_grad():
+                mod.weight.copy_(1.0 + 0.1 * torch.randn_like(mod.weight))
+    fused = Decoder(cfg).to("cuda", dtype).eval()
+    fused.load_state_dict(plain.state_dict())
+    assert fuse_rmsnorm(fused) == 2 * cfg.num_hidden_layers + 1
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, cfg.vocab_size, (2, 7), generator=g).to("cuda")
+    nxt = torch.randint(0, cfg.vocab_size, (3, 1), generator=g).to("cuda")
+    pos = torch.tensor([3], device="cuda")
+    with torch.inference_mode():
+        torch.testing.assert_close(fused(input_ids=ids, use_cache=False).logits.float(),
+                                   plain(input_ids=ids, use_cache=False).logits.float(), atol=atol, rtol=atol)
+        got = fused.forward_mixed(ids, nxt, StaticKV(cfg, 3, 8, "cuda", dtype), pos)
+        want = plain.forward_mixed(ids, nxt, StaticKV(cfg, 3, 8, "cuda", dtype), pos)
+    torch.testing.assert_close(got.float(), want.float(), atol=atol, rtol=atol)

@@ -232,6 +232,46 @@ def test_mixed_batch_expand_at_the_pool_size_limit(dev, n_slots):
     assert_tol_f64(got, apply_f64(x, As, Bs, meta_cpu, base, cols), f"{n_slots} slots")
 
 
+def test_interleaved_mixed_expand_in_a_replayed_graph_follows_table_rewrites(dev):
+    """A wide mixed expand (2 x 14336 columns) whose short items exceed a round
+    of workgroup slots interleaves long and short units and launches half as
+    many short units as short slots.  Captured with 10 short slots, it is
+    replayed after rewrites to 40 and back to 10, and each replay equals
+    the tiled result."""
+    g = torch.Generator().manual_seed(78)
+    lens = [512, 300] + [1] * 40
+    ranks = [16] * 64
+    slots0 = [0, 1] + [2 + (i % 10) for i in range(40)]            # 10 distinct short slots
+    slots1 = [0, 1] + [20 + i for i in range(40)]                  # 40 after the rewrite
+    x, As, Bs, base, cols, _, scal = case(dev, lens, slots0, ranks, 512, [14336, 14336], 16, torch.bfloat16, 4)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    meta = make_meta(lens, slots0, ranks, scal, dev, torch.bfloat16)
+    assert meta.table_summary(64)[2] == 10
+    out = base.to(dev).clone()
+    ws = Workspace()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)
+    for rep, slots in enumerate((slots0, slots1, slots0)):
+        meta.weight_indices.copy_(torch.tensor(slots, dtype=torch.int32))
+        meta.set_host_copies(lens, slots)
+        out.copy_(base.to(dev))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = base.to(dev).clone()
+        apply_segments(xd, Ad, Bd, make_meta(lens, slots, ranks, scal, dev, torch.bfloat16, host_copies=False), want,
+                       cols, workspace=Workspace())
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want.cpu()), f"replay {rep}"
+
+
 def test_mixed_batch_expand_in_a_replayed_graph_follows_table_rewrites(dev):
     """A captured mixed expand keeps the launch size of its capture; after an
     in-place rewrite that gives the short segments more distinct slots, the

@@ -213,7 +213,14 @@ def check(rc: int, what: str) -> None:
     raise MloraError(f"{what}: {msg} (hipError {rc})")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle (the raw
+    getter skips building a Stream object: about 0.06 vs 1.8 us a call)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

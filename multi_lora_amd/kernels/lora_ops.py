@@ -92,6 +92,10 @@ class LinkedWorkspace:
             b[4 * _ffi.WS_WAIT_TICKS:4 * _ffi.WS_WAIT_TICKS + 4].view(torch.int32).fill_(int(ticks))
 
 
+# mlora_grouped_workspace_bytes is host arithmetic of its arguments alone.
+_GROUPED_WS_BYTES: Dict[tuple, int] = {}
+
+
 def _default_workspace(device: torch.device, linked: bool = False) -> Workspace:
     key = (device.type, device.index if device.index is not None else torch.cuda.current_device(), linked)
     ws = _WORKSPACES.get(key)
@@ -286,7 +290,10 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
     lib = _ffi.lib()
     dt = _ffi.dtype_code(x.dtype)
     m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
-    need = lib.mlora_grouped_workspace_bytes(in_dim, r_max, n, x.shape[0], m.num_slots, dt, int(mode))
+    key = (in_dim, r_max, n, x.shape[0], m.num_slots, dt, int(mode))
+    need = _GROUPED_WS_BYTES.get(key)
+    if need is None:
+        need = _GROUPED_WS_BYTES[key] = lib.mlora_grouped_workspace_bytes(*key)
     if need == 0:
         return False
     stream = _ffi.stream_ptr(dev)

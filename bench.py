@@ -968,7 +968,7 @@ def main() -> int:
         step(i)
     torch.cuda.synchronize()
 
-    # The host enqueues a call in ~10-20 us, slower than the kernels run, so
+    # The host enqueues a call in ~12 us, slower than the kernels run, so
     # steps are timed as HIP graph replays: a graph of one pass over the
     # replicas, and one of the remaining steps, make up exactly `steps` steps.
     def capture(n, phases=3, mode=None):

@@ -451,12 +451,14 @@ def test_streamed_expand_long_segments(dev, dtype):
         st += n
 
 
-@pytest.mark.parametrize("part", ["qkv", "down"])
+@pytest.mark.parametrize("part", ["qkv", "gate_up", "down"])
 def test_c5_mixed_batch_full_shape(dev, part):
     """The 32-layer step's batch at its real shape: 2 x 512 prefill rows and
     64 one-row decode segments (1088 rows, 66 segments) through the fused
-    q|k|v (4096 -> 4096/1024/1024) or the down projection (14336 -> 4096),
-    rank 16 in a 128-slot pool with adapters drawn Zipf(1.1) over 512."""
+    q|k|v (4096 -> 4096/1024/1024), the fused gate|up (4096 -> 2 x 14336:
+    streamed long tiles interleaved with the short items) or the down
+    projection (14336 -> 4096), rank 16 in a 128-slot pool with adapters
+    drawn Zipf(1.1) over 512."""
     g = torch.Generator().manual_seed(4)
     lens = [512, 512] + [1] * 64
     zipf = torch.tensor([(i + 1) ** -1.1 for i in range(512)])
@@ -465,7 +467,8 @@ def test_c5_mixed_batch_full_shape(dev, part):
     slots = [first.setdefault(p, len(first)) for p in picks]
     n_slots, r = 128, 16
     ranks = [r] * len(first) + [0] * (n_slots - len(first))
-    in_dim, outs = (4096, [4096, 1024, 1024]) if part == "qkv" else (14336, [4096])
+    in_dim, outs = {"qkv": (4096, [4096, 1024, 1024]), "gate_up": (4096, [14336, 14336]),
+                    "down": (14336, [4096])}[part]
     used = sorted(set(slots))
     x = torch.randn(sum(lens), in_dim, generator=g).bfloat16()
     As, Bs = [], []

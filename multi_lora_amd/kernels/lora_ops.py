@@ -293,6 +293,8 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
     key = (in_dim, r_max, n, x.shape[0], m.num_slots, dt, int(mode))
     need = _GROUPED_WS_BYTES.get(key)
     if need is None:
+        if len(_GROUPED_WS_BYTES) >= 4096:  # row counts vary per step: keep the cache bounded
+            _GROUPED_WS_BYTES.clear()
         need = _GROUPED_WS_BYTES[key] = lib.mlora_grouped_workspace_bytes(*key)
     if need == 0:
         return False

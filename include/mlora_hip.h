@@ -10,7 +10,11 @@
  *   - Every call is launch-only on `stream` (a hipStream_t passed as void*):
  *     no host synchronisation, no allocation, so it can be captured into a
  *     HIP graph.  Per-step values (segment bounds, slots, ranks, scalings) are
- *     read from device memory; only `bs` and `max_len` size the grid.
+ *     read from device memory; only `bs` and `max_len` size the grid.  A
+ *     replayed call keeps the host values it was captured with, so a table
+ *     rewritten in place between replays must have at most `bs` segments of
+ *     at most `max_len` rows (the table summary and plan counts only size
+ *     grids whose kernels recount from the device and loop).
  *   - Return value: 0 = ok, < 0 = invalid argument (nothing launched),
  *     > 0 = a hipError_t from the launch.  mlora_last_error() returns a
  *     thread-local message for the last non-zero return on this thread.

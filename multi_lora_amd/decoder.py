@@ -145,6 +145,7 @@ class Attention(nn.Module):
         h, kvh, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         rows = q.shape[0]
         if (q.stride(-1) == 1 and k.stride(-1) == 1 and q.stride(0) == k.stride(0) and q.dtype == k.dtype
+                and q.untyped_storage().data_ptr() == k.untyped_storage().data_ptr()
                 and k.data_ptr() == q.data_ptr() + h * d * q.element_size()):
             qk = torch.as_strided(q, (rows, h + kvh, d), (q.stride(0), d, 1))
             r = _rotate(qk, rot.cos, rot.sin)

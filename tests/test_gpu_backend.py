@@ -171,3 +171,26 @@ def test_fused_groups_on_every_shape_equal_separate_layers(dev, leaves, lens):
     assert grp._delta_done and grp._cached_x is x
     for g_, r_ in zip(got, ref):
         torch.testing.assert_close(g_, r_, atol=2e-2, rtol=1e-2)
+
+
+def test_launches_follow_the_current_stream(dev):
+    """The stream handle the library is given is torch's current stream (the
+    default one, and a side stream inside ``torch.cuda.stream``), and a call
+    made on a side stream equals the same call on the default stream."""
+    from multi_lora_amd import _ffi
+
+    assert _ffi.stream_ptr(dev) == torch.cuda.current_stream(dev).cuda_stream
+    assert _ffi.stream_ptr(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
+    wl = synthetic.decode_q(device=dev, tokens=48, in_dim=1024, out=1536, n_slots=12, n_adapters=7, rank=16, seed=21)
+    hip = HipLoRABackend()
+    hip.set_kernel_input_metadata(wl.meta)
+    want = hip.apply_lora(wl.x, wl.a_stacks[0], wl.b_stacks[0], wl.clone_base())
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        assert _ffi.stream_ptr(dev) == side.cuda_stream
+        base = wl.clone_base()
+        got = hip.apply_lora(wl.x, wl.a_stacks[0], wl.b_stacks[0], base)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

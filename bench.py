@@ -72,6 +72,10 @@ OTHER_WORKLOADS = {
                   "rows (66 segments), 128-slot pool holding 35 rank-16 adapters",
     "c5_qkv": "the 32-layer step's q|k|v LoRA call: 4096->[4096,1024,1024], mixed batch of 2 x 512 prefill + 64 "
               "decode rows (66 segments), 128-slot pool holding 35 rank-16 adapters",
+    "c5_o": "the 32-layer step's o LoRA call: 4096->4096, mixed batch of 2 x 512 prefill + 64 decode rows "
+            "(66 segments), 128-slot pool holding 35 rank-16 adapters",
+    "c5_down": "the 32-layer step's down LoRA call: 14336->4096, mixed batch of 2 x 512 prefill + 64 decode rows "
+               "(66 segments), 128-slot pool holding 35 rank-16 adapters",
     "pool_upload": "pool upload scatter, Llama-3-8B 32 layers x 7 projections (224 keys), rank 16, "
                    "4 staged adapters (84 MB each) into an 8-slot pool",
     "c5_step": "Llama-3-8B-shaped 32-layer model step (random init): 7 projections per layer LoRA-ed at rank 16, "
@@ -706,7 +710,7 @@ def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> di
 COPY_ELEMS = 32 << 20
 PROFILE_CALLS = 64
 GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_qkv")
-PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down", "c5_gate_up", "c5_qkv")
+PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down", "c5_gate_up", "c5_qkv", "c5_o", "c5_down")
 MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
 

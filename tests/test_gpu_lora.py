@@ -17,7 +17,7 @@ from multi_lora_amd.kernels import (
     sgemm_lora_b_fwd,
     sgemm_lora_b_multi_fwd,
 )
-from multi_lora_amd.kernels.lora_ops import apply_segments, shrink
+from multi_lora_amd.kernels.lora_ops import Workspace, apply_segments, shrink
 from multi_lora_amd.synthetic import make_meta
 from oracle.lora_ref import TorchLoRABackend, apply_f64, apply_kernel_numerics
 from tests.gpu_helpers import assert_tol_f64, assert_ulp_close
@@ -451,13 +451,14 @@ def test_streamed_expand_long_segments(dev, dtype):
         st += n
 
 
-@pytest.mark.parametrize("part", ["qkv", "gate_up", "down"])
+@pytest.mark.parametrize("part", ["qkv", "gate_up", "o", "down"])
 def test_c5_mixed_batch_full_shape(dev, part):
     """The 32-layer step's batch at its real shape: 2 x 512 prefill rows and
     64 one-row decode segments (1088 rows, 66 segments) through the fused
     q|k|v (4096 -> 4096/1024/1024), the fused gate|up (4096 -> 2 x 14336:
-    streamed long tiles interleaved with the short items) or the down
-    projection (14336 -> 4096), rank 16 in a 128-slot pool with adapters
+    streamed long tiles interleaved with the short items), the o projection
+    (4096 -> 4096) or the down projection (14336 -> 4096; o and down add the
+    split sums in the expand), rank 16 in a 128-slot pool with adapters
     drawn Zipf(1.1) over 512."""
     g = torch.Generator().manual_seed(4)
     lens = [512, 512] + [1] * 64
@@ -467,7 +468,7 @@ def test_c5_mixed_batch_full_shape(dev, part):
     slots = [first.setdefault(p, len(first)) for p in picks]
     n_slots, r = 128, 16
     ranks = [r] * len(first) + [0] * (n_slots - len(first))
-    in_dim, outs = {"qkv": (4096, [4096, 1024, 1024]), "gate_up": (4096, [14336, 14336]),
+    in_dim, outs = {"qkv": (4096, [4096, 1024, 1024]), "gate_up": (4096, [14336, 14336]), "o": (4096, [4096]),
                     "down": (14336, [4096])}[part]
     used = sorted(set(slots))
     x = torch.randn(sum(lens), in_dim, generator=g).bfloat16()
@@ -483,6 +484,13 @@ def test_c5_mixed_batch_full_shape(dev, part):
     cols = [sum(outs[:i]) for i in range(len(outs))]
     meta_cpu = make_meta(lens, slots, ranks, [2.0] * n_slots, "cpu", torch.bfloat16)
     want = apply_f64(x, As, Bs, meta_cpu, base, cols)
-    mid, out = run_hip(x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs],
-                       make_meta(lens, slots, ranks, [2.0] * n_slots, dev, torch.bfloat16), base.to(dev), cols)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    meta = make_meta(lens, slots, ranks, [2.0] * n_slots, dev, torch.bfloat16)
+    mid, out = run_hip(xd, Ad, Bd, meta, base.to(dev), cols)
     assert_tol_f64(out, want, f"c5 {part}")
+    # The backend's one-call path (the expand adds the split sums itself for
+    # o and down) equals the two-call path element for element.
+    one = base.to(dev)
+    apply_segments(xd, Ad, Bd, meta, one, cols, workspace=Workspace())
+    torch.cuda.synchronize()
+    assert torch.equal(one.cpu(), out), f"c5 {part}: one call differs from shrink then expand"

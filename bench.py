@@ -8,8 +8,12 @@ scaling 2.0, seed 1.  One step = one shrink+expand pass
 (``HipLoRABackend.apply_lora``) over the 128 tokens, inputs resident in HBM.
 
 Cold-cache protocol: the step rotates through ``--replicas`` independent
-copies of x / A pool / B pool / output (default 32 x ~18 MiB = 576 MiB, over
-twice the 256 MiB MALL), so weights come from HBM rather than the caches.
+copies of x / A pool / B pool / output.  A step touches 10.5 MiB of them
+(x 1 MiB, the 32 used adapters' A and B rows 4 MiB each, the output 1 MiB
+read and written), so the default 64 replicas touch 672 MiB a rotation,
+over twice the 256 MiB MALL.  Every timed region of exactly ``--steps``
+steps starts at the replica after the previous region's last (one captured
+graph per start offset), so no region finds its replicas in the caches.
 
 Output: one JSON line.  ``value`` is the step's algorithmic HBM bytes divided
 by its time (GB/s); ``ms_per_step`` gives the latency.  ``roofline`` covers
@@ -38,11 +42,14 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--replicas", type=int, default=32)
+    ap.add_argument("--replicas", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="headline only: skip the prefill (c3), RMSNorm + q|k|v (c4) and mixed-batch (c5) calls "
+                         "that the default line carries under other_configs")
     ap.add_argument("--kernel-steps", type=int, default=2000, help="launches in each per-kernel timing")
     ap.add_argument("--workload", choices=("decode_q",) + tuple(OTHER_WORKLOADS), default="decode_q",
                     help="decode_q is the headline; the others print a line of the same form for their shape")
@@ -55,6 +62,9 @@ def parse():
     ap.add_argument("--sweep", choices=("decode",),
                     help="decode: one JSON line per decode shape (tokens, adapters, rank, slices), graph-timed "
                          "over cold replicas, with the schedule the library picks")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="launch floors (empty kernel, one-launch cold stream of the headline's bytes) and the "
+                         "planned decode kernel's per-phase timeline, from the measurement library")
     ap.add_argument("--regions", type=int, default=0,
                     help="timed regions of exactly --steps steps each (default: enough for ~2000 steps, 5..101); "
                          "the step time is their median")
@@ -371,25 +381,69 @@ def bench_pool_upload(args) -> int:
     return 0
 
 
-def time_calls(torch, fn, k: int, per_graph: int, stream) -> float:
-    """Milliseconds per call over exactly ``k`` calls of ``fn``: graphs of
-    ``per_graph`` calls replayed back to back, then one graph of the rest."""
-    full, rem = divmod(k, per_graph)
-    g_full = capture(torch, fn, per_graph) if full else None
-    g_rem = capture(torch, fn, rem) if rem else None
-    for g in (g_full, g_rem):
-        if g is not None:
+class RotatingTimer:
+    """Regions of exactly ``k`` calls of ``fn`` over ``n_rep`` rotating replicas.
+
+    Call ``i`` of the sequence uses replica ``i % n_rep`` (``fn(i)`` picks it),
+    and every region starts at the call after the previous region's last, so a
+    replica comes back only after the ``n_rep - 1`` others, however ``k`` and
+    ``n_rep`` relate.  One HIP graph is captured per start offset the rotation
+    reaches (``n_rep / gcd(k, n_rep)`` of them); constructing the timer replays
+    each once, in rotation order, untimed.  ``run(regions)`` returns the
+    milliseconds per call of each region, each timed with HIP events on
+    ``stream`` between synchronisations.
+    """
+
+    MAX_CAPTURED_CALLS = 40000
+
+    def __init__(self, torch, fn, n_rep: int, k: int, stream):
+        import math
+
+        n_off = n_rep // math.gcd(k, n_rep)
+        if n_off * k > self.MAX_CAPTURED_CALLS:
+            raise SystemExit(f"{k} steps over {n_rep} replicas need {n_off} graphs of {k} calls; "
+                             f"pick a step count with a larger common divisor with {n_rep}")
+        self.torch, self.k, self.stream = torch, k, stream
+        self.graphs = [capture(torch, lambda i, o=(j * k) % n_rep: fn(o + i), k) for j in range(n_off)]
+        self.next = 0
+        self.run(n_off)
+
+    def run(self, regions: int) -> list:
+        torch = self.torch
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        out = []
+        for _ in range(regions):
+            g = self.graphs[self.next % len(self.graphs)]
+            self.next += 1
+            torch.cuda.synchronize()
+            t0.record(self.stream)
             g.replay()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(full):
-        g_full.replay()
-    if g_rem is not None:
-        g_rem.replay()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / k
+            t1.record(self.stream)
+            torch.cuda.synchronize()
+            out.append(t0.elapsed_time(t1) / self.k)
+        return out
+
+    def median(self, regions: int) -> float:
+        t = sorted(self.run(regions))
+        return t[len(t) // 2]
+
+
+def touched_bytes(host) -> int:
+    """Distinct bytes one call touches: the algorithmic bytes with the output counted once."""
+    from multi_lora_amd import synthetic
+
+    return synthetic.algorithmic_bytes(host) - host.base.numel() * host.base.element_size()
+
+
+def replicas_for(touched_bytes: int, floor: int = 2) -> int:
+    """Replicas whose touched bytes add up to at least 600 MB, over twice the
+    256 MiB MALL, so a replica's lines are gone from it when it comes back."""
+    return max(floor, -(-600_000_000 // max(1, touched_bytes)))
+
+
+def rotation_calls(n_rep: int, at_least: int = 32) -> int:
+    """A region length that is a whole number of rotations (one graph) and at least ``at_least`` calls."""
+    return n_rep * max(1, -(-at_least // n_rep))
 
 
 def time_graph(torch, g, calls: int, per_graph: int, stream) -> float:
@@ -448,8 +502,7 @@ def bench_other(args) -> int:
     host = workload_host(name)
     meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
     e = host.x.element_size()
-    rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + 2 * host.base.numel()) * e
-    n_rep = max(2, -(-600_000_000 // rep_bytes))
+    n_rep = replicas_for(touched_bytes(host))
     reps = []
     for _ in range(n_rep):
         reps.append((host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
@@ -566,12 +619,12 @@ def bench_other(args) -> int:
     for i in range(max(args.warmup // 10, 2 * n_rep)):
         step(i)
     torch.cuda.synchronize()
-    # Each graph rotates through the replicas for at least 32 calls, so that a
-    # replay's own launch cost is spread over many kernels.
-    per_graph = max(32, n_rep)
-    step_ms = time_calls(torch, step, args.steps, per_graph, stream)
+    regions = args.regions or min(101, max(5, -(-2000 // args.steps)))
+    step_ms = RotatingTimer(torch, step, n_rep, args.steps, stream).median(regions)
+    # Parts: regions of whole rotations (one graph of at least 32 calls).
+    per_graph = rotation_calls(n_rep)
     for k, (fn, nbytes) in parts.items():
-        ms = time_graph(torch, capture(torch, fn, per_graph), calls, per_graph, stream)
+        ms = RotatingTimer(torch, fn, n_rep, per_graph, stream).median(max(3, calls // per_graph))
         kernels[k] = {"us": ms * 1e3, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9}
     fb, pe = be.linked_workspace.counters()
     if pe:
@@ -635,9 +688,7 @@ def sweep_decode(args) -> int:
         else:
             host = synthetic.decode_q(device="cpu", n_slots=n_slots, seed=5, **sh)
         meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
-        e = host.x.element_size()
-        rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + host.base.numel()) * e
-        n_rep = max(2, -(-600_000_000 // rep_bytes))
+        n_rep = replicas_for(touched_bytes(host))
         reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
                  host.base.to(dev)) for _ in range(n_rep)]
         lws = LinkedWorkspace()
@@ -647,8 +698,9 @@ def sweep_decode(args) -> int:
             def call(i, mode=mode):
                 x, a, b, out = reps[i % n_rep]
                 assert apply_grouped(x, a, b, meta, out, host.col_offsets, lws, mode=mode)
-            per_graph = max(32, n_rep)
-            res[mode] = time_calls(torch, call, max(args.kernel_steps, 2 * per_graph), per_graph, stream) * 1e3
+            per_graph = rotation_calls(n_rep)
+            timer = RotatingTimer(torch, call, n_rep, per_graph, stream)
+            res[mode] = timer.median(max(5, args.kernel_steps // per_graph)) * 1e3
         fb, pe = lws.counters()
         if pe:
             raise RuntimeError(f"{pe} plan errors; timings are void")
@@ -766,9 +818,7 @@ def profile_traffic(name: str) -> int:
     torch.cuda.set_device(dev)
     host = workload_host(name)
     meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
-    e = host.x.element_size()
-    rep_bytes = (host.x.numel() + sum(t.numel() for t in host.a_stacks + host.b_stacks) + host.base.numel()) * e
-    n_rep = max(2, -(-600_000_000 // rep_bytes))
+    n_rep = replicas_for(touched_bytes(host))
     reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
              host.base.to(dev)) for _ in range(n_rep)]
     if "norm_weight" in host.extra:
@@ -932,6 +982,8 @@ def main() -> int:
 
     if args.profile_traffic:
         return profile_traffic(args.workload)
+    if args.calibrate:
+        return calibrate(args)
     if args.sweep == "decode":
         return sweep_decode(args)
     if args.workload == "pool_upload":
@@ -973,55 +1025,19 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # The host enqueues a call in ~12 us, slower than the kernels run, so
-    # steps are timed as HIP graph replays: a graph of one pass over the
-    # replicas, and one of the remaining steps, make up exactly `steps` steps.
-    def capture(n, phases=3, mode=None):
-        s = capture_stream(torch)
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):  # the capture stream's workspace exists before capture
-            for i in range(n):
-                step(i, phases, mode)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            for i in range(n):
-                step(i, phases, mode)
-        torch.cuda.synchronize()
-        return g
-
-    def region_timer(k, phases=3, mode=None):
-        """Times regions of exactly k steps (ms per step of each region)."""
-        full, rem = divmod(k, len(reps))
-        g_full = capture(len(reps), phases, mode) if full else None
-        g_rem = capture(rem, phases, mode) if rem else None
-
-        def run():
-            torch.cuda.synchronize()
-            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            t0.record(stream)
-            for _ in range(full):
-                g_full.replay()
-            if g_rem is not None:
-                g_rem.replay()
-            t1.record(stream)
-            torch.cuda.synchronize()
-            return t0.elapsed_time(t1) / k
-
-        run()  # first replay of fresh graphs, untimed
-        return run
-
-    def median_ms(k, regions, phases=3, mode=None):
-        run = region_timer(k, phases, mode)
-        times = sorted(run() for _ in range(regions))
-        return times[len(times) // 2]
-
+    # steps are timed as HIP graph replays.  Each region is exactly `steps`
+    # steps and starts at the replica after the previous region's last, so a
+    # replica's lines have left the MALL when it comes back.
     regions = args.regions or min(101, max(5, -(-2000 // args.steps)))
-    ms_per_step = median_ms(args.steps, regions)
+    ms_per_step = RotatingTimer(torch, step, args.replicas, args.steps, stream).median(regions)
     timed_steps = args.steps
     # The backend's step is one launch of the planned kernel; the two-launch
-    # schedule of the same work items is timed for comparison.
-    kreg = max(1, -(-args.kernel_steps // len(reps)))
-    shrink_ms = median_ms(len(reps), kreg, 1, mode=2)
-    expand_ms = median_ms(len(reps), kreg, 2, mode=2)
+    # schedule of the same work items is timed for comparison (regions of
+    # whole rotations).
+    per_rot = rotation_calls(args.replicas)
+    kreg = max(3, -(-args.kernel_steps // per_rot))
+    shrink_ms = RotatingTimer(torch, lambda i: step(i, 1, 2), args.replicas, per_rot, stream).median(kreg)
+    expand_ms = RotatingTimer(torch, lambda i: step(i, 2, 2), args.replicas, per_rot, stream).median(kreg)
     fb, pe = be.linked_workspace.counters()
     if pe:
         raise RuntimeError(f"{pe} plan errors; timings are void")
@@ -1033,6 +1049,7 @@ def main() -> int:
     expand_bytes = len(used) * out_dim * r * e + 2 * host.tokens * out_dim * e
     total_bytes = synthetic.algorithmic_bytes(host)
     assert total_bytes == shrink_bytes + expand_bytes
+    touched = total_bytes - host.base.numel() * e  # the output's lines are read and written once each
     step_gbs = total_bytes / (ms_per_step * 1e-3) / 1e9
 
     def entry(ms, nbytes):
@@ -1069,8 +1086,10 @@ def main() -> int:
             "distinct_slots": len(used),
             "algorithmic_bytes_per_step": total_bytes,
             "replicas": args.replicas,
+            "touched_bytes_per_rotation": args.replicas * touched,
             "timing": (f"median over {regions} regions of exactly {args.steps} steps, each a HIP graph replay "
-                       f"timed with HIP events on the launch stream"),
+                       f"timed with HIP events on the launch stream; each region starts at the replica after "
+                       f"the previous region's last"),
             "path": "slot-planned shrink + expand, one launch (HipLoRABackend.apply_lora)",
             "handoff_fallback_chunks": fb,
         },
@@ -1086,11 +1105,249 @@ def main() -> int:
         },
     }
 
+    if not args.no_other_configs:
+        result["other_configs"] = other_configs()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(host, total_bytes, args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+def calibrate(args) -> int:
+    """Floors of one launch at the headline size, and where the headline kernel's time goes.
+
+    Loads the measurement library (``libmlora_calib.so``: the product's
+    sources built with per-phase timestamps in the planned decode kernel,
+    plus an empty and a streaming kernel) and prints one JSON line:
+
+    * ``empty_kernel_us``: an empty kernel (1 and 1024 workgroups) per launch
+      under HIP graph replay, 64 launches a graph;
+    * ``stream_us``: one launch of 1024 workgroups reading the headline's
+      11,534,336 algorithmic bytes, over rotating replicas (cold, at least
+      600 MB a rotation) and from one buffer (hot, MALL-resident);
+    * ``planned_decode_us``: the headline call (planned kernel, one launch)
+      through the same library, graph-timed as the headline;
+    * ``timeline``: per-phase quantiles (ns after the first workgroup
+      starts) of the last call of 32 graph replays of 8 calls, cold
+      replicas rotating as in the headline.
+    """
+    import ctypes
+    import statistics
+
+    import torch
+
+    from multi_lora_amd import _ffi, synthetic
+    from multi_lora_amd.build import CALIB_LIB
+    from multi_lora_amd.kernels.lora_ops import _slices, seg_meta
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    if not CALIB_LIB.exists():
+        raise SystemExit(f"{CALIB_LIB} is not built (python -m multi_lora_amd.build)")
+    lib = ctypes.CDLL(str(CALIB_LIB))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.mlora_calib_empty.argtypes = [ctypes.c_int, vp, vp]
+    lib.mlora_calib_stream.argtypes = [vp, i64, vp, ctypes.c_int, vp]
+    lib.mlora_tl_clear.argtypes = [ctypes.c_int, vp]
+    lib.mlora_tl_read.argtypes = [vp, ctypes.c_int]
+    lib.mlora_last_error.restype = ctypes.c_char_p
+    for name in ("mlora_apply_grouped", "mlora_grouped_workspace_bytes"):
+        res, argt = _ffi._SIGNATURES[name]
+        getattr(lib, name).restype = res
+        getattr(lib, name).argtypes = argt
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: rc {rc} {lib.mlora_last_error().decode(errors='replace')}")
+
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    result = {"metric": "launch floors and the planned decode kernel's timeline at the headline size",
+              "workload": HEADLINE_WORKLOAD, "n_gpus": 1}
+
+    # 1. The launch itself.
+    empty = {}
+    for blocks in (1, 1024):
+        g = capture(torch, lambda i, b=blocks: ok(lib.mlora_calib_empty(b, sink.data_ptr(), _ffi.stream_ptr(dev)),
+                                                  "empty"), 64)
+        empty[f"{blocks}_workgroups"] = round(time_graph(torch, g, 64 * 50, 64, stream) * 1e3, 3)
+    result["empty_kernel_us"] = empty
+
+    # 2. One launch streaming the headline's bytes.
+    host = synthetic.decode_q(device="cpu")
+    nbytes = synthetic.algorithmic_bytes(host)
+    n_rep = max(args.replicas, replicas_for(nbytes))
+    bufs = [torch.full((nbytes,), i & 0x7F, dtype=torch.uint8, device=dev) for i in range(n_rep)]
+
+    def stream_call(i):
+        ok(lib.mlora_calib_stream(bufs[i % n_rep].data_ptr(), nbytes, sink.data_ptr(), 1024, _ffi.stream_ptr(dev)),
+           "stream")
+
+    per_rot = rotation_calls(n_rep)
+    cold = RotatingTimer(torch, stream_call, n_rep, per_rot, stream).median(9)
+    hot = time_graph(torch, capture(torch, lambda i: stream_call(0), 64), 64 * 20, 64, stream)
+    result["stream_us"] = {"bytes": nbytes, "cold": round(cold * 1e3, 3), "hot": round(hot * 1e3, 3),
+                           "cold_GB/s": round(nbytes / (cold * 1e-3) / 1e9, 1), "replicas": n_rep}
+    del bufs
+
+    # 3. The headline call through the same library.
+    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+    reps = [(host.x.to(dev), host.a_stacks[0].to(dev), host.b_stacks[0].to(dev), host.base.to(dev))
+            for _ in range(args.replicas)]
+    n_slots, r_max = host.a_stacks[0].shape[0], host.a_stacks[0].shape[1]
+    in_dim, S = host.x.shape[1], host.tokens
+    cmeta, keep = seg_meta(meta, dev, n_slots)
+    slices = [_slices([a], [b], [0]) for _, a, b, _ in reps]
+    ws_bytes = lib.mlora_grouped_workspace_bytes(in_dim, r_max, 1, S, n_slots, _ffi.MLORA_BF16, 1)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def decode_call(i):
+        x, _, _, out = reps[i % len(reps)]
+        ok(lib.mlora_apply_grouped(x.data_ptr(), x.stride(0), S, in_dim, slices[i % len(reps)], 1, r_max,
+                                   out.data_ptr(), out.stride(0), ctypes.byref(cmeta), _ffi.MLORA_BF16,
+                                   ws.data_ptr(), ws_bytes, 1, 3, _ffi.stream_ptr(dev)), "apply_grouped")
+
+    timer = RotatingTimer(torch, decode_call, len(reps), args.steps, stream)
+    result["planned_decode_us"] = round(timer.median(args.regions or 41) * 1e3, 3)
+
+    # 4. Timeline: every workgroup writes its whole stamp record at its end,
+    # so after a graph replay of 8 calls back to back the records are the
+    # last call's, made in the timed protocol's conditions.
+    e_grid = (int(meta.plan_entries) + 7) // 8 * 8
+    kc, n_tiles = in_dim // 256, host.b_stacks[0].shape[1] // 256
+    n_blk = (kc + n_tiles) * e_grid
+    words = n_blk * 4 * 8
+    buf = (ctypes.c_uint32 * words)()
+    ph = {k: [] for k in ("s_start", "e_start", "s_entry", "s_data_wave", "s_reduced", "s_flag", "s_end", "e_entry", "e_requested",
+                          "e_flags_seen", "e_sums", "e_y", "e_stored", "kernel_end")}
+    crit = []
+    tl_timer = RotatingTimer(torch, decode_call, len(reps), 8, stream)
+    for it in range(32):
+        ok(lib.mlora_tl_clear(words, _ffi.stream_ptr(dev)), "tl_clear")
+        tl_timer.run(1)
+        ok(lib.mlora_tl_read(ctypes.cast(buf, vp), words), "tl_read")
+        t = torch.tensor(list(buf), dtype=torch.int64).view(n_blk, 4, 8)
+        starts = t[:, :, 0][t[:, :, 0] > 0]
+        # Low words of a 100 MHz counter: order them relative to one start,
+        # modulo 2^32, then take the earliest start as time 0.
+        ref0 = int(starts[0])
+        wrap = lambda v: ((int(v) - ref0 + (1 << 31)) % (1 << 32)) - (1 << 31)  # noqa: E731
+        t0 = min(wrap(v) for v in starts.tolist())
+        rel = lambda v: (wrap(v) - t0) * 10  # noqa: E731  (10 ns ticks)
+        flag_by_entry, seen_by_entry = {}, {}
+        end = 0
+        for b in range(n_blk):
+            item, j = divmod(b, e_grid)
+            w = t[b]
+            if int(w[0, 1]) == 0:
+                continue
+            if item < kc:
+                ph["s_start"].append(rel(w[0, 0]))
+                ph["s_entry"].append(rel(w[0, 1]))
+                ph["s_data_wave"] += [rel(w[q, 2]) for q in range(4) if int(w[q, 2]) > 0]
+                ph["s_reduced"].append(rel(w[0, 3]))
+                ph["s_flag"].append(rel(w[0, 4]))
+                ph["s_end"].append(rel(w[0, 5]))
+                flag_by_entry[j] = max(flag_by_entry.get(j, 0), rel(w[0, 4]))
+                end = max(end, rel(w[0, 5]))
+            else:
+                ph["e_start"].append(rel(w[0, 0]))
+                ph["e_entry"].append(rel(w[0, 1]))
+                ph["e_requested"].append(rel(w[0, 2]))
+                ph["e_flags_seen"].append(rel(w[0, 3]))
+                ph["e_sums"].append(rel(w[0, 4]))
+                ph["e_y"].append(rel(w[0, 5]))
+                st = max(rel(w[q, 6]) for q in range(4))
+                ph["e_stored"].append(st)
+                seen_by_entry.setdefault(j, []).append(rel(w[0, 3]))
+                end = max(end, st)
+        ph["kernel_end"].append(end)
+        crit += [statistics.median(v) - flag_by_entry[j] for j, v in seen_by_entry.items() if j in flag_by_entry]
+    fb = int(ws[:4].view(torch.int32)[_ffi.WS_FALLBACKS].item())
+
+    def q(v, f):
+        v = sorted(v)
+        return round(v[min(len(v) - 1, int(f * (len(v) - 1)))]) if v else None
+
+    result["timeline_ns"] = {k: {"p10": q(v, 0.1), "p50": q(v, 0.5), "p90": q(v, 0.9), "max": q(v, 1.0)}
+                             for k, v in ph.items()}
+    result["timeline_ns"]["entry_last_flag_to_flags_seen"] = {"p50": q(crit, 0.5), "p90": q(crit, 0.9)}
+    result["timeline_launches"] = 32
+    result["handoff_fallback_chunks"] = fb
+    result["phases"] = {
+        "s_*": "shrink items: entry in, A and x in (each wave), four waves' sums in LDS, flag stored after the sums' "
+               "acknowledgement, item done",
+        "e_*": "expand items: entry in, B and output requested, every chunk flag seen, sums gathered, y in LDS, "
+               "output stored and acknowledged (last wave)",
+        "kernel_end": "last workgroup's end, ns after the first workgroup's start",
+        "entry_last_flag_to_flags_seen": "per entry: median expand item's flags-seen minus the entry's last flag store",
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+# The other configurations' calls, timed into the headline line (key
+# "other_configs"): name -> (workload, what one step is).
+OTHER_CONFIGS = {
+    "c3_prefill_gate_up": ("prefill_gate_up", "HipLoRABackend.apply_lora_multi, gate|up (two slices)"),
+    "c3_prefill_down": ("prefill_down", "HipLoRABackend.apply_lora_multi"),
+    "c4_rmsnorm_qkv": ("decode_qkv", "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi over q|k|v"),
+    "c5_qkv": ("c5_qkv", "HipLoRABackend.apply_lora_multi over q|k|v, one layer's call"),
+    "c5_o": ("c5_o", "HipLoRABackend.apply_lora_multi, one layer's call"),
+    "c5_gate_up": ("c5_gate_up", "HipLoRABackend.apply_lora_multi over gate|up, one layer's call"),
+    "c5_down": ("c5_down", "HipLoRABackend.apply_lora_multi, one layer's call"),
+}
+
+
+def other_configs(regions: int = 7) -> dict:
+    """Each other configuration's call as the backend makes it, under the
+    headline's cold-replica protocol: replicas touching at least 600 MB in
+    all, regions of whole rotations, median region."""
+    import torch
+
+    from multi_lora_amd import HipLoRABackend, synthetic
+    from multi_lora_amd.kernels.rmsnorm import rmsnorm_fwd
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for key, (name, what) in OTHER_CONFIGS.items():
+        host = workload_host(name)
+        meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev,
+                                   torch.bfloat16)
+        n_rep = replicas_for(touched_bytes(host))
+        reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
+                 host.base.to(dev)) for _ in range(n_rep)]
+        be = HipLoRABackend()
+        be.set_kernel_input_metadata(meta)
+        cols = host.col_offsets
+        nbytes = synthetic.algorithmic_bytes(host)
+        w = host.extra.get("norm_weight")
+        if w is not None:
+            w = w.to(dev)
+            eps = host.extra["eps"]
+            nbytes += 2 * host.x.numel() * host.x.element_size() + w.numel() * w.element_size()
+
+        def step(i, reps=reps, be=be, cols=cols, w=w):
+            x, a, b, out = reps[i % len(reps)]
+            if w is not None:
+                x = rmsnorm_fwd(x, w, eps)
+            be.apply_lora_multi(x, a, b, out, cols)
+
+        k = rotation_calls(n_rep)
+        ms = RotatingTimer(torch, step, n_rep, k, stream).median(regions)
+        fb, pe = be.linked_workspace.counters()
+        if pe:
+            raise RuntimeError(f"{key}: {pe} plan errors; timings are void")
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[key] = {"us": round(ms * 1e3, 3), "algorithmic_bytes": nbytes, "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens": host.tokens, "replicas": n_rep,
+                    "calls_per_region": k, "step": what, "workload": OTHER_WORKLOADS[name]}
+        del reps, be, meta, host
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(host, total_bytes: int, budget_s: float) -> dict:

@@ -3,6 +3,12 @@
 Usage: ``python -m multi_lora_amd.build`` (or ``__graft_entry__.build()``).
 Each source is compiled to an object under ``multi_lora_amd/_build/`` in
 parallel, then linked into ``multi_lora_amd/libmlora_hip.so``.
+
+The same sources, compiled again with ``MLORA_TIMELINE`` (per-phase
+timestamps in the planned decode kernel) and linked with
+``csrc/calib/*.hip`` (an empty kernel and a streaming kernel), make
+``multi_lora_amd/libmlora_calib.so``: the measurement library that
+``bench.py --calibrate`` loads.  The product path never loads it.
 """
 
 from __future__ import annotations
@@ -18,6 +24,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libmlora_hip.so"
+CALIB_LIB = PKG / "libmlora_calib.so"
 ARCH = os.environ.get("MLORA_OFFLOAD_ARCH", "gfx950")
 
 HIP_FLAGS = [
@@ -51,30 +58,43 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+def calib_sources() -> list[Path]:
+    return sorted((CSRC / "calib").glob("*.hip"))
+
+
+def _compile(job) -> Path:
+    src, obj, extra = job
+    cmd = [_hipcc(), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
-    BUILD.mkdir(exist_ok=True)
-    srcs = sources()
-    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 16)
-    with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {lib.name} failed:\n{proc.stderr}")
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every HIP source, link the product library and the
+    measurement library; returns the product library's path."""
+    cal_dir = BUILD / "calib"
+    cal_dir.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    jobs = [(s, BUILD / (s.stem + ".o"), []) for s in srcs]
+    cal_jobs = [(s, cal_dir / (s.stem + ".o"), ["-DMLORA_TIMELINE=1"]) for s in srcs + calib_sources()]
+    workers = min(len(jobs) + len(cal_jobs), int(os.environ.get("MAX_JOBS", "8")), 16)
+    with ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
+        objs = list(pool.map(_compile, jobs + cal_jobs))
+    _link(objs[:len(jobs)], LIB)
+    _link(objs[len(jobs):], CALIB_LIB)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB} from {len(srcs)} sources and {CALIB_LIB.name}", file=sys.stderr)
     return LIB
 
 

@@ -474,8 +474,15 @@ void* scratch_ptr() {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    // The first call on a device may come while the caller's stream is
+    // being captured into a graph, and the lookup may load the code object
+    // first.  The thread's capture mode is relaxed around it, so a lookup
+    // made under capture is allowed, then restored.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t ex = hipThreadExchangeStreamCaptureMode(&mode);
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (ex == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || p == nullptr) {
       hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
       return nullptr;

@@ -53,6 +53,61 @@
 
 namespace mlora {
 
+// Per-phase timestamps of the planned kernel, in builds made with
+// MLORA_TIMELINE (the calibration library; the product library has none):
+// lane 0 of each wave keeps the low 32 bits of s_memrealtime (100 MHz) at
+// the phases below in LDS, and the workgroup writes them out once, at its
+// end, to tl_stamps[workgroup][wave][phase] (workgroup = its linear id,
+// y * gridDim.x + x).  Phases of a shrink item: 0
+// start, 1 plan entry in, 2 this wave's A and x in, 3 the four waves' sums
+// in LDS, 4 flag stored (wave 0, after the sums' acknowledgement), 5 item
+// done.  Of an expand item: 0 start, 1 entry in, 2 B and output requested,
+// 3 every chunk flag seen (or given up), 4 sums gathered, 5 y in LDS, 6
+// output stored and acknowledged.  A wait for vmcnt(0) precedes the
+// data-arrival stamps.
+#ifdef MLORA_TIMELINE
+constexpr int kTlBlocks = 8192;
+constexpr int kTlPhases = 8;
+__device__ uint32_t tl_stamps[kTlBlocks][4][kTlPhases];
+__shared__ uint32_t tl_lds[4][kTlPhases];
+#define MLORA_STAMP(k)                                                                                  \
+  do {                                                                                                  \
+    const uint32_t t_ = static_cast<uint32_t>(__builtin_amdgcn_s_memrealtime());                        \
+    if ((threadIdx.x & 63) == 0) tl_lds[threadIdx.x >> 6][k] = t_;                                      \
+  } while (0)
+#define MLORA_STAMP_AFTER_LOADS(k) \
+  do {                             \
+    wait_vmcnt<0>();               \
+    MLORA_STAMP(k);                \
+  } while (0)
+#define MLORA_STAMP_BEGIN()                                                    \
+  do {                                                                         \
+    if (threadIdx.x < 4 * kTlPhases) (&tl_lds[0][0])[threadIdx.x] = 0u;        \
+    lds_barrier();                                                             \
+    MLORA_STAMP(0);                                                            \
+  } while (0)
+#define MLORA_STAMP_FLUSH()                                                                               \
+  do {                                                                                                    \
+    lds_barrier();                                                                                        \
+    const unsigned b_ = blockIdx.y * gridDim.x + blockIdx.x;                                              \
+    if (threadIdx.x < 4 * kTlPhases && b_ < kTlBlocks)                                                    \
+      (&tl_stamps[b_][0][0])[threadIdx.x] = (&tl_lds[0][0])[threadIdx.x];                                 \
+  } while (0)
+#else
+#define MLORA_STAMP(k) \
+  do {                 \
+  } while (0)
+#define MLORA_STAMP_AFTER_LOADS(k) \
+  do {                             \
+  } while (0)
+#define MLORA_STAMP_BEGIN() \
+  do {                      \
+  } while (0)
+#define MLORA_STAMP_FLUSH() \
+  do {                      \
+  } while (0)
+#endif
+
 // The launch's dispatch id (its AQL packet index on the hardware queue).
 __device__ uint64_t planned_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
 
@@ -174,12 +229,14 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
     for (int j = 0; j < NBT; ++j)
       if (j < nbt) acc[j] = T::mma(acc[j], kk < a.in_dim ? af[sp][j] : zero_chunk(), xv[sp]);
   }
+  MLORA_STAMP_AFTER_LOADS(2);
   if (wave > 0) {
 #pragma unroll
     for (int j = 0; j < NBT; ++j)
       if (j < nbt) red[(wave - 1) * NBT + j][lane] = acc[j];
   }
   lds_barrier();
+  MLORA_STAMP(3);
   if (wave == 0) {
 #pragma unroll 1
     for (int w2 = 0; w2 < 3; ++w2)
@@ -204,9 +261,11 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
       wait_vmcnt<0>();
       asm volatile("" ::: "memory");
       if (lane == 0) __hip_atomic_store(flag_ptr(a, e, sg, c), flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      MLORA_STAMP(4);
     }
   }
   lds_barrier();
+  MLORA_STAMP(5);
 }
 
 template <class T, int WN>
@@ -224,25 +283,28 @@ __device__ __forceinline__ u32x4 load16_l2(__amdgpu_buffer_rsrc_t rsrc, int64_t 
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(off), 0, /*sc1*/ 16));
 }
 
-// The y sums of rows < nr and columns < rank of slice s into lds.part: unit
-// u = (group, row, quad) adds the chunks of its group in chunk order, up to
-// four chunks' sums requested together.
+// The y sums of rows < nr and columns < rank of slice s into lds.part: wave
+// g adds the chunks of group g in chunk order, lane l the (row l / 16, quad
+// l % 16) unit (and l + 64, ... for more rows), up to four chunks' sums
+// requested together.  The mapping uses shifts only: the item's set-up is
+// on the decode path's critical chain, and every instruction a wave issues
+// there costs about 4 cycles at four waves a SIMD.
 template <class T, int WN>
 __device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeLds<T, WN>& lds) {
+  static_assert(kGroups == 4 && kGroupMaxRank / 4 <= 16, "one chunk group per wave, at most 16 quads a row");
   const int quads = (en.rank + 3) >> 2;
   const int per = (a.kc + kGroups - 1) / kGroups;  // chunks per group
-  const int units = kGroups * en.nr * quads;
   const int ncols = a.n_slices * a.r_max;
   const int64_t bytes = static_cast<int64_t>(a.ws_rows) * a.kc * ncols * 4;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       a.partials, 0, static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff), kBufferRsrcWord3);
-  for (int u = threadIdx.x; u < units; u += 256) {
-    const int grp = u / (en.nr * quads);
-    const int rem = u - grp * (en.nr * quads);
-    const int row = rem / quads;
-    const int q = rem - row * quads;
-    const int c0 = grp * per;
-    const int c1 = min(c0 + per, a.kc);
+  const int grp = threadIdx.x >> 6;
+  const int c0 = grp * per;
+  const int c1 = min(c0 + per, a.kc);
+  for (int u = threadIdx.x & 63; u < en.nr * 16; u += 64) {
+    const int row = u >> 4;
+    const int q = u & 15;
+    if (q >= quads) continue;
     const int64_t base = sum_index(a, en.pos + row, 0, s * a.r_max + 4 * q);
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int cb = c0; cb < c1; cb += 4) {
@@ -258,12 +320,21 @@ __device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeL
   lds_barrier();
 }
 
+// Output chunks per thread of an expand item, and the entry row of chunk i
+// of thread tid.
+template <class T, int WN>
+struct ExpandRows {
+  static constexpr int CPR = kExpandBN * WN / T::VEC;  // chunks per output row
+  static constexpr int RPT = 16 * CPR / 256;
+  __device__ static __forceinline__ int row_of(int tid, int i) { return (tid + i * 256) / CPR; }
+};
+
 // Expand item (entry e, column tile nt_g).  LINKED: the sums come as tagged
 // words from this launch's shrink items (or are computed here), else as
 // fp32 from the previous launch.
 template <class T, int NBT, int SP, int WN, int RS, bool LINKED>
 __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, const Entry& en, int nt_g,
-                             const int (&orow_raw)[16 * kExpandBN * WN / T::VEC / 256], DecodeLds<T, WN>& lds,
+                             const int (&orow_raw)[ExpandRows<T, WN>::RPT], DecodeLds<T, WN>& lds,
                              f32x4 (*red)[kWave]) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -325,6 +396,7 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
   // item by as much (measured: +0.5 us per 0.5 us of delay).
   load_b();
   load_out();
+  MLORA_STAMP(2);
 
   if constexpr (LINKED) {
     // Wave 0 polls the flags of the chunks this slice needs (at most 64),
@@ -338,7 +410,9 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
       const uint64_t* fp = flag_ptr(a, e, sg, min(lane, a.kc - 1));
       const uint64_t limit = over > 0 ? static_cast<uint64_t>(over) : kDefaultWaitTicks;
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-      // A negative limit skips the wait: every chunk is computed here.
+      // A negative limit skips the wait: every chunk is computed here.  The
+      // clock (a scalar memory round trip) is read every eighth poll only.
+      uint32_t polls = 0;
       while (over >= 0) {
         if (st == 0) {
           const uint64_t w = __hip_atomic_load(fp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -348,13 +422,13 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
             st = 2;
         }
         if (__all(st != 0)) break;
-        if (__builtin_amdgcn_s_memrealtime() - t0 >= limit) break;
-        __builtin_amdgcn_s_sleep(1);
+        if ((++polls & 7) == 0 && __builtin_amdgcn_s_memrealtime() - t0 >= limit) break;
       }
       const uint64_t miss = __ballot(st != 1);
       if (lane == 0) lds.missing = miss;
     }
     lds_barrier();
+    MLORA_STAMP(3);
     uint64_t miss = lds.missing;
     if (miss != 0) {
       // Compute the missing chunks here, bit for bit as their shrink items
@@ -373,15 +447,16 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
     }
   }
   gather_sums<T, WN>(a, en, s, lds);
+  MLORA_STAMP(4);
   fence_regs(bf);
 
   // y = the chunk groups' sums added in group order, rounded like the
   // reference's mid; zero at and past the rank and for rows past the entry's.
   {
-    const int quads = a.r_max / 4;
-    for (int q = tid; q < 16 * quads; q += 256) {
-      const int row = q / quads;
-      const int c4 = (q - row * quads) * 4;
+    // Thread t: row t / 16, columns 4 (t % 16) .. + 3 (16 rows x 64 columns).
+    const int row = tid >> 4;
+    const int c4 = (tid & 15) * 4;
+    if (c4 < a.r_max) {
       f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
       if (row < en.nr && c4 < rank) {
 #pragma unroll
@@ -393,6 +468,7 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
     }
   }
   lds_barrier();
+  MLORA_STAMP(5);
 
   f32x4 acc[NBW];
 #pragma unroll
@@ -421,78 +497,143 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
     const int row = cidx / CPR;
     const int cc = cidx - row * CPR;
     const int n = n0 + cc * VEC;
-    if (row < en.nr && n < out_dim) {
+    // A plan row outside the call's rows (a plan made for a longer table)
+    // is not stored: its clamped reads served only memory safety.  The
+    // first column tile counts each such row as a plan error.
+    const bool in_rows = orow_raw[i] == orow[i];
+    if (row < en.nr && n < out_dim && in_rows) {
       const u32x4 d = *reinterpret_cast<const u32x4*>(lds.delta + row * LDS_STRIDE + cc * VEC);
       float f[VEC];
 #pragma unroll
       for (int q = 0; q < VEC; ++q) f[q] = chunk_elem<T>(ov[i], q) + chunk_elem<T>(d, q);
       st_chunk(out + static_cast<int64_t>(orow[i]) * a.out_stride + n, pack_chunk<T>(f));
+    } else if (row < en.nr && !in_rows && cc == 0 && nt_g == 0) {
+      atomicAdd(a.header + kWsPlanErrors, 1);
     }
   }
+  MLORA_STAMP_AFTER_LOADS(6);
   lds_barrier();
 }
 
-// Items [0, n_shrink) of an entry are its shrink items, the next n_tiles its
-// expand items; workgroup b is item b / e_grid of entry b % e_grid, then of
-// entries b % e_grid + e_grid, + 2 e_grid, ... while the plan has them.
-template <class T, int NBT, int WN, int RS, int SCHED>
-__global__ __launch_bounds__(256, NBT >= 8 ? 2 : 4) void planned_kernel(const int32_t* __restrict__ plan, DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
-  __shared__ f32x4 red[3 * NBT][kWave];
+// Shrink items of entries j, j + e_grid, ... (item: K chunk, and slice group
+// when the slices' A blocks are split over items).  en / xrow_raw: entry j
+// and this thread's row word, already requested.
+template <class T, int NBT, int SCHED>
+__device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, int item, int n_ent, Entry en,
+                             int xrow_raw, f32x4 (*red)[kWave]) {
   constexpr int SP = kGroupStepsLinked;
-  const int n_shrink = (SCHED == kGroupExpandOnly) ? 0 : a.s_groups * a.kc;
-  const int item = blockIdx.x / a.e_grid;
-  const int j = blockIdx.x - item * a.e_grid;
-  constexpr int RPT = 16 * kExpandBN * WN / T::VEC / 256;  // output chunks per thread of an expand item
-  const bool shrink = item < n_shrink;
-  // The first entry, its rows this thread needs and the plan's entry count
-  // go out together.
-  int e = j;
-  const int ef = min(e, a.plan_cap - 1);
-  int rows_raw[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i)
-    rows_raw[i] = load_entry_row(plan, ef, shrink ? (threadIdx.x & 15) : (threadIdx.x + i * 256) * T::VEC / (kExpandBN * WN));
-  Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
-  const int n_ent = min(plan[0], min(a.plan_cap, a.e_cap));
-  if (j == 0 && item == 0 && threadIdx.x == 0 && plan[0] > min(a.plan_cap, a.e_cap))
+  int sg = 0, c = item;
+  if (a.s_groups != 1) {
+    sg = item / a.kc;
+    c = item - sg * a.kc;
+  }
+  const uint64_t flag = SCHED == kGroupLinked ? flag_word() : 0;
+  // The first entry is taken apart from the loop over the others (rare: a
+  // grid smaller than the plan), so nothing the loop hoists runs before it.
+  MLORA_STAMP(1);
+  if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
+    shrink_chunk<T, NBT, SP>(a, j, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag);
+  else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0)
     atomicAdd(a.header + kWsPlanErrors, 1);
-  while (e < n_ent) {
-    if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows) {
-      if (shrink) {
-        if constexpr (SCHED != kGroupExpandOnly)
-          shrink_chunk<T, NBT, SP>(a, e, en, clamp_row(rows_raw[0], a.rows), item / a.kc, item % a.kc, red,
-                                   SCHED == kGroupLinked ? flag_word() : 0);
-      } else if constexpr (SCHED != kGroupShrinkOnly) {
-        expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked>(a, plan, e, en, item - n_shrink, rows_raw, lds, red);
-      }
-    } else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0) {
+  for (int e = j + a.e_grid; e < n_ent; e += a.e_grid) {
+    xrow_raw = load_entry_row(plan, e, threadIdx.x & 15);
+    en = load_entry(plan, e, a.r_max, a.num_slots);
+    if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
+      shrink_chunk<T, NBT, SP>(a, e, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag);
+    else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0)
       atomicAdd(a.header + kWsPlanErrors, 1);
-    }
+  }
+}
+
+// Expand items (column tile `tile`) of entries j, j + e_grid, ...;
+// count_errors: this launch has no shrink items, so tile 0 reports entries
+// it cannot take.
+template <class T, int NBT, int WN, int RS, int SCHED>
+__device__ void expand_items(const int32_t* plan, const DecodeArgs& a, int j, int tile, int n_ent, Entry en,
+                             int (&rows_raw)[ExpandRows<T, WN>::RPT], DecodeLds<T, WN>& lds, f32x4 (*red)[kWave],
+                             bool count_errors) {
+  constexpr int SP = kGroupStepsLinked;
+  constexpr int RPT = ExpandRows<T, WN>::RPT;
+  for (int e = j;;) {
+    MLORA_STAMP(1);
+    if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
+      expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked>(a, plan, e, en, tile, rows_raw, lds, red);
+    else if (count_errors && en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && tile == 0)
+      atomicAdd(a.header + kWsPlanErrors, 1);
     e += a.e_grid;
     if (e >= n_ent) break;
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      rows_raw[i] = load_entry_row(plan, e, shrink ? (threadIdx.x & 15) : (threadIdx.x + i * 256) * T::VEC / (kExpandBN * WN));
+    for (int i = 0; i < RPT; ++i) rows_raw[i] = load_entry_row(plan, e, ExpandRows<T, WN>::row_of(threadIdx.x, i));
     en = load_entry(plan, e, a.r_max, a.num_slots);
   }
 }
 
+// Workgroup (j, item) of the grid (e_grid x items) is item `item` of entry
+// j, then of entries j + e_grid, ... while the plan has them; items [0,
+// n_shrink) are shrink items, the next n_tiles expand items.  Workgroups go
+// to the XCDs round-robin in x-fastest order and e_grid is a multiple of 8,
+// so every item of entry j runs on XCD j mod 8.  plan_cap and n_shrink come
+// as leading arguments (preloaded in SGPRs), so the first entry, the row
+// words and the plan's entry count are requested at once, together with
+// every cache line of the other arguments.
+template <class T, int NBT, int WN, int RS, int SCHED>
+__global__ __launch_bounds__(256, NBT >= 8 ? 2 : 4) void planned_kernel(const int32_t* __restrict__ plan,
+                                                                       int plan_cap, int n_shrink, DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
+  __shared__ f32x4 red[3 * NBT][kWave];
+  MLORA_STAMP_BEGIN();
+  constexpr int RPT = ExpandRows<T, WN>::RPT;
+  const int j = blockIdx.x;
+  const int item = blockIdx.y;
+  const bool shrink = item < n_shrink;
+  const int ef = min(j, plan_cap - 1);
+  int rows_raw[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    rows_raw[i] = load_entry_row(plan, ef, shrink ? (threadIdx.x & 15) : ExpandRows<T, WN>::row_of(threadIdx.x, i));
+  const Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
+  const int p0 = plan[0];
+  {
+    // Touch every cache line of the kernel arguments in the round trip that
+    // brings the entry, so the argument loads the compiler places over the
+    // item's set-up hit the scalar cache (which every launch starts cold).
+    const char* ks = (const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int kLines = static_cast<int>((sizeof(DecodeArgs) + 16 + 63) / 64);
+    int acc = 0;
+#pragma unroll
+    for (int i = 0; i < kLines; ++i) acc |= *reinterpret_cast<const int*>(ks + i * 64);
+    asm volatile("" ::"s"(acc), "s"(p0), "s"(en.slot), "s"(en.rank), "s"(en.nr), "s"(en.pos));
+  }
+  const int n_ent = min(p0, min(plan_cap, a.e_cap));
+  if (j == 0 && item == 0 && threadIdx.x == 0 && p0 > min(plan_cap, a.e_cap)) atomicAdd(a.header + kWsPlanErrors, 1);
+  if (j < n_ent) {
+    if (shrink) {
+      if constexpr (SCHED != kGroupExpandOnly) shrink_items<T, NBT, SCHED>(plan, a, j, item, n_ent, en, rows_raw[0], red);
+    } else if constexpr (SCHED != kGroupShrinkOnly) {
+      expand_items<T, NBT, WN, RS, SCHED>(plan, a, j, item - n_shrink, n_ent, en, rows_raw, lds, red, n_shrink == 0);
+    }
+  }
+  MLORA_STAMP_FLUSH();
+}
+
 template <class T, int NBT, int WN, int RS>
 hipError_t launch_sched(const int32_t* plan, const DecodeArgs& a, int sched, int n_items, hipStream_t stream) {
-  const int64_t blocks = static_cast<int64_t>(n_items) * a.e_grid;
-  if (blocks <= 0) return hipSuccess;
-  if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<unsigned>(blocks));
+  if (n_items <= 0 || a.e_grid <= 0) return hipSuccess;
+  if (n_items > 65535 || !grid_fits(static_cast<int64_t>(n_items) * a.e_grid)) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(a.e_grid), static_cast<unsigned>(n_items));
+  const int n_shrink = sched == kGroupExpandOnly ? 0 : a.s_groups * a.kc;
   switch (sched) {
     case kGroupLinked:
-      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupLinked>), grid, dim3(256), 0, stream, plan, a);
+      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupLinked>), grid, dim3(256), 0, stream, plan, a.plan_cap,
+                         n_shrink, a);
       break;
     case kGroupShrinkOnly:
-      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupShrinkOnly>), grid, dim3(256), 0, stream, plan, a);
+      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupShrinkOnly>), grid, dim3(256), 0, stream, plan,
+                         a.plan_cap, n_shrink, a);
       break;
     default:
-      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupExpandOnly>), grid, dim3(256), 0, stream, plan, a);
+      hipLaunchKernelGGL((planned_kernel<T, NBT, WN, RS, kGroupExpandOnly>), grid, dim3(256), 0, stream, plan,
+                         a.plan_cap, n_shrink, a);
       break;
   }
   return hipGetLastError();
@@ -586,11 +727,7 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
     __syncthreads();
   }
   const int n_entries = run[0];
-  if (tid == 0) {
-    plan[0] = n_entries;
-    plan[1] = run[1];
-    plan[2] = cap;
-  }
+  if (tid < kPlanHeaderWords) plan[tid] = tid == 0 ? n_entries : tid == 1 ? run[1] : tid == 2 ? cap : 0;
   // Entry headers, with every row word first set to an invalid row.
   for (int s = tid; s < ns; s += kBuildThreads) {
     const int c = cnt[s];
@@ -692,3 +829,25 @@ hipError_t launch_planned(const int32_t* plan, const DecodeArgs& args, int dtype
 }
 
 }  // namespace mlora
+
+#ifdef MLORA_TIMELINE
+// Calibration builds: clear and read the planned kernel's timestamps
+// ([kTlBlocks][4 waves][kTlPhases] uint32, the low word of a 100 MHz
+// counter: differences modulo 2^32 are ticks of 10 ns).
+extern "C" int mlora_tl_words(void) { return mlora::kTlBlocks * 4 * mlora::kTlPhases; }
+
+// Zero the first `words` stamp words (a phase left at 0 was not reached).
+extern "C" int mlora_tl_clear(int words, void* stream) {
+  if (words < 0 || words > mlora_tl_words()) return -1;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(mlora::tl_stamps));
+  if (e == hipSuccess) e = hipMemsetAsync(p, 0, sizeof(uint32_t) * words, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+
+extern "C" int mlora_tl_read(uint32_t* host, int words) {
+  if (host == nullptr || words < 0 || words > mlora_tl_words()) return -1;
+  const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(mlora::tl_stamps), sizeof(uint32_t) * words);
+  return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+#endif

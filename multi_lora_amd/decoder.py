@@ -73,6 +73,22 @@ class StaticKV:
         self.values: List[torch.Tensor] = [torch.zeros(vshape, device=device, dtype=dtype)
                                            for _ in range(config.num_hidden_layers)]
 
+    @property
+    def layers(self) -> List["KVLayer"]:
+        """Per-layer views ``layers[i].keys`` / ``layers[i].values`` of the same
+        buffers, as a transformers ``StaticCache`` exposes its layers
+        (multi_lora/tests/test_graph_decode.py:93-97 reads them)."""
+        return [KVLayer(k, v) for k, v in zip(self.keys, self.values)]
+
+
+@dataclass
+class KVLayer:
+    """One layer's key buffer (``[batch, kv_heads, head_dim, max_len]``) and
+    value buffer (``[batch, kv_heads, max_len, head_dim]``) of a ``StaticKV``."""
+
+    keys: torch.Tensor
+    values: torch.Tensor
+
 
 class DecoderRMSNorm(nn.Module):
     """``x * rsqrt(mean(x^2) + eps) * w`` (fp32 math, one rounding); replaced by the HIP kernel via fuse_rmsnorm."""

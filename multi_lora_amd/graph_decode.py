@@ -55,6 +55,11 @@ class DecodeStep:
     def new(cls, mgr, batch: int, start: int, max_len: int) -> "DecodeStep":
         return cls(mgr, batch, start, max_len)
 
+    def like_new(self, mgr) -> "DecodeStep":
+        """A second step of the same shape (batch, start, max_len), with its own
+        empty KV cache and its counter at ``start`` (multi_lora/graph_decode.py:55-57)."""
+        return DecodeStep.new(mgr, self.batch, self.start, self.max_len)
+
     def rewind(self) -> None:
         """Return to position ``start``: the counter and the mask, nothing else."""
         self.kv_pos.fill_(self.start)

@@ -65,6 +65,26 @@ class _RankPlan:
         self.dims = dims
         self.device_table: Optional[torch.Tensor] = None  # mlora_pool_key[len(keys)] on the device
         self.max_numel = max([rank * dims[k][0] for k in keys] + [dims[k][1] * rank for k in keys] + [0])
+        self.tables: Optional[dict] = None
+
+    def build_tables(self, buffers: "_GpuBuffers", device) -> dict:
+        """The scatter tables of this layout over ``buffers``' slot tensors, built
+        once (the slot tensors keep their addresses while the key set holds):
+        ``keys`` (the mlora_pool_key array on the device), ``n`` keys,
+        ``max_numel`` and ``num_slots``; what ``kernels.scatter_stage`` takes,
+        as the reference's ``_RankPlan.build_tables`` feeds its scatter kernel
+        (multi_lora/pool.py:60-96)."""
+        if self.tables is None:
+            arr = (_ffi.PoolKey * len(self.keys))()
+            for j, key in enumerate(self.keys):
+                a, b = buffers.A[key], buffers.B[key]
+                arr[j] = _ffi.PoolKey(a.data_ptr(), a.stride(0), self.a_off[key], b.data_ptr(), b.stride(0),
+                                      b.stride(1), self.b_off[key], a.shape[2], b.shape[1])
+            host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+            self.device_table = host.to(device)
+            self.tables = {"keys": self.device_table, "n": len(self.keys), "max_numel": self.max_numel,
+                           "num_slots": buffers.max_loras_per_batch}
+        return self.tables
 
 
 class _GpuBuffers:
@@ -224,27 +244,15 @@ class _GpuBuffers:
 
     def _key_table(self, plan: _RankPlan) -> torch.Tensor:
         """The plan's mlora_pool_key array on the device, built once per plan."""
-        if plan.device_table is None:
-            arr = (_ffi.PoolKey * len(plan.keys))()
-            for j, key in enumerate(plan.keys):
-                a, b = self.A[key], self.B[key]
-                arr[j] = _ffi.PoolKey(a.data_ptr(), a.stride(0), plan.a_off[key], b.data_ptr(), b.stride(0),
-                                      b.stride(1), plan.b_off[key], a.shape[2], b.shape[1])
-            host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
-            plan.device_table = host.to(self.device)
-        return plan.device_table
+        return plan.build_tables(self, self.device)["keys"]
 
     def _scatter_staged(self, stage: torch.Tensor, slots: List[int], plan: _RankPlan) -> None:
         """One launch: staged rows [0, len(slots)) into their slots, every key."""
-        table = self._key_table(plan)
+        from .kernels.scatter_bank import scatter_stage
+
         # From pinned memory, so the host does not wait for the copies queued before it.
         slots_dev = torch.tensor(slots, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
-        rc = _ffi.lib().mlora_pool_scatter(
-            stage.data_ptr(), stage.stride(0), len(slots), slots_dev.data_ptr(), table.data_ptr(), len(plan.keys),
-            plan.rank, self.max_loras_per_batch, plan.max_numel, _ffi.dtype_code(self.dtype),
-            _ffi.stream_ptr(self.device),
-        )
-        _ffi.check(rc, "mlora_pool_scatter")
+        scatter_stage(stage, slots_dev, plan.build_tables(self, self.device), plan.total, len(slots), plan.rank)
 
     def _scatter(self, flat: torch.Tensor, slot: int, plan: _RankPlan) -> None:
         """Copy one adapter's packed blocks into slot ``slot`` (first ``rank`` rows / columns)."""

@@ -204,3 +204,40 @@ def test_static_grouped_rejects_shapes_beyond_its_scratch():
     rc = lib.mlora_apply_grouped_static(4096, 16384, 4096, 16384, sl, 3, 64, 8192, 16384, ctypes.byref(meta),
                                         _ffi.MLORA_BF16, 0, 3, None)
     assert rc == -3 and b"static scratch" in lib.mlora_last_error()
+
+
+def test_scatter_stage_export_mirrors_the_reference():
+    """multi_lora_amd.kernels exports scatter_stage with the reference's
+    signature (multi_lora/kernels/scatter_bank.py:68), and, like every
+    product entry point, has no CPU path."""
+    import inspect
+
+    import torch
+
+    from multi_lora_amd import kernels
+
+    assert "scatter_stage" in kernels.__all__
+    params = list(inspect.signature(kernels.scatter_stage).parameters)
+    assert params == ["stage", "slots", "tables", "total", "h", "rank", "BLOCK"]
+    assert inspect.signature(kernels.scatter_stage).parameters["BLOCK"].default == 8192
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        kernels.scatter_stage(torch.zeros(1, 8), torch.zeros(1, dtype=torch.int64), {}, 8, 1, 1)
+
+
+def test_calibration_library_exports():
+    """The measurement library (built beside the product) carries the
+    timeline readers and the calibration kernels; the product carries none
+    of them."""
+    import ctypes
+
+    from multi_lora_amd.build import CALIB_LIB
+
+    if not CALIB_LIB.exists():
+        pytest.skip("measurement library not built")
+    cal = ctypes.CDLL(str(CALIB_LIB))
+    for name in ("mlora_tl_words", "mlora_tl_clear", "mlora_tl_read", "mlora_calib_empty", "mlora_calib_stream",
+                 "mlora_apply_grouped"):
+        assert hasattr(cal, name), name
+    prod = _ffi.lib()
+    for name in ("mlora_tl_words", "mlora_tl_clear", "mlora_calib_empty"):
+        assert not hasattr(prod, name), name

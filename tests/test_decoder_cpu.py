@@ -102,3 +102,30 @@ def test_rotary_over_a_fused_qkv_output_equals_q_and_k_apart():
 
     qr = q.reshape(rows, h, d)
     torch.testing.assert_close(qj, qr * cos + rotate_half(qr) * sin, atol=1e-6, rtol=1e-6)
+
+
+def test_decode_step_like_new_and_layer_views():
+    """DecodeStep.like_new (multi_lora/graph_decode.py:55-57) gives a second
+    step of the same shape with its own empty cache, counter at start and
+    prompt-only mask; kv.layers[i].keys / .values are the cache's buffers
+    (the view multi_lora/tests/test_graph_decode.py:93-97 reads)."""
+    from types import SimpleNamespace
+
+    from multi_lora_amd.graph_decode import DecodeStep
+
+    m = model()
+    mgr = SimpleNamespace(model=m, pool=SimpleNamespace(device=torch.device("cpu"), dtype=torch.float32))
+    step = DecodeStep.new(mgr, batch=2, start=3, max_len=8)
+    step.kv_pos.add_(2)
+    step.kv.keys[0].fill_(1.0)
+    twin = step.like_new(mgr)
+    assert (twin.batch, twin.start, twin.max_len) == (2, 3, 8)
+    assert int(twin.kv_pos) == 3 and int(step.kv_pos) == 5
+    assert twin.kv.keys[0].data_ptr() != step.kv.keys[0].data_ptr()
+    assert not twin.kv.keys[0].any()
+    assert twin.attn_mask[..., :3].all() and not twin.attn_mask[..., 3:].any()
+    layers = step.kv.layers
+    assert len(layers) == m.config.num_hidden_layers
+    for i, layer in enumerate(layers):
+        assert layer.keys.data_ptr() == step.kv.keys[i].data_ptr()
+        assert layer.values.data_ptr() == step.kv.values[i].data_ptr()

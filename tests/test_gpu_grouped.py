@@ -285,6 +285,57 @@ def test_plan_too_small_is_reported(dev):
     assert torch.equal(got[4:], base[4:])
 
 
+@pytest.mark.parametrize("mode", [1, 2])
+def test_plan_for_more_rows_than_the_call(dev, mode):
+    """A plan made for a longer table than the call (40 rows planned, 24
+    rows called): plan rows at or past the call's rows are not stored, and
+    no row receives another row's delta.  Every output row is either left
+    untouched or equal, bit for bit, to the same call with a table of the
+    24 rows; some rows are computed, and the workspace counts plan errors."""
+    wl = synthetic.decode_q(device=dev, tokens=40, in_dim=1024, out=512, n_slots=8, n_adapters=5, rank=16, seed=81)
+    rows = 24
+    x, base = wl.x[:rows], wl.base[:rows]
+    lws = LinkedWorkspace()
+    out = base.clone()
+    assert apply_grouped(x, wl.a_stacks, wl.b_stacks, wl.meta, out, [0], lws, mode=mode)
+    proper = make_meta(wl.seg_lens[:rows], wl.seg_slots[:rows], wl.slot_ranks, wl.scalings, dev, torch.bfloat16)
+    want = base.clone()
+    assert apply_grouped(x, wl.a_stacks, wl.b_stacks, proper, want, [0], LinkedWorkspace(), mode=mode)
+    assert counters(lws)[1] > 0
+    got, want, base = out.cpu(), want.cpu(), base.cpu()
+    untouched = (got == base).all(dim=1)
+    computed = (got == want).all(dim=1)
+    assert bool((untouched | computed).all())
+    assert bool((computed & ~(want == base).all(dim=1)).any())
+
+
+def test_device_plan_into_a_dirty_buffer(dev):
+    """mlora_build_plan writes every header word (the rest 0) and every word of
+    the entries it makes, so a buffer full of garbage gives the host's plan."""
+    wl = synthetic.decode_q(device=dev, tokens=50, in_dim=1024, out=512, n_slots=12, n_adapters=7, rank=16, seed=82)
+    cap = 50
+    bare = make_meta(wl.seg_lens, wl.seg_slots, wl.slot_ranks, wl.scalings, dev, torch.bfloat16, with_plan=False)
+    lib = _ffi.lib()
+    words = lib.mlora_plan_bytes(cap) // 4
+    plan = torch.full((words,), -123457, dtype=torch.int32, device=dev)
+    from multi_lora_amd.kernels.lora_ops import seg_meta
+    import ctypes
+    m, keep = seg_meta(bare, dev, 12)
+    m.plan, m.plan_cap, m.plan_entries = None, 0, -1
+    _ffi.check(lib.mlora_build_plan(ctypes.byref(m), 50, plan.data_ptr(), cap, _ffi.stream_ptr(dev)), "build_plan")
+    torch.cuda.synchronize()
+    got = plan.cpu().numpy()
+    host = np.zeros(plan_words(cap), dtype=np.int32)
+    indptr = [0]
+    for n in wl.seg_lens:
+        indptr.append(indptr[-1] + n)
+    scal_f32 = torch.tensor(wl.scalings, dtype=torch.bfloat16).float().numpy()
+    n = build_plan(indptr, wl.seg_slots, wl.slot_ranks, scal_f32, 12, 50, host)
+    used = 16 + n * 32
+    assert np.array_equal(got[:used], host[:used])
+    del keep
+
+
 def test_linked_repeated_calls_are_bit_identical(dev):
     wl = synthetic.decode_q(device=dev, tokens=128, seed=21)
     lws = LinkedWorkspace()

@@ -73,6 +73,39 @@ def test_resident_metadata_rewrite_matches_oracle_padding():
     assert all(a <= b for a, b in zip(ip, ip[1:]))
 
 
+# Literal columns after an in-place rewrite, worked out by hand from
+# multi_lora/batch_info.py:169-176: every column keeps its length, unused
+# segment slots get weight 0, length 0, indptr = the new total (so seg_indptr
+# stays monotone), and lora_ranks / scalings (one per pool slot) are
+# overwritten whole.
+RESIDENT_PADDING_CASES = [
+    # (first batch: weight_indices, seq_lens), (rewrite: weight_indices, ranks, scalings, seq_lens), expected
+    (([1, 0, 2, 1], [3, 1, 2, 5]), ([2, 0], [4, 8, 1], [0.5, 2.0, 1.0], []),
+     {"weight_indices": [2, 0, 0, 0], "seg_lens": [1, 1, 0, 0], "seg_indptr": [0, 1, 2, 2, 2],
+      "lora_ranks": [4, 8, 1], "scalings": [0.5, 2.0, 1.0]}),
+    (([0, 1, 2], []), ([1], [0, 16, 8], [0.0, 0.25, 4.0], [5]),
+     {"weight_indices": [1, 0, 0], "seg_lens": [5, 0, 0], "seg_indptr": [0, 5, 5, 5],
+      "lora_ranks": [0, 16, 8], "scalings": [0.0, 0.25, 4.0]}),
+]
+
+
+@pytest.mark.parametrize("first,rewrite,want", RESIDENT_PADDING_CASES)
+def test_resident_padding_known_answer(first, rewrite, want):
+    """The padding of an in-place rewrite, as literals: the oracle and the product both give them."""
+    w0, lens0 = first
+    w1, ranks, scal, lens1 = rewrite
+    assert resident_columns(w1, ranks, scal, lens1, capacity=len(w0)) == want
+    cpu = torch.device("cpu")
+    meta = bi.empty_kernel_input_metadata(device=cpu, dtype=torch.float32)
+    info0 = bi.BatchLoRAInfo(weight_indices=w0, lora_ranks=[8] * len(ranks), scalings=[1.0] * len(ranks))
+    meta = bi.write_kernel_input_metadata(meta, info0, device=cpu, dtype=torch.float32, seq_lens=lens0)
+    info1 = bi.BatchLoRAInfo(weight_indices=w1, lora_ranks=ranks, scalings=scal)
+    assert bi.write_kernel_input_metadata(meta, info1, device=cpu, dtype=torch.float32, seq_lens=lens1) is meta
+    for col, v in want.items():
+        assert getattr(meta, col).tolist() == v, col
+    assert meta.bs == len(w1) and meta.max_len == max(lens1 or [1])
+
+
 def test_metadata_shapes_known_answer():
     # multi_lora/tests/test_phase4_backend.py:85-95: two decode rows [a, None]
     # in a 3-slot pool -> bs 2, seg_indptr[:3] == [0, 1, 2], one rank per slot.

@@ -7,6 +7,9 @@ given and with the plan built on the device into the scratch.
 """
 
 import ctypes
+import subprocess
+import sys
+from pathlib import Path
 
 import pytest
 import torch
@@ -68,3 +71,15 @@ def test_static_scratch_with_a_device_built_plan_and_both_schedules(dev):
     smaller = synthetic.decode_q(device=dev, tokens=9, in_dim=1024, out=512, n_slots=6, n_adapters=4, rank=16,
                                  seed=64)
     assert torch.equal(static_call(smaller, smaller.meta), workspace_call(smaller, smaller.meta))
+
+
+def test_static_entry_captured_as_the_first_library_call_in_a_fresh_process():
+    """The static scratch is looked up on the first call on a device; that
+    call may be under graph capture.  A child process (so no earlier call has
+    made the lookup) captures the static entry first, replays the graph
+    three times, and compares each replay with the workspace entry point."""
+    helper = Path(__file__).resolve().parent / "static_first_call_in_capture.py"
+    print(f"child: {helper.name}", flush=True)
+    r = subprocess.run([sys.executable, str(helper)], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "replays equal: 3" in r.stdout

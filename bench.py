@@ -78,6 +78,9 @@ OTHER_WORKLOADS = {
                   "128 rank-32 adapters",
     "decode_q_resident": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool holding 64 resident "
                          "rank-16 adapters, tokens drawn over 32 of them",
+    "decode_q_device_plan": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters; "
+                            "the segment table carries no plan (device tensors only, as a hand-built "
+                            "KernelInputMetaData), so the library builds the plan on the device for every call",
     "c5_gate_up": "the 32-layer step's gate|up LoRA call: 4096->2x14336, mixed batch of 2 x 512 prefill + 64 decode "
                   "rows (66 segments), 128-slot pool holding 35 rank-16 adapters",
     "c5_qkv": "the 32-layer step's q|k|v LoRA call: 4096->[4096,1024,1024], mixed batch of 2 x 512 prefill + 64 "
@@ -500,7 +503,9 @@ def bench_other(args) -> int:
     torch.cuda.set_device(dev)
     name = args.workload
     host = workload_host(name)
-    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+    bare = name == "decode_q_device_plan"
+    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16,
+                               host_copies=not bare, with_plan=not bare)
     e = host.x.element_size()
     n_rep = replicas_for(touched_bytes(host))
     reps = []
@@ -761,7 +766,7 @@ def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> di
 # COPY_ELEMS bf16 values (read once, written once).
 COPY_ELEMS = 32 << 20
 PROFILE_CALLS = 64
-GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_qkv")
+GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_q_device_plan", "decode_qkv")
 PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down", "c5_gate_up", "c5_qkv", "c5_o", "c5_down")
 MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
@@ -769,7 +774,7 @@ MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "GR
 def grouped_host(name: str):
     from multi_lora_amd import synthetic
 
-    if name == "decode_q":
+    if name in ("decode_q", "decode_q_device_plan"):
         return synthetic.decode_q(device="cpu")
     if name == "decode_q_resident":
         return synthetic.decode_q(device="cpu", resident=64)
@@ -817,7 +822,9 @@ def profile_traffic(name: str) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     host = workload_host(name)
-    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16)
+    bare = name == "decode_q_device_plan"
+    meta = synthetic.make_meta(host.seg_lens, host.seg_slots, host.slot_ranks, host.scalings, dev, torch.bfloat16,
+                               host_copies=not bare, with_plan=not bare)
     n_rep = replicas_for(touched_bytes(host))
     reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
              host.base.to(dev)) for _ in range(n_rep)]

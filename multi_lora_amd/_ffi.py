@@ -55,6 +55,8 @@ PLAN_ROW_WORD = 8
 WS_FALLBACKS = 0
 WS_WAIT_TICKS = 1
 WS_PLAN_ERRORS = 2
+# Pools of up to this many slots get a device-built plan (mlora_build_plan).
+PLAN_BUILD_MAX_SLOTS = 2048
 
 
 # Segments of at most this many rows are short in the table summary

@@ -568,6 +568,12 @@ __device__ void expand_items(const int32_t* plan, const DecodeArgs& a, int j, in
   }
 }
 
+// Three workgroups a CU for the single launch over four A blocks (r_max 48
+// and 64): at four, the loop invariants of its expand items (their row
+// words and pointers) spilled 12-20 bytes a lane to scratch; at three it
+// holds them in 135-138 VGPRs (rank 64: 14.07 vs 13.88 us, rank 48: 11.58
+// vs 11.62 us).
+//
 // Workgroup (j, item) of the grid (e_grid x items) is item `item` of entry
 // j, then of entries j + e_grid, ... while the plan has them; items [0,
 // n_shrink) are shrink items, the next n_tiles expand items.  Workgroups go
@@ -577,7 +583,7 @@ __device__ void expand_items(const int32_t* plan, const DecodeArgs& a, int j, in
 // words and the plan's entry count are requested at once, together with
 // every cache line of the other arguments.
 template <class T, int NBT, int WN, int RS, int SCHED>
-__global__ __launch_bounds__(256, NBT >= 8 ? 2 : 4) void planned_kernel(const int32_t* __restrict__ plan,
+__global__ __launch_bounds__(256, NBT >= 8 ? 2 : (NBT >= 4 && SCHED == kGroupLinked) ? 3 : 4) void planned_kernel(const int32_t* __restrict__ plan,
                                                                        int plan_cap, int n_shrink, DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
   __shared__ f32x4 red[3 * NBT][kWave];
@@ -675,37 +681,59 @@ hipError_t launch_dtype(const int32_t* plan, const DecodeArgs& a, int nbt, int m
 // Segment bounds are clamped to [0, rows); slots outside [0, num_slots) and
 // rank-0 slots get no entry.  Entries past `cap` are not written (the header
 // still counts them, and the apply kernels report a plan error).
+//
+// The table is read once: every slot's rank and scaling and a pass of up to
+// kBuildSegs segments are requested together and kept in LDS, so a pass
+// costs one round trip to memory; the rest is LDS work and stores.
 constexpr int kBuildThreads = 1024;
 constexpr int kBuildSegs = 1024;  // segments staged in LDS per pass
 
 __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, int rows, int32_t* plan, int cap) {
-  __shared__ int cnt[kPlanBuildMaxSlots];
-  __shared__ int eoff[kPlanBuildMaxSlots];
-  __shared__ int poff[kPlanBuildMaxSlots];
-  __shared__ int seg_slot[kBuildSegs];
-  __shared__ int seg_start[kBuildSegs];
-  __shared__ int seg_len[kBuildSegs];
+  __shared__ int cnt[kPlanBuildMaxSlots];   // rows of each slot
+  __shared__ int fill[kPlanBuildMaxSlots];  // rows of each slot placed by earlier passes
+  __shared__ int eoff[kPlanBuildMaxSlots];  // first entry of each slot
+  __shared__ int poff[kPlanBuildMaxSlots];  // first row position of each slot
+  __shared__ int rank_of[kPlanBuildMaxSlots];
+  __shared__ int seg_w[kBuildSegs];         // live slot of the pass's segments (-1: none)
+  __shared__ int seg_a[kBuildSegs];
+  __shared__ int seg_n[kBuildSegs];
   __shared__ int tmp[kBuildThreads / kWave];
   __shared__ int run[2];
   const int tid = threadIdx.x;
   const int ns = m.num_slots;
-  for (int s = tid; s < ns; s += kBuildThreads) cnt[s] = 0;
-  __syncthreads();
-  auto seg_of = [&](int i, int* slot, int* st, int* len) {
-    const int a0 = min(max(m.indptr[i], 0), rows);
-    const int a1 = min(max(m.indptr[i + 1], 0), rows);
-    const int w = m.widx[i];
-    const bool live = w >= 0 && w < ns && m.ranks[w] > 0 && a1 > a0;
-    *slot = live ? w : -1;
-    *st = a0;
-    *len = live ? a1 - a0 : 0;
-  };
-  for (int i = tid; i < m.bs; i += kBuildThreads) {
-    int w, st, len;
-    seg_of(i, &w, &st, &len);
-    if (w >= 0) atomicAdd(&cnt[w], len);
+  const int passes = (m.bs + kBuildSegs - 1) / kBuildSegs;
+  // Ranks of every slot and the first pass of segments, requested at once.
+  for (int s = tid; s < ns; s += kBuildThreads) {
+    rank_of[s] = m.ranks[s];
+    cnt[s] = 0;
+    fill[s] = 0;
   }
+  auto stage = [&](int b0) {
+    // Segment b0 + tid (one per thread: kBuildSegs == kBuildThreads).
+    const int i = b0 + tid;
+    int a0 = 0, a1 = 0, w = -1;
+    if (i < m.bs) {
+      a0 = min(max(m.indptr[i], 0), rows);
+      a1 = min(max(m.indptr[i + 1], 0), rows);
+      w = m.widx[i];
+    }
+    return int3{a0, a1, w};
+  };
+  int3 sg = stage(0);
   __syncthreads();
+  auto publish = [&](int3 v) {
+    const bool live = v.z >= 0 && v.z < ns && v.y > v.x && rank_of[v.z] > 0;
+    seg_w[tid] = live ? v.z : -1;
+    seg_a[tid] = v.x;
+    seg_n[tid] = live ? v.y - v.x : 0;
+  };
+  // Pass 1 counts every slot's rows.
+  for (int pass = 0; pass < passes; ++pass) {
+    if (pass > 0) sg = stage(pass * kBuildSegs);
+    publish(sg);
+    if (seg_w[tid] >= 0) atomicAdd(&cnt[seg_w[tid]], seg_n[tid]);
+    __syncthreads();
+  }
   // Exclusive scans over the slots (in chunks of kBuildThreads): entries and rows.
   if (tid == 0) run[0] = run[1] = 0;
   __syncthreads();
@@ -728,7 +756,7 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
   }
   const int n_entries = run[0];
   if (tid < kPlanHeaderWords) plan[tid] = tid == 0 ? n_entries : tid == 1 ? run[1] : tid == 2 ? cap : 0;
-  // Entry headers, with every row word first set to an invalid row.
+  // Entry words other than the rows: one thread per (slot, entry).
   for (int s = tid; s < ns; s += kBuildThreads) {
     const int c = cnt[s];
     if (c == 0) continue;
@@ -737,51 +765,52 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
       const int e = eoff[s] + k;
       if (e >= cap) break;
       int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords;
-      for (int w = 0; w < kPlanEntryWords; ++w) p[w] = 0;
-      p[kPlanSlot] = s;
-      p[kPlanRank] = m.ranks[s];
-      p[kPlanScale] = __float_as_int(sc);
-      p[kPlanRowCount] = min(kPlanRows, c - k * kPlanRows);
-      p[kPlanPos] = poff[s] + k * kPlanRows;
+      const int nr = min(kPlanRows, c - k * kPlanRows);
+      *reinterpret_cast<int4*>(p) = int4{s, rank_of[s], __float_as_int(sc), nr};
+      *reinterpret_cast<int4*>(p + 4) = int4{poff[s] + k * kPlanRows, 0, 0, 0};
+      *reinterpret_cast<int4*>(p + 24) = int4{0, 0, 0, 0};
+      *reinterpret_cast<int4*>(p + 28) = int4{0, 0, 0, 0};
     }
   }
-  // Rows: each thread walks the segments in order for its slots, so a
-  // slot's rows come out in row order.
-  for (int s = tid; s < ((ns + kBuildThreads - 1) / kBuildThreads) * kBuildThreads; s += kBuildThreads) {
-    const bool mine = s < ns && cnt[s] > 0;
-    int q = 0;
-    for (int b0 = 0; b0 < m.bs; b0 += kBuildSegs) {
+  // Pass 2 places the rows: segment i's rows follow the rows of the same
+  // slot in earlier segments (earlier passes: fill; this pass: a scan of the
+  // staged segments before it).
+  for (int pass = 0; pass < passes; ++pass) {
+    if (passes > 1) {
       __syncthreads();
-      for (int i = tid; i < kBuildSegs; i += kBuildThreads) {
-        int w = -1, st = 0, len = 0;
-        if (b0 + i < m.bs) seg_of(b0 + i, &w, &st, &len);
-        seg_slot[i] = w;
-        seg_start[i] = st;
-        seg_len[i] = len;
-      }
+      sg = stage(pass * kBuildSegs);
+      publish(sg);
       __syncthreads();
-      if (!mine) continue;
-      const int nseg = min(kBuildSegs, m.bs - b0);
-      for (int i = 0; i < nseg; ++i) {
-        if (seg_slot[i] != s) continue;
-        for (int r = 0; r < seg_len[i]; ++r, ++q) {
-          const int e = eoff[s] + q / kPlanRows;
-          if (e < cap)
-            plan[kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord + q % kPlanRows] =
-                seg_start[i] + r;
-        }
+    }
+    const int w = seg_w[tid];
+    if (w >= 0) {
+      int q = fill[w];
+      for (int j = 0; j < tid; ++j) q += seg_w[j] == w ? seg_n[j] : 0;
+      const int a0 = seg_a[tid];
+      const int n = seg_n[tid];
+      for (int r = 0; r < n; ++r, ++q) {
+        const int e = eoff[w] + q / kPlanRows;
+        if (e < cap) plan[kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord + q % kPlanRows] = a0 + r;
       }
     }
+    __syncthreads();
+    if (w >= 0) atomicAdd(&fill[w], seg_n[tid]);
   }
   __syncthreads();
   // Pad each entry's unused row words with its first row.  (Global writes
   // of this workgroup above are visible to it after the barrier: same CU.)
   __threadfence_block();
-  for (int e = tid; e < min(n_entries, cap); e += kBuildThreads) {
-    int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords;
-    const int nr = p[kPlanRowCount];
-    const int r0 = p[kPlanRowWord];
-    for (int i = nr; i < kPlanRows; ++i) p[kPlanRowWord + i] = r0;
+  for (int s = tid; s < ns; s += kBuildThreads) {
+    const int c = cnt[s];
+    for (int k = 0; k * kPlanRows < c; ++k) {
+      const int e = eoff[s] + k;
+      if (e >= cap) break;
+      const int nr = min(kPlanRows, c - k * kPlanRows);
+      if (nr == kPlanRows) continue;
+      int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord;
+      const int r0 = p[0];
+      for (int i = nr; i < kPlanRows; ++i) p[i] = r0;
+    }
   }
 }
 

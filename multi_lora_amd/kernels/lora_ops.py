@@ -257,6 +257,59 @@ def expand(mid: torch.Tensor, b_stacks: Sequence[torch.Tensor], meta: KernelInpu
 GROUPED_MAX_LEN = 16
 
 
+class _DevicePlan:
+    """A plan built on the device for a table that carries none, kept with the
+    table while its tensors stay the same objects at the same versions."""
+
+    __slots__ = ("key", "plan", "cap", "count_host", "ready")
+
+    def __init__(self, key, plan, cap, count_host, ready):
+        self.key, self.plan, self.cap, self.count_host, self.ready = key, plan, cap, count_host, ready
+
+
+def _table_key(meta: KernelInputMetaData, rows: int, num_slots: int):
+    """Identity of a table's contents as torch tracks them: each column's
+    object, address and in-place version counter; None when torch does not
+    track versions (inference tensors)."""
+    cols = (meta.seg_indptr, meta.weight_indices, meta.lora_ranks, meta.scalings)
+    try:
+        return (int(meta.bs), int(rows), int(num_slots)) + tuple((id(t), t.data_ptr(), t._version) for t in cols)
+    except RuntimeError:
+        return None
+
+
+def _device_plan(meta: KernelInputMetaData, m: "_ffi.SegMeta", rows: int, dev: torch.device) -> None:
+    """Give a plan-less table a plan built on the device once, outside graph
+    capture, and reuse it while the table is unchanged (torch bumps a
+    tensor's version on every in-place write).  The entry count is copied to
+    pinned host memory without a wait and sizes the grid once it has
+    arrived.  Under capture, or for tables whose versions torch does not
+    track, the library builds the plan into the workspace for every call,
+    so a replayed graph follows in-place rewrites."""
+    if m.num_slots > _ffi.PLAN_BUILD_MAX_SLOTS or torch.cuda.is_current_stream_capturing():
+        return
+    key = _table_key(meta, rows, m.num_slots)
+    if key is None:
+        return
+    cached = getattr(meta, "_device_plan", None)
+    if cached is None or cached.key != key:
+        lib = _ffi.lib()
+        cap = max(1, int(rows))
+        plan = torch.empty(lib.mlora_plan_bytes(cap) // 4, dtype=torch.int32, device=dev)
+        built = _ffi.SegMeta.from_buffer_copy(m)
+        built.plan, built.plan_cap, built.plan_entries = None, 0, -1
+        _ffi.check(lib.mlora_build_plan(ctypes.byref(built), int(rows), plan.data_ptr(), cap, _ffi.stream_ptr(dev)),
+                   "mlora_build_plan")
+        count_host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        count_host.copy_(plan[:1], non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(dev))
+        cached = _DevicePlan(key, plan, cap, count_host, ready)
+        meta._device_plan = cached
+    m.plan, m.plan_cap = cached.plan.data_ptr(), cached.cap
+    m.plan_entries = int(cached.count_host[0]) if cached.ready.query() else -1
+
+
 def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],
                   meta: KernelInputMetaData, out: torch.Tensor, out_cols: Sequence[int],
                   workspace: Optional[LinkedWorkspace] = None, phases: int = 3, mode: int = 0) -> bool:
@@ -290,6 +343,8 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
     lib = _ffi.lib()
     dt = _ffi.dtype_code(x.dtype)
     m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
+    if m.plan is None:
+        _device_plan(meta, m, x.shape[0], dev)
     key = (in_dim, r_max, n, x.shape[0], m.num_slots, dt, int(mode))
     need = _GROUPED_WS_BYTES.get(key)
     if need is None:

@@ -207,6 +207,34 @@ def test_host_and_device_plans_give_the_same_bits(dev):
         assert torch.equal(grouped(wl, mode=mode), grouped(wl, mode=mode, meta=bare))
 
 
+def test_device_plan_kept_with_the_table_follows_in_place_rewrites(dev):
+    """A table without a plan gets one built on the device once and kept
+    while its tensors are unchanged; an in-place rewrite of a column (torch
+    bumps its version) makes the next call build a new one.  Every call
+    equals the same call with a host-built plan, bit for bit."""
+    wl = synthetic.decode_q(device=dev, tokens=64, in_dim=1024, out=512, n_slots=16, n_adapters=9, rank=16, seed=83)
+    bare = make_meta(wl.seg_lens, wl.seg_slots, wl.slot_ranks, wl.scalings, dev, torch.bfloat16,
+                     host_copies=False, with_plan=False)
+    lws = LinkedWorkspace()
+    for mode in (1, 2):
+        assert torch.equal(grouped(wl, mode=mode, lws=lws, meta=bare), grouped(wl, mode=mode))
+    first = bare._device_plan
+    assert torch.equal(grouped(wl, mode=1, lws=lws, meta=bare), grouped(wl, mode=1))
+    assert bare._device_plan is first
+    torch.cuda.synchronize()
+    assert first.ready.query() and int(first.count_host[0]) == wl.meta.plan_entries
+    # Rewrite the slots in place: rows move to other adapters.
+    new_slots = [(s + 3) % 9 for s in wl.seg_slots]
+    bare.weight_indices.copy_(torch.tensor(new_slots, dtype=torch.int32))
+    moved = synthetic.LoRAWorkload(**{**wl.__dict__, "seg_slots": new_slots,
+                                      "meta": make_meta(wl.seg_lens, new_slots, wl.slot_ranks, wl.scalings, dev,
+                                                        torch.bfloat16)})
+    got = grouped(wl, mode=1, lws=lws, meta=bare)
+    assert bare._device_plan is not first
+    assert torch.equal(got, grouped(moved, mode=1))
+    assert counters(lws)[1] == 0
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_device_plan_builder_matches_host_and_oracle(dev, seed):
     g = torch.Generator().manual_seed(100 + seed)

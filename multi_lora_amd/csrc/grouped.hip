@@ -286,39 +286,51 @@ __device__ int short_slot(const unsigned* bits, const int* offs, int nwords, int
 // rows of a long-segment tile, 32 (expand_kernel's register-prefetched
 // tile) or 64 (expand_dma_kernel's tile streamed through LDS; y from mid
 // only).  A workgroup runs units of one kind, so the kinds share one LDS
-// area.  Unit order (each unit is n_tiles workgroups, the column tile
-// fastest): the short units first, or (interleave) long and short units
-// alternating while both last, then the rest.
+// area.  A long unit is ea.n_tiles workgroups (256-column tiles), a short
+// unit ga.n_tiles (WS * 256-column tiles), the column fastest.
+// Unit order: the short units first, or (interleave) a short and a long
+// unit alternating while both last, then the rest.
 template <class T, bool FUSED, int RS, int LBM>
-__global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, GroupedArgs ga, int long_units,
+__global__ __launch_bounds__(256, RS == 1 ? 3 : 4) void expand_mixed_kernel(ExpandArgs ea, GroupedArgs ga, int long_units,
                                                               int short_units, int interleave) {
   constexpr bool STREAMED = LBM == kExpandStreamBM;
+  constexpr int WS = RS == 1 ? kMixedShortWn : 1;  // wider short items fit the registers at one K-step
   static_assert(LBM == kExpandLongBM || (STREAMED && !FUSED), "32-row tiles, or 64-row streamed ones from mid");
   using TileLds = ExpandTileLds<T, kExpandLongBM, FUSED>;
   constexpr int kLongBytes = STREAMED ? expand_dma_lds_bytes<LBM>() : static_cast<int>(sizeof(TileLds));
-  constexpr int kShortBytes = static_cast<int>(sizeof(ExpandLds<T, 1>));
+  constexpr int kShortBytes = static_cast<int>(sizeof(ExpandLds<T, WS>));
   __shared__ __attribute__((aligned(1024))) unsigned char area[kLongBytes > kShortBytes ? kLongBytes : kShortBytes];
   __shared__ unsigned bits[kMixedMaxSlots / 32];
   __shared__ int offs[kMixedMaxSlots / 32];
   __shared__ int pick;
   const int nt = ea.n_tiles;
-  const int v = blockIdx.x / nt;
-  const int nt_g = blockIdx.x - v * nt;
-  bool is_short;
-  int idx;
+  const int ns = ga.n_tiles;
+  const int b = blockIdx.x;
   const int m = interleave ? min(long_units, short_units) : 0;
-  if (v < 2 * m) {
-    is_short = v & 1;
-    idx = v >> 1;
-  } else if (interleave) {
-    is_short = short_units > long_units;
-    idx = v - m;
+  bool is_short;
+  int idx, nt_g;
+  if (b < m * (ns + nt)) {
+    const int pair = b / (ns + nt);
+    const int off = b - pair * (ns + nt);
+    is_short = off < ns;
+    idx = pair;
+    nt_g = is_short ? off : off - ns;
   } else {
-    is_short = v < short_units;
-    idx = is_short ? v : v - short_units;
+    int rb = b - m * (ns + nt);
+    if (interleave)
+      is_short = short_units > long_units;
+    else if (rb < short_units * ns)
+      is_short = true;
+    else {
+      is_short = false;
+      rb -= short_units * ns;
+    }
+    const int w = is_short ? ns : nt;
+    idx = m + rb / w;
+    nt_g = rb - (rb / w) * w;
   }
   if (is_short) {
-    auto& gl = *reinterpret_cast<ExpandLds<T, 1>*>(area);
+    auto& gl = *reinterpret_cast<ExpandLds<T, WS>*>(area);
     const int j = idx;
     const int n_short = short_slot_map(ga, bits, offs, gl.tmp);
     const int nwords = (ga.meta.num_slots + 31) >> 5;
@@ -328,7 +340,7 @@ __global__ __launch_bounds__(256, 4) void expand_mixed_kernel(ExpandArgs ea, Gro
     // j + 2 short_units, ...
     for (int k = j; k < n_short; k += short_units) {
       const int slot = short_slot(bits, offs, nwords, k, &pick);
-      expand_item<T, FUSED ? kSumF32 : kSumMid, 1, RS>(ga, slot, nt_g, gl);
+      expand_item<T, FUSED ? kSumF32 : kSumMid, WS, RS>(ga, slot, nt_g, gl);
       __syncthreads();
     }
     return;
@@ -375,9 +387,21 @@ int64_t mixed_long_units(int64_t long_rows, int long_segs) {
   return std::max<int64_t>(1, (long_rows + static_cast<int64_t>(LBM - 1) * long_segs) / LBM);
 }
 
+// The short items' column tiles: `wn` 256-column tiles of one slice each.
+void set_short_tiles(const ExpandArgs& ea, int wn, GroupedArgs* ga) {
+  ga->tile_base[0] = 0;
+  for (int s = 0; s < kMaxSlices; ++s)
+    ga->tile_base[s + 1] = ga->tile_base[s] + (s < ea.n_slices ? cdiv(ea.slices[s].out_dim, kExpandBN * wn) : 0);
+  ga->n_tiles = ga->tile_base[ea.n_slices];
+  ga->expand_wn = wn;
+}
+
 template <class T, bool FUSED, int LBM>
-hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int64_t long_rows, int long_segs,
+hipError_t launch_mixed_t(const ExpandArgs& ea, GroupedArgs ga, int64_t long_rows, int long_segs,
                           int short_units, int cus, hipStream_t stream) {
+  // One K-step (r_max <= 32): short items of kMixedShortWn tiles (c5 gate|up
+  // 38.3 vs 39.3 us for the expand); two: one tile, as the registers allow.
+  set_short_tiles(ea, ga.r_max <= T::KSTEP ? kMixedShortWn : 1, &ga);
   const int64_t lu = mixed_long_units<LBM>(long_rows, long_segs);
   if (lu > INT32_MAX) return hipErrorInvalidConfiguration;
   const int long_units = static_cast<int>(lu);
@@ -389,9 +413,9 @@ hipError_t launch_mixed_t(const ExpandArgs& ea, const GroupedArgs& ga, int64_t l
   // (c5 gate|up: 3136 short items, 49.7 vs 51.3 us), and each short unit
   // takes two slots one after the other, which halves the workgroups that
   // wait on their table scans (48.2 vs 49.4 us; three slots a unit: 48.5).
-  const int interleave = static_cast<int64_t>(short_units) * ea.n_tiles > 4 * static_cast<int64_t>(cus) ? 1 : 0;
+  const int interleave = static_cast<int64_t>(short_units) * ga.n_tiles > 4 * static_cast<int64_t>(cus) ? 1 : 0;
   if (interleave) short_units = (short_units + 1) / 2;
-  const int64_t blocks = (static_cast<int64_t>(long_units) + short_units) * ea.n_tiles;
+  const int64_t blocks = static_cast<int64_t>(long_units) * ea.n_tiles + static_cast<int64_t>(short_units) * ga.n_tiles;
   if (blocks <= 0) return hipSuccess;
   if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   if (ga.r_max <= T::KSTEP)
@@ -430,9 +454,6 @@ hipError_t launch_mixed(const ExpandArgs& args, int dtype, int64_t long_rows, in
   ga.meta = args.meta;
   ga.partials = const_cast<float*>(args.partials);
   ga.kc = args.ks > 1 ? args.ks : 1;
-  ga.n_tiles = args.n_tiles;
-  for (int s = 0; s <= kMaxSlices; ++s) ga.tile_base[s] = args.tile_base[s];
-  ga.expand_wn = 1;
   ga.short_only = 1;
   ga.mid = args.mid;
   ga.mid_stride = args.mid_stride;

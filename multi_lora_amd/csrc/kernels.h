@@ -217,6 +217,8 @@ hipError_t launch_build_plan(const SegView& m, int rows, int32_t* plan, int cap,
 constexpr int kShortSegRows = 16;
 // Pools of up to this many slots (a bitmap of 32-bit words in LDS).
 constexpr int kMixedMaxSlots = 2048;
+// 256-column tiles a short item of the mixed expand covers.
+constexpr int kMixedShortWn = 2;
 // One launch for a batch mixing long and short segments: units
 // [0, short_units * n_tiles) are slot-grouped items (distinct slot of the
 // short segments, in slot order; 256-column tile), which read each adapter's

@@ -694,17 +694,20 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
   __shared__ int eoff[kPlanBuildMaxSlots];  // first entry of each slot
   __shared__ int poff[kPlanBuildMaxSlots];  // first row position of each slot
   __shared__ int rank_of[kPlanBuildMaxSlots];
-  __shared__ int seg_w[kBuildSegs];         // live slot of the pass's segments (-1: none)
+  __shared__ float scal_of[kPlanBuildMaxSlots];
+  __shared__ __attribute__((aligned(16))) int seg_w[kBuildSegs];  // live slot of the pass's segments (-1: none)
   __shared__ int seg_a[kBuildSegs];
-  __shared__ int seg_n[kBuildSegs];
+  __shared__ __attribute__((aligned(16))) int seg_n[kBuildSegs];
   __shared__ int tmp[kBuildThreads / kWave];
   __shared__ int run[2];
   const int tid = threadIdx.x;
   const int ns = m.num_slots;
   const int passes = (m.bs + kBuildSegs - 1) / kBuildSegs;
-  // Ranks of every slot and the first pass of segments, requested at once.
+  // Ranks and scalings of every slot and the first pass of segments,
+  // requested at once.
   for (int s = tid; s < ns; s += kBuildThreads) {
     rank_of[s] = m.ranks[s];
+    scal_of[s] = load_scaling(m.scalings, s, m.scal_dtype);
     cnt[s] = 0;
     fill[s] = 0;
   }
@@ -760,7 +763,7 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
   for (int s = tid; s < ns; s += kBuildThreads) {
     const int c = cnt[s];
     if (c == 0) continue;
-    const float sc = load_scaling(m.scalings, s, m.scal_dtype);
+    const float sc = scal_of[s];
     for (int k = 0; k * kPlanRows < c; ++k) {
       const int e = eoff[s] + k;
       if (e >= cap) break;
@@ -774,7 +777,8 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
   }
   // Pass 2 places the rows: segment i's rows follow the rows of the same
   // slot in earlier segments (earlier passes: fill; this pass: a scan of the
-  // staged segments before it).
+  // staged segments before it).  The thread that places an entry's first
+  // row also fills the entry's unused row words with it.
   for (int pass = 0; pass < passes; ++pass) {
     if (passes > 1) {
       __syncthreads();
@@ -783,34 +787,43 @@ __global__ __launch_bounds__(kBuildThreads) void build_plan_kernel(SegView m, in
       __syncthreads();
     }
     const int w = seg_w[tid];
+    // Rows of slot w in this pass's segments before this one: a wave-uniform
+    // loop (eight segments a step, read as 16-byte words) up to the wave's
+    // last segment of the pass, counting those before this thread's.
+    int before = 0;
+    const int in_pass = min(m.bs - pass * kBuildSegs, kBuildSegs);
+    const int wave0 = tid & ~(kWave - 1);
+    const int lim = wave0 < in_pass ? min(wave0 + kWave, (in_pass + 7) & ~7) : 0;
+    for (int j0 = 0; j0 < lim; j0 += 8) {
+      const int4 wa = *reinterpret_cast<const int4*>(seg_w + j0);
+      const int4 wb = *reinterpret_cast<const int4*>(seg_w + j0 + 4);
+      const int4 na = *reinterpret_cast<const int4*>(seg_n + j0);
+      const int4 nb = *reinterpret_cast<const int4*>(seg_n + j0 + 4);
+      before += (j0 + 0 < tid && wa.x == w) ? na.x : 0;
+      before += (j0 + 1 < tid && wa.y == w) ? na.y : 0;
+      before += (j0 + 2 < tid && wa.z == w) ? na.z : 0;
+      before += (j0 + 3 < tid && wa.w == w) ? na.w : 0;
+      before += (j0 + 4 < tid && wb.x == w) ? nb.x : 0;
+      before += (j0 + 5 < tid && wb.y == w) ? nb.y : 0;
+      before += (j0 + 6 < tid && wb.z == w) ? nb.z : 0;
+      before += (j0 + 7 < tid && wb.w == w) ? nb.w : 0;
+    }
     if (w >= 0) {
-      int q = fill[w];
-      for (int j = 0; j < tid; ++j) q += seg_w[j] == w ? seg_n[j] : 0;
+      int q = fill[w] + before;
       const int a0 = seg_a[tid];
       const int n = seg_n[tid];
+      const int c = cnt[w];
       for (int r = 0; r < n; ++r, ++q) {
         const int e = eoff[w] + q / kPlanRows;
-        if (e < cap) plan[kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord + q % kPlanRows] = a0 + r;
+        if (e >= cap) continue;
+        int32_t* rw = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord;
+        rw[q % kPlanRows] = a0 + r;
+        if (q % kPlanRows == 0)
+          for (int i = min(kPlanRows, c - q); i < kPlanRows; ++i) rw[i] = a0 + r;
       }
     }
     __syncthreads();
     if (w >= 0) atomicAdd(&fill[w], seg_n[tid]);
-  }
-  __syncthreads();
-  // Pad each entry's unused row words with its first row.  (Global writes
-  // of this workgroup above are visible to it after the barrier: same CU.)
-  __threadfence_block();
-  for (int s = tid; s < ns; s += kBuildThreads) {
-    const int c = cnt[s];
-    for (int k = 0; k * kPlanRows < c; ++k) {
-      const int e = eoff[s] + k;
-      if (e >= cap) break;
-      const int nr = min(kPlanRows, c - k * kPlanRows);
-      if (nr == kPlanRows) continue;
-      int32_t* p = plan + kPlanHeaderWords + static_cast<int64_t>(e) * kPlanEntryWords + kPlanRowWord;
-      const int r0 = p[0];
-      for (int i = nr; i < kPlanRows; ++i) p[i] = r0;
-    }
   }
 }
 

@@ -177,7 +177,12 @@ __device__ __forceinline__ int64_t sum_index(const DecodeArgs& a, int pos, int c
 // the workspace by wave 0 for the entry's rows, then (flag != 0) the chunk's
 // flag once the sums are acknowledged.  xrow: this lane's x row (row
 // lane & 15 of the entry).  All threads call it; it ends with an LDS barrier.
-template <class T, int NBT, int SP>
+// LEAN: one A block's fragments in flight at a time instead of all NBT (the
+// same products in the same order, so the same sums), for the expand items'
+// rare recompute when it has four A blocks and one expand K-step, so that
+// the single launch keeps four workgroups a CU without spilling (q|k|v at
+// rank 16: 12.6 vs 14.0 us at 64 tokens, 19.2 vs 20.9 at 256).
+template <class T, int NBT, int SP, bool LEAN = false>
 __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xrow, int sg, int c,
                              f32x4 (*red)[kWave], uint64_t flag) {
   using raw = typename T::raw_t;
@@ -198,36 +203,71 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
   // where the MFMA uses them, so nothing between here and the x loads waits
   // for them.  in_dim is a multiple of the chunk: a chunk is wholly inside
   // or wholly outside.
-  u32x4 af[SP][NBT];
-#pragma unroll
-  for (int j = 0; j < NBT; ++j) {
+  auto a_row = [&](int j) {
     const int jj = j < nbt ? j : 0;
     const int sl = jj / nb_act;  // slice within the group
-    const raw* arow = slice_a<raw>(a.slices, s_first + sl, en.slot, min((jj - sl * nb_act) * 16 + r16, rank - 1));
+    return slice_a<raw>(a.slices, s_first + sl, en.slot, min((jj - sl * nb_act) * 16 + r16, rank - 1));
+  };
+  auto x_frags = [&](u32x4 (&xv)[SP]) {
+    const raw* xr = static_cast<const raw*>(a.x) + static_cast<int64_t>(xrow) * a.x_stride;
 #pragma unroll
     for (int sp = 0; sp < SP; ++sp) {
       const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
-      af[sp][j] = ld_chunk(arow + (kk < a.in_dim ? kk : 0));
+      const u32x4 v = ld_chunk(xr + (kk < a.in_dim ? kk : 0));
+      xv[sp] = kk < a.in_dim ? v : zero_chunk();
     }
-  }
-  const raw* xr = static_cast<const raw*>(a.x) + static_cast<int64_t>(xrow) * a.x_stride;
-  u32x4 xv[SP];
-#pragma unroll
-  for (int sp = 0; sp < SP; ++sp) {
-    const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
-    const u32x4 v = ld_chunk(xr + (kk < a.in_dim ? kk : 0));
-    xv[sp] = kk < a.in_dim ? v : zero_chunk();
-  }
-  fence_regs(af);
+  };
   f32x4 acc[NBT];
 #pragma unroll
   for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (!LEAN) {
+    u32x4 af[SP][NBT];
 #pragma unroll
-  for (int sp = 0; sp < SP; ++sp) {
-    const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+    for (int j = 0; j < NBT; ++j) {
+      const int jj = j < nbt ? j : 0;
+      const int sl = jj / nb_act;  // slice within the group
+      const raw* arow = slice_a<raw>(a.slices, s_first + sl, en.slot, min((jj - sl * nb_act) * 16 + r16, rank - 1));
 #pragma unroll
-    for (int j = 0; j < NBT; ++j)
-      if (j < nbt) acc[j] = T::mma(acc[j], kk < a.in_dim ? af[sp][j] : zero_chunk(), xv[sp]);
+      for (int sp = 0; sp < SP; ++sp) {
+        const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+        af[sp][j] = ld_chunk(arow + (kk < a.in_dim ? kk : 0));
+      }
+    }
+    const raw* xr = static_cast<const raw*>(a.x) + static_cast<int64_t>(xrow) * a.x_stride;
+    u32x4 xv[SP];
+#pragma unroll
+    for (int sp = 0; sp < SP; ++sp) {
+      const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+      const u32x4 v = ld_chunk(xr + (kk < a.in_dim ? kk : 0));
+      xv[sp] = kk < a.in_dim ? v : zero_chunk();
+    }
+    fence_regs(af);
+#pragma unroll
+    for (int sp = 0; sp < SP; ++sp) {
+      const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+#pragma unroll
+      for (int j = 0; j < NBT; ++j)
+        if (j < nbt) acc[j] = T::mma(acc[j], kk < a.in_dim ? af[sp][j] : zero_chunk(), xv[sp]);
+    }
+  } else {
+    u32x4 xv[SP];
+    x_frags(xv);
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) {
+      if (j >= nbt) break;
+      const raw* arow = a_row(j);
+      u32x4 af[SP];
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp) {
+        const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+        af[sp] = ld_chunk(arow + (kk < a.in_dim ? kk : 0));
+      }
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp) {
+        const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+        acc[j] = T::mma(acc[j], kk < a.in_dim ? af[sp] : zero_chunk(), xv[sp]);
+      }
+    }
   }
   MLORA_STAMP_AFTER_LOADS(2);
   if (wave > 0) {
@@ -438,7 +478,7 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
       while (miss != 0) {
         const int z = __builtin_ctzll(miss);
         miss &= miss - 1;
-        shrink_chunk<T, NBT, SP>(a, e, en, xrow, sg, z, red, want);
+        shrink_chunk<T, NBT, SP, (NBT >= 4 && RS == 1)>(a, e, en, xrow, sg, z, red, want);
       }
       // The prefetched B fragments and output rows are requested again, so
       // they hold no registers across the computation above (a rare path).
@@ -583,7 +623,7 @@ __device__ void expand_items(const int32_t* plan, const DecodeArgs& a, int j, in
 // words and the plan's entry count are requested at once, together with
 // every cache line of the other arguments.
 template <class T, int NBT, int WN, int RS, int SCHED>
-__global__ __launch_bounds__(256, NBT >= 8 ? 2 : (NBT >= 4 && SCHED == kGroupLinked) ? 3 : 4) void planned_kernel(const int32_t* __restrict__ plan,
+__global__ __launch_bounds__(256, NBT >= 8 ? 2 : (NBT >= 4 && SCHED == kGroupLinked && RS == 2) ? 3 : 4) void planned_kernel(const int32_t* __restrict__ plan,
                                                                        int plan_cap, int n_shrink, DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
   __shared__ f32x4 red[3 * NBT][kWave];

@@ -105,6 +105,27 @@ def test_schedules_are_bit_identical(dev):
     assert fb > 0 and pe == 0
 
 
+@pytest.mark.parametrize("outs,rank", [([1024, 256, 256], 16), ([768, 768], 32), ([512, 256, 256, 128], 16)])
+def test_four_block_forced_fallback_equals_handoff(dev, outs, rank):
+    """Four 16-row A blocks per shrink item with one expand K-step (q|k|v at
+    rank 16, gate|up at rank 32, four slices at rank 16): the expand items'
+    recompute of a missing chunk runs one A block at a time there, and must
+    give the chunk sums the shrink items hand over, bit for bit."""
+    g = torch.Generator().manual_seed(rank + len(outs))
+    n_slots, rows = 24, 96
+    slots = torch.randint(0, n_slots, (rows,), generator=g).tolist()
+    ranks = [rank] * n_slots
+    ranks[5] = 0
+    wl = workload("four_blocks", dev, [1] * rows, slots, ranks, [1.5] * n_slots, 2048, outs, rank, 40 + rank)
+    ref = check(wl, mode=1)
+    lws = LinkedWorkspace()
+    grouped(wl, mode=1, lws=lws)
+    lws.set_wait_ticks(-1)
+    assert torch.equal(grouped(wl, mode=1, lws=lws), ref)
+    fb, pe = counters(lws)
+    assert fb > 0 and pe == 0
+
+
 @pytest.mark.parametrize("mode", [0, 2])
 def test_decode_qkv_three_slices(dev, mode):
     check(synthetic.decode_qkv(device=dev), mode=mode)

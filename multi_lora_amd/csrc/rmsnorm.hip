@@ -76,6 +76,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     const int c = li + j * tpr;
     cache[j] = load_row_chunk<T, AL>(xrow, c * VEC, (row_ok && c < nch) ? hidden - c * VEC : 0);
   }
+  // The weight chunks go out with the row's, before the add waits for them
+  // (fused add + RMSNorm at 1088 x 4096: 9.9 vs 10.2 us).
+#pragma unroll
+  for (int j = 0; j < NC; ++j) weight_chunk<T, WV>(a, li + j * tpr, wf[j]);
   if constexpr (ADD) {
     u32x4 res[NC];
 #pragma unroll
@@ -90,8 +94,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
       if (row_ok && c < nch) store_row_chunk<T, AL>(rrow + c * VEC, cache[j], hidden - c * VEC);
     }
   }
-#pragma unroll
-  for (int j = 0; j < NC; ++j) weight_chunk<T, WV>(a, li + j * tpr, wf[j]);
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; ++j)

@@ -162,3 +162,45 @@ def test_fused_norms_equal_the_torch_norms(dev, dtype, atol):
         got = fused.forward_mixed(ids, nxt, StaticKV(cfg, 3, 8, "cuda", dtype), pos)
         want = plain.forward_mixed(ids, nxt, StaticKV(cfg, 3, 8, "cuda", dtype), pos)
     torch.testing.assert_close(got.float(), want.float(), atol=atol, rtol=atol)
+
+
+@pytest.mark.parametrize("dtype,atol", [(torch.float32, 2e-4), (torch.bfloat16, 6e-2)])
+def test_mixed_step_matches_oracle_backend(dev, dtype, atol):
+    """The 32-layer benchmark's packed step on the small model, configured as
+    the benchmark configures it (q|k|v and gate|up fused on every shape, one
+    multi-slice LoRA call each; the manager's HIP norms): its logits against
+    the same model whose LoRA deltas come from the oracle's per-segment
+    PyTorch backend (oracle/lora_ref.py, restating
+    multi_lora/backend/torch_backend.py:17-90), layer by layer through the
+    whole forward."""
+    from multi_lora_amd import fuse_gate_up_projections, fuse_qkv_projections
+    from multi_lora_amd.decoder import StaticKV
+    from oracle.lora_ref import TorchLoRABackend
+
+    mgr, cfg = build(dtype)
+    layers = cfg.num_hidden_layers
+    assert fuse_qkv_projections(mgr.lora_wrappers, all_shapes=True) == layers
+    assert fuse_gate_up_projections(mgr.lora_wrappers) == layers
+    g = torch.Generator().manual_seed(9)
+    prompts = torch.randint(0, cfg.vocab_size, (2, 6), generator=g).to("cuda")
+    nxt = torch.randint(0, cfg.vocab_size, (3, 1), generator=g).to("cuda")
+    pos = torch.tensor([4], device="cuda")
+    names = ["a", "b", "b", None, "a"]
+
+    def step(names=names):
+        mgr._setup_forward_batch(names, seq_lens=[6, 6, 1, 1, 1])
+        with torch.inference_mode():
+            return mgr.model.forward_mixed(prompts, nxt, StaticKV(cfg, 3, 8, "cuda", dtype), pos).float()
+
+    got = step()
+    hip_backend = mgr._lora_backend
+    mgr._lora_backend = TorchLoRABackend()
+    try:
+        want = step()
+    finally:
+        mgr._lora_backend = hip_backend
+    torch.testing.assert_close(got, want, atol=atol, rtol=atol)
+    mgr._lora_backend = hip_backend
+    assert torch.equal(step(), got)  # the HIP step again, bit for bit
+    if dtype == torch.float32:  # the deltas move the logits far beyond the tolerance
+        assert (got - step([None] * 5)).abs().max() > 50 * atol

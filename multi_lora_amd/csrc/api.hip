@@ -95,11 +95,13 @@ size_t mid_region_bytes(int32_t rows, int32_t n_slices, int32_t r_max, int32_t d
 }
 
 // Shrink; with skip_reduce the split sums stay in the workspace for the
-// expand (no reduce launch).
+// expand (no reduce launch).  private_mid: only the apply path's expand
+// reads mid, so the split reduce may fill every row and column of it
+// (values the expand never reads included) without looking up the table.
 int shrink_impl(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim, const mlora_slice* slices,
                 int32_t n_slices, int32_t r_max, int32_t rank_mult, void* mid, int64_t mid_row_stride,
                 const mlora_seg_meta* meta, int32_t dtype, void* workspace, size_t workspace_bytes, bool skip_reduce,
-                void* stream) {
+                bool private_mid, void* stream) {
   if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
   if (int rc = check_meta(meta)) return rc;
   if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
@@ -144,6 +146,7 @@ int shrink_impl(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t i
   args.meta = seg_view(meta);
   args.partials = static_cast<float*>(workspace);
   args.skip_reduce = skip_reduce ? 1 : 0;
+  args.row_reduce = private_mid ? 1 : 0;
   hipError_t e = mlora::launch_shrink(plan, args, dtype, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "shrink launch");
   return 0;
@@ -241,7 +244,7 @@ int mlora_shrink(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t 
                  void* stream) {
   g_err[0] = '\0';
   return shrink_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, rank_mult, mid, mid_row_stride, meta,
-                     dtype, workspace, workspace_bytes, false, stream);
+                     dtype, workspace, workspace_bytes, false, false, stream);
 }
 
 int mlora_expand(const void* mid, int64_t mid_row_stride, int32_t num_rows, const mlora_slice* slices, int32_t n_slices,
@@ -296,7 +299,7 @@ int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, 
   char* ws = static_cast<char*>(workspace);
   const int64_t mid_stride = static_cast<int64_t>(n_slices) * r_max;
   int rc = shrink_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, 1, ws, mid_stride, meta, dtype,
-                       ws + mid_bytes, plan.ws_bytes, fused, stream);
+                       ws + mid_bytes, plan.ws_bytes, fused, true, stream);
   if (rc != 0) return rc;
   return expand_impl(ws, mid_stride, num_rows, slices, n_slices, r_max, out, out_row_stride, meta, dtype,
                      fused ? reinterpret_cast<const float*>(ws + mid_bytes) : nullptr, fused ? plan.ks : 0, stream);

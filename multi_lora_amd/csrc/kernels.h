@@ -43,6 +43,7 @@ struct ShrinkArgs {
   float* partials;  // ks > 1: [ks][rows][part_cols] fp32 split sums (this launch's columns first)
   int part_cols;    // row width of the split sums: n_slices * r_max of the whole call
   int skip_reduce;  // ks > 1: leave the split sums for the expand (no reduce launch)
+  int row_reduce;   // ks > 1, mid private to the apply path: reduce every row and column, no table lookup
 };
 
 struct ShrinkPlan {

@@ -70,6 +70,44 @@ def test_one_call_equals_two_calls(dev, name, lens, slots, ranks, in_dim, outs, 
     assert_tol_f64(one.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), name)
 
 
+@pytest.mark.parametrize("name,lens,slots,ranks,in_dim,outs,r_max,dtype", [
+    # split K with an output too wide for the expand to add the split sums:
+    # the split reduce fills the call's own mid over every row and column
+    ("wide_mixed", [70] + [1] * 30 + [130], [0] + [i % 5 for i in range(30)] + [3], [32, 16, 0, 9, 32], 4096,
+     [4096, 512], 32, torch.bfloat16),
+    # long segments (the streamed expand reads mid), a rank-0 slot, an empty
+    # segment, ranks below r_max
+    ("long_ranks", [150, 200, 0, 130, 90], [0, 1, 2, 3, 1], [16, 0, 48, 64], 8192, [1024, 256], 64,
+     torch.float16),
+])
+@pytest.mark.parametrize("fill", [0xFF, 0x7F])
+def test_apply_ignores_what_the_workspace_held(dev, name, lens, slots, ranks, in_dim, outs, r_max, dtype, fill):
+    """The apply path's split reduce writes its private mid over every row and
+    column, stale split sums included (rank-0 rows, columns past a rank,
+    rows no segment covers).  With the workspace's bytes set beforehand to
+    0xFF (fp32 NaN) or 0x7F (3.4e38, whose sums overflow), the output equals
+    the zeroed workspace's and the two-call path's bit for bit, and the rows
+    past the table keep their base values."""
+    extra = 7
+    x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens + [extra], slots + [0], ranks, in_dim, outs, r_max, dtype,
+                                                 len(name))
+    meta = make_meta(lens, slots, ranks, scal, dev, dtype)
+    meta_cpu = make_meta(lens, slots, ranks, scal, "cpu", dtype)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    zeroed = base.to(dev).clone()
+    apply_segments(xd, Ad, Bd, meta, zeroed, cols, workspace=Workspace())
+    stale_ws = Workspace()
+    stale_ws.buf = torch.full((64 << 20,), fill, dtype=torch.uint8, device=dev)
+    stale = base.to(dev).clone()
+    apply_segments(xd, Ad, Bd, meta, stale, cols, workspace=stale_ws)
+    torch.cuda.synchronize()
+    assert torch.equal(stale.cpu(), zeroed.cpu()), f"{name}: the workspace's old bytes reached the output"
+    _, two = run_hip(xd, Ad, Bd, meta, base.to(dev), cols)
+    assert torch.equal(zeroed.cpu(), two), f"{name}: one-call result differs from shrink + expand"
+    assert torch.equal(stale.cpu()[sum(lens):], base[sum(lens):]), f"{name}: rows past the table changed"
+    assert_tol_f64(stale.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), name)
+
+
 @pytest.mark.parametrize("r_max", [4, 12])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_backend_decode_at_rank_widths_the_grouped_path_refuses(dev, r_max, dtype):

@@ -208,6 +208,7 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
   args.out_stride = out_row_stride;
   args.meta = seg_view(meta);
   args.m_tiles = mlora::cdiv(meta->max_len > 0 ? meta->max_len : 1, bm);
+  args.cus = num_cus();
   args.n_tiles = tiles;
   args.partials = partials;
   args.ks = ks;

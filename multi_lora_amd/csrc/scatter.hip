@@ -13,7 +13,9 @@
 // of its B block.  A is a straight copy in 16-byte chunks; B is copied one
 // rank-wide row piece at a time, in 16-byte chunks when the rank and the row
 // stride allow.  Pure data movement: the bound is HBM bandwidth (each element
-// read once from the stage and written once to the pool).
+// read once from the stage and written once to the pool), so the 16-byte
+// copies carry the non-temporal hint (the Llama-3-8B bank of 4 adapters:
+// 137.4 -> 135.4 us).
 #include "kernels.h"
 #include "loads.h"
 
@@ -27,7 +29,7 @@ __device__ __forceinline__ void copy_run(const R* src, R* dst, int64_t n0, int64
   constexpr int V = 16 / sizeof(R);
   if (vec) {
     for (int64_t e = n0 + static_cast<int64_t>(threadIdx.x) * V; e < n1; e += static_cast<int64_t>(blockDim.x) * V)
-      *reinterpret_cast<u32x4*>(dst + e) = *reinterpret_cast<const u32x4*>(src + e);
+      st_chunk_nt(dst + e, ld_chunk_nt(src + e));
   } else {
     for (int64_t e = n0 + threadIdx.x; e < n1; e += blockDim.x) dst[e] = src[e];
   }
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(256) void scatter_kernel(ScatterArgs a) {
       for (int64_t q = e0 / V + threadIdx.x; q < e1 / V; q += blockDim.x) {
         const int64_t o = q / per_row;
         const int64_t c = (q - o * per_row) * V;
-        *reinterpret_cast<u32x4*>(dst + o * k.b_row_stride + c) = *reinterpret_cast<const u32x4*>(src + q * V);
+        st_chunk_nt(dst + o * k.b_row_stride + c, ld_chunk_nt(src + q * V));
       }
     } else {
       for (int64_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {

@@ -91,7 +91,7 @@ hipError_t launch_streamed(ExpandArgs args, hipStream_t stream) {
   // workgroups): prefill gate|up (7728 tiles) expand 106.2 -> 97.8 us.  In a
   // launch of about one round the hint costs: prefill down (1104 tiles)
   // 17.3 -> 20.1 us.
-  if (blocks >= static_cast<int64_t>(kStreamNtTilesPerCu) * args.cus)
+  if (args.cus > 0 && blocks >= static_cast<int64_t>(kStreamNtTilesPerCu) * args.cus)
     hipLaunchKernelGGL((expand_dma_kernel<T, BM, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                        args);
   else

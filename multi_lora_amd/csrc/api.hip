@@ -289,8 +289,8 @@ int mlora_apply_segments(const void* x, int64_t x_row_stride, int32_t num_rows, 
   // column tile of a row tile adds the same sums again, which costs more
   // than the reduce launch it saves on wide outputs (measured per layer at
   // the 32-layer step: o 20.5 vs 21.8 us, down 32.2 vs 32.9, but gate|up
-  // 82.1 vs 64.7; q|k|v, 24 tiles, 24.6 us either way with the mixed-batch
-  // expand).
+  // 82.1 vs 64.7; q|k|v, 24 tiles, 25.6 vs 24.3 us with the mixed-batch
+  // expand's non-temporal tiles).
   int col_tiles = 0;
   for (int s = 0; s < n_slices && slices != nullptr; ++s) col_tiles += mlora::cdiv(slices[s].out_dim, mlora::kExpandBN);
   const bool long_segments =

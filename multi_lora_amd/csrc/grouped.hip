@@ -438,7 +438,7 @@ hipError_t launch_mixed_dt(const ExpandArgs& ea, const GroupedArgs& ga, bool fus
   // tiles are read and written with the non-temporal hint (c5 gate|up, 1792
   // tiles: expand 38.4 -> 33.1 us).
   const int64_t streamed = mixed_long_units<kExpandStreamBM>(long_rows, long_segs) * ea.n_tiles;
-  if (streamed >= static_cast<int64_t>(kStreamNtTilesPerCu) * cus)
+  if (cus > 0 && streamed >= static_cast<int64_t>(kStreamNtTilesPerCu) * cus)
     return launch_mixed_t<T, false, kExpandStreamBM, true>(ea, ga, long_rows, long_segs, short_units, cus, stream);
   if (streamed >= 4 * static_cast<int64_t>(cus))
     return launch_mixed_t<T, false, kExpandStreamBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);

@@ -103,11 +103,16 @@ hipError_t launch_streamed(ExpandArgs args, hipStream_t stream) {
 hipError_t launch_expand(int bm, ExpandArgs args, int dtype, bool aligned, hipStream_t stream) {
   // Long segments on average (at least kExpandStreamBM rows a segment),
   // 16-bit and aligned: 64-row tiles with the output streamed into LDS
-  // (measured at prefill gate|up 113.9 vs 126.7 us, down 21.1 vs 21.7 us).
+  // (measured at prefill gate|up 113.9 vs 126.7 us, down 21.1 vs 21.7 us),
+  // when the 64-row tiles give every CU four workgroups: fewer, and the
+  // 32-row tiles' twice as many workgroups are faster (two 512-row prompts,
+  // out 4096: 5.9 vs 8.8 us; q|k|v 4096->[4096,1024,1024]: 7.6 vs 10.1 us).
   // Mixed batches, whose tiles are mostly one-row decode segments, keep the
   // 32-row tiles.
+  const int64_t streamed = dense_tiles(args.meta.bs, (args.m_tiles + 1) / 2, args.rows, kExpandStreamBM) * args.n_tiles;
   if (aligned && bm == kExpandLongBM && (dtype == MLORA_BF16 || dtype == MLORA_F16) && args.ks <= 1 &&
-      static_cast<int64_t>(args.rows) >= static_cast<int64_t>(kExpandStreamBM) * args.meta.bs)
+      static_cast<int64_t>(args.rows) >= static_cast<int64_t>(kExpandStreamBM) * args.meta.bs &&
+      (args.cus <= 0 || streamed >= 4 * static_cast<int64_t>(args.cus)))
     return dtype == MLORA_BF16 ? launch_streamed<BF16>(args, stream) : launch_streamed<F16>(args, stream);
   switch (dtype) {
     case MLORA_BF16:

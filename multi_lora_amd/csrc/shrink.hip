@@ -773,7 +773,7 @@ template <class T>
 hipError_t launch_reduce(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
   if constexpr (sizeof(typename T::raw_t) == 2) {
     if (args.row_reduce && args.part_cols % 4 == 0 && args.mid_stride % 4 == 0 &&
-        reinterpret_cast<uintptr_t>(args.mid) % 8 == 0) {
+        reinterpret_cast<uintptr_t>(args.mid) % 8 == 0 && reinterpret_cast<uintptr_t>(args.partials) % 16 == 0) {
       const int64_t n = (static_cast<int64_t>(args.rows) * (args.part_cols / 4) + 255) / 256;
       if (n <= 0) return hipSuccess;
       if (!grid_fits(n)) return hipErrorInvalidConfiguration;

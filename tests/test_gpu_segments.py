@@ -310,6 +310,46 @@ def test_interleaved_mixed_expand_in_a_replayed_graph_follows_table_rewrites(dev
         assert torch.equal(out.cpu(), want.cpu()), f"replay {rep}"
 
 
+def test_split_reduce_in_a_replayed_graph_follows_table_rewrites(dev):
+    """Split K with an output too wide for the expand to add the split sums:
+    the call runs the shrink, the table-free split reduce and the expand.
+    Captured once, replayed after in-place rewrites of the slots (one of
+    them moves segments to rank-0 slots, whose rows' reduced values are
+    never read), each replay equals a fresh eager call."""
+    lens = [300, 200] + [1] * 30
+    ranks = [16] * 32 + [0] * 32
+    slots0 = [0, 1] + [2 + (i % 8) for i in range(30)]
+    slots1 = [40, 1] + [20 + (i % 16) + (i % 2) * 20 for i in range(30)]
+    x, As, Bs, base, cols, _, scal = case(dev, lens, slots0, ranks, 4096, [4096, 1024], 16, torch.bfloat16, 9)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    meta = make_meta(lens, slots0, ranks, scal, dev, torch.bfloat16)
+    out = base.to(dev).clone()
+    ws = Workspace()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        apply_segments(xd, Ad, Bd, meta, out, cols, workspace=ws)
+    for rep, slots in enumerate((slots0, slots1, slots0)):
+        meta.weight_indices.copy_(torch.tensor(slots, dtype=torch.int32))
+        meta.set_host_copies(lens, slots)
+        out.copy_(base.to(dev))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = base.to(dev).clone()
+        apply_segments(xd, Ad, Bd, make_meta(lens, slots, ranks, scal, dev, torch.bfloat16, host_copies=False), want,
+                       cols, workspace=Workspace())
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want.cpu()), f"replay {rep}"
+        assert_tol_f64(out.cpu(), apply_f64(x, As, Bs, make_meta(lens, slots, ranks, scal, "cpu", torch.bfloat16),
+                                            base, cols), f"replay {rep}")
+
+
 def test_mixed_batch_expand_in_a_replayed_graph_follows_table_rewrites(dev):
     """A captured mixed expand keeps the launch size of its capture; after an
     in-place rewrite that gives the short segments more distinct slots, the

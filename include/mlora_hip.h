@@ -245,6 +245,37 @@ int mlora_apply_grouped_static(const void* x, int64_t x_row_stride, int32_t num_
                                int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, int32_t mode,
                                int32_t phases, void* stream);
 
+/* RMSNorm fused into the slot-grouped apply (two launches), for a decoder
+ * layer's input norm feeding LoRA-wrapped projections:
+ *   y[t] = round(x[t] * rsqrt(mean(x[t]^2) + eps) * w)     (every row t)
+ *   out[t, out_col_s + n] += round(scaling * round(rstd_t * (round(x[t] * w) . A_s[slot,:rank]))
+ *                                  . B_s[slot, n, :rank])
+ * The first launch (phases & 1) writes y, the same bits mlora_rmsnorm writes,
+ * and the shrink's K-chunk sums: the shrink reads x once and multiplies
+ * round(x * w) with A on MFMA, keeping each row's sum of x^2 per chunk, so it
+ * needs no y and no pass before it.  The second launch (phases & 2) adds a
+ * row's sums, rstd_t = rsqrt(sum of x^2 / in_dim + eps) scales them before the
+ * reference's `mid` rounding, and the expand follows as in
+ * mlora_apply_grouped.  In a layer the base GEMM on y runs between the two
+ * halves (phases 1, GEMM, phases 2), since the expand adds into its output.
+ * Against the unfused path (mlora_rmsnorm, then mlora_apply_grouped on y)
+ * only the rounding of the MFMA inputs differs (round(x * w) scaled after
+ * the sum instead of round(x * rstd * w)), within the tolerance of an fp32
+ * reference.  The weight has the data dtype; y must not overlap x.
+ * Workspace: mlora_grouped_workspace_bytes (any mode), the same conditions
+ * as mlora_apply_grouped (zero-filled before its first use, one stream);
+ * a table without LoRA work still writes y.
+ * Requirements (else -2): bf16 or fp16, the grouped path's shape and
+ * alignment conditions, and 16-byte aligned rows of y and of the weight.
+ * No counterpart is called in the reference: it fuses rmsnorm_fwd
+ * (multi_lora/kernels/rmsnorm.py:48-92) into the decode shrink it feeds
+ * (sgemm_lora_a.py:118-183); the expand half replaces sgemm_lora_b.py:93-153. */
+int mlora_rmsnorm_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                                const void* norm_w, float eps, void* y, int64_t y_row_stride,
+                                const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                                int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                                size_t workspace_bytes, int32_t phases, void* stream);
+
 /* Bytes of a plan with room for `entries_cap` entries. */
 size_t mlora_plan_bytes(int32_t entries_cap);
 

@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MLORA_F32, MLORA_F16, MLORA_BF16 = 0, 1, 2
 MAX_SLICES = 4
@@ -41,6 +41,7 @@ EXPORTS = (
     "mlora_plan_bytes",
     "mlora_build_plan",
     "mlora_apply_grouped_static",
+    "mlora_rmsnorm_apply_grouped",
 )
 
 # include/mlora_hip.h: MLORA_STATIC_SCRATCH_BYTES
@@ -166,6 +167,11 @@ _SIGNATURES = {
          _i32, _vp],
     ),
     "mlora_build_plan": (ctypes.c_int, [ctypes.POINTER(SegMeta), _i32, _vp, _i32, _vp]),
+    "mlora_rmsnorm_apply_grouped": (
+        ctypes.c_int,
+        [_vp, _i64, _i32, _i32, _vp, _f32, _vp, _i64, ctypes.POINTER(Slice), _i32, _i32, _vp, _i64,
+         ctypes.POINTER(SegMeta), _i32, _vp, _sz, _i32, _vp],
+    ),
 }
 
 

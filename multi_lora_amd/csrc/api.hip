@@ -227,7 +227,7 @@ int expand_impl(const void* mid, int64_t mid_row_stride, int32_t num_rows, const
 
 extern "C" {
 
-int mlora_abi_version(void) { return 5; }
+int mlora_abi_version(void) { return 6; }
 
 const char* mlora_last_error(void) { return g_err; }
 
@@ -333,12 +333,44 @@ int mlora_build_plan(const mlora_seg_meta* meta, int32_t num_rows, int32_t* plan
   return 0;
 }
 
+// The RMSNorm folded into a grouped call (mlora_rmsnorm_apply_grouped):
+// weight of the data dtype, output rows y.
+struct NormCall {
+  const void* w;
+  float eps;
+  void* y;
+  int64_t y_stride;
+};
+
+// RMSNorm arguments of a fused call over the call's rows of x.
+static mlora::RmsArgs norm_rms_args(const NormCall& nc, const void* x, int64_t x_row_stride, int32_t num_rows,
+                                    int32_t in_dim, int32_t dtype) {
+  mlora::RmsArgs a{};
+  a.x = x;
+  a.x_stride_outer = x_row_stride;
+  a.x_stride_inner = x_row_stride;
+  a.inner = 1;
+  a.w = nc.w;
+  a.w_dtype = dtype;
+  a.y = nc.y;
+  a.y_stride = nc.y_stride;
+  a.rows = num_rows;
+  a.hidden = in_dim;
+  a.eps = nc.eps;
+  mlora::rmsnorm_shape(in_dim, dtype, &a.tpr, &a.nc);
+  a.aligned = 1;
+  a.w_vec = 1;
+  return a;
+}
+
 // mlora_apply_grouped on a given workspace (the caller's, or the static
-// scratch of mlora_apply_grouped_static).
+// scratch of mlora_apply_grouped_static); with `norm`, the fused RMSNorm
+// form (two launches).
 static int apply_grouped_impl(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
                               const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
                               int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
-                              size_t workspace_bytes, int32_t mode, int32_t phases, void* stream) {
+                              size_t workspace_bytes, int32_t mode, int32_t phases, void* stream,
+                              const NormCall* norm = nullptr) {
   if (!valid_dtype(dtype)) return fail(kBadArg, "bad dtype %d", dtype);
   if (int rc = check_meta(meta)) return rc;
   if (n_slices < 1 || n_slices > MLORA_MAX_SLICES) return fail(kBadArg, "n_slices %d not in [1, %d]", n_slices, MLORA_MAX_SLICES);
@@ -347,7 +379,15 @@ static int apply_grouped_impl(const void* x, int64_t x_row_stride, int32_t num_r
   if (x_row_stride < in_dim) return fail(kBadArg, "x row stride %lld < in_dim %d", (long long)x_row_stride, in_dim);
   if (phases < 1 || phases > 3) return fail(kBadArg, "phases %d not in 1..3", phases);
   if (mode < 0 || mode > 2) return fail(kBadArg, "mode %d not in 0..2", mode);
-  if (meta->bs == 0 || num_rows == 0 || meta->num_slots == 0) return 0;
+  if (meta->bs == 0 || num_rows == 0 || meta->num_slots == 0) {
+    // No LoRA work: the fused call still owes the RMSNorm rows.
+    if (norm == nullptr || num_rows == 0 || !(phases & 1)) return 0;
+    if (x == nullptr) return fail(kBadArg, "x is null");
+    const hipError_t e = mlora::launch_rmsnorm(norm_rms_args(*norm, x, x_row_stride, num_rows, in_dim, dtype), dtype,
+                                               static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+    return 0;
+  }
   if (x == nullptr || out == nullptr) return fail(kBadArg, "x or out is null");
   if (mode != mlora::kGroupTwo && phases != 3)
     return fail(kBadArg, "phases %d: only the two-launch mode runs one half (use phases=3)", phases);
@@ -429,6 +469,14 @@ static int apply_grouped_impl(const void* x, int64_t x_row_stride, int32_t num_r
   // once; beyond that expand items wait behind shrink items and two launches
   // are faster (q|k|v over 110 entries, 8064 items: 28.5 vs 34.6 us; the
   // 128-token q_proj batch, 1024 items: 7.4 vs 9.1 us).
+  if (norm != nullptr) {
+    mlora::NormShrinkArgs na{};
+    na.rms = norm_rms_args(*norm, x, x_row_stride, num_rows, in_dim, dtype);
+    na.sumsq = reinterpret_cast<float*>(ws + sh.sumsq_off);
+    const hipError_t e = mlora::launch_planned_norm(plan, args, na, dtype, sh.nbt, phases, st);
+    if (e != hipSuccess) return hip_fail(e, "fused RMSNorm grouped launch");
+    return 0;
+  }
   int m = mode;
   if (m == mlora::kGroupAuto) {
     const int64_t items = static_cast<int64_t>(args.e_grid) * (sh.s_groups * sh.kc + tiles);
@@ -446,6 +494,34 @@ int mlora_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, i
   g_err[0] = '\0';
   return apply_grouped_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, out, out_row_stride, meta,
                             dtype, workspace, workspace_bytes, mode, phases, stream);
+}
+
+int mlora_rmsnorm_apply_grouped(const void* x, int64_t x_row_stride, int32_t num_rows, int32_t in_dim,
+                                const void* norm_w, float eps, void* y, int64_t y_row_stride,
+                                const mlora_slice* slices, int32_t n_slices, int32_t r_max, void* out,
+                                int64_t out_row_stride, const mlora_seg_meta* meta, int32_t dtype, void* workspace,
+                                size_t workspace_bytes, int32_t phases, void* stream) {
+  g_err[0] = '\0';
+  if (dtype != MLORA_BF16 && dtype != MLORA_F16) return fail(kUnsupported, "fused RMSNorm path needs bf16 or fp16, got dtype %d", dtype);
+  if (in_dim <= 0 || num_rows < 0) return fail(kBadArg, "in_dim %d, num_rows %d", in_dim, num_rows);
+  if (num_rows == 0) return 0;
+  if (x == nullptr || norm_w == nullptr || y == nullptr) return fail(kBadArg, "null x, weight or y");
+  if (x_row_stride < in_dim || y_row_stride < in_dim)
+    return fail(kBadArg, "x / y row strides %lld / %lld below in_dim %d", (long long)x_row_stride,
+                (long long)y_row_stride, in_dim);
+  const int vec = vec_elems(dtype);
+  if (!al16(x) || !al16(y) || !al16(norm_w) || in_dim % vec != 0 || x_row_stride % vec != 0 || y_row_stride % vec != 0)
+    return fail(kUnsupported, "fused RMSNorm path needs 16-byte aligned rows of x, y and the weight");
+  // The launch that writes y also reads x: the two must not share a byte.
+  const int eb = elem_bytes(dtype);
+  const uintptr_t x0 = reinterpret_cast<uintptr_t>(x);
+  const uintptr_t y0 = reinterpret_cast<uintptr_t>(y);
+  const uintptr_t x1 = x0 + static_cast<uintptr_t>((static_cast<int64_t>(num_rows - 1) * x_row_stride + in_dim) * eb);
+  const uintptr_t y1 = y0 + static_cast<uintptr_t>((static_cast<int64_t>(num_rows - 1) * y_row_stride + in_dim) * eb);
+  if (x0 < y1 && y0 < x1) return fail(kBadArg, "y overlaps x (the fused call reads x while it writes y)");
+  const NormCall nc{norm_w, eps, y, y_row_stride};
+  return apply_grouped_impl(x, x_row_stride, num_rows, in_dim, slices, n_slices, r_max, out, out_row_stride, meta,
+                            dtype, workspace, workspace_bytes, mlora::kGroupTwo, phases, stream, &nc);
 }
 
 }  // extern "C"
@@ -532,9 +608,6 @@ int rmsnorm_call(const void* x, int64_t x_stride_outer, int64_t x_stride_inner, 
   if (rows == 0) return 0;
   if (x == nullptr || w == nullptr || y == nullptr) return fail(kBadArg, "null x, w or y");
   const int vec = vec_elems(dtype);
-  const int nch = mlora::cdiv(hidden, vec);
-  int tpr = 16;
-  while (tpr < 256 && tpr * 2 <= nch) tpr *= 2;
   mlora::RmsArgs a{};
   a.x = x;
   a.x_stride_outer = x_stride_outer;
@@ -547,9 +620,7 @@ int rmsnorm_call(const void* x, int64_t x_stride_outer, int64_t x_stride_inner, 
   a.rows = rows;
   a.hidden = hidden;
   a.eps = eps;
-  a.tpr = tpr;
-  a.nc = 1;
-  while (a.nc < 8 && a.nc * tpr < nch) a.nc *= 2;
+  mlora::rmsnorm_shape(hidden, dtype, &a.tpr, &a.nc);
   a.aligned = al16(x) && al16(y) && hidden % vec == 0 && x_stride_outer % vec == 0 &&
               x_stride_inner % vec == 0 && y_row_stride % vec == 0 &&
               (residual == nullptr || (al16(residual) && residual_row_stride % vec == 0));

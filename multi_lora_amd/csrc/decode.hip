@@ -48,8 +48,15 @@
 //
 // Two launches: shrink items, then expand items, with the same bodies and
 // the same sums (bit-identical results); the kernel boundary orders them.
+//
+// Fused RMSNorm (two launches): the shrink launch also holds the RMSNorm of
+// the call's rows (the RMSNorm kernel's row body, so the same y), and its
+// shrink items multiply round(x * w) instead of y, storing each row's sum of
+// x^2 per K chunk; the expand items scale a row's summed chunks by its
+// rsqrt(mean(x^2) + eps) before the mid rounding.
 #include "kernels.h"
 #include "loads.h"
+#include "rmsnorm_row.h"
 
 namespace mlora {
 
@@ -182,9 +189,14 @@ __device__ __forceinline__ int64_t sum_index(const DecodeArgs& a, int pos, int c
 // rare recompute when it has four A blocks and one expand K-step, so that
 // the single launch keeps four workgroups a CU without spilling (q|k|v at
 // rank 16: 12.6 vs 14.0 us at 64 tokens, 19.2 vs 20.9 at 256).
-template <class T, int NBT, int SP, bool LEAN = false>
+// NORM (the fused RMSNorm launch): the MFMA takes round(x * w) with the
+// RMSNorm weight nw, and the chunk's fp32 sum of x^2 of each row goes to
+// sumsq[pos + row][c] (slice group 0; ssl: 48 floats of LDS).
+template <class T, int NBT, int SP, bool LEAN = false, bool NORM = false>
 __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xrow, int sg, int c,
-                             f32x4 (*red)[kWave], uint64_t flag) {
+                             f32x4 (*red)[kWave], uint64_t flag, const typename T::raw_t* nw = nullptr,
+                             float* sumsq = nullptr, float* ssl = nullptr) {
+  static_assert(!(NORM && LEAN), "the fused RMSNorm shrink has no recompute path");
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   constexpr int KSTEP = T::KSTEP;
@@ -220,6 +232,7 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
   f32x4 acc[NBT];
 #pragma unroll
   for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.f;  // NORM: this lane's sum of x^2
   if constexpr (!LEAN) {
     u32x4 af[SP][NBT];
 #pragma unroll
@@ -241,7 +254,29 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
       const u32x4 v = ld_chunk(xr + (kk < a.in_dim ? kk : 0));
       xv[sp] = kk < a.in_dim ? v : zero_chunk();
     }
+    u32x4 wv[SP];
+    if constexpr (NORM) {
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp) {
+        const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
+        const u32x4 v = ld_chunk(nw + (kk < a.in_dim ? kk : 0));
+        wv[sp] = kk < a.in_dim ? v : zero_chunk();
+      }
+    }
     fence_regs(af);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int sp = 0; sp < SP; ++sp) {
+        float f[VEC];
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const float v = chunk_elem<T>(xv[sp], q);
+          ss += v * v;
+          f[q] = v * chunk_elem<T>(wv[sp], q);
+        }
+        xv[sp] = pack_chunk<T>(f);
+      }
+    }
 #pragma unroll
     for (int sp = 0; sp < SP; ++sp) {
       const int kk = kbeg + (wave + 4 * sp) * KSTEP + g * VEC;
@@ -270,6 +305,12 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
     }
   }
   MLORA_STAMP_AFTER_LOADS(2);
+  if constexpr (NORM) {
+    // Lanes r16 + 16 g hold row r16's elements of the chunk.
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    if (wave > 0 && g == 0) ssl[(wave - 1) * 16 + r16] = ss;
+  }
   if (wave > 0) {
 #pragma unroll
     for (int j = 0; j < NBT; ++j)
@@ -295,6 +336,10 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
         *reinterpret_cast<f32x4*>(a.partials + sum_index(a, en.pos + r16, c, (s_first + sl) * a.r_max + n)) = acc[j];
       }
     }
+    if constexpr (NORM) {
+      const float tot = ((ss + ssl[r16]) + ssl[16 + r16]) + ssl[32 + r16];
+      if (sg == 0 && g == 0 && r16 < en.nr) sumsq[static_cast<int64_t>(en.pos + r16) * a.kc + c] = tot;
+    }
     if (flag != 0) {
       // The flag goes out only once every sum of the chunk has reached the L2.
       asm volatile("" ::: "memory");
@@ -315,6 +360,7 @@ struct DecodeLds {
   raw ytile[16 * (kGroupMaxRank + T::VEC)];
   f32x4 part[kGroups][16][kGroupMaxRank / 4];  // per chunk group: sums of each (row, 4 columns)
   uint64_t missing;                             // chunks not received
+  float rstd[16];                               // fused RMSNorm: each row's rsqrt(mean(x^2) + eps)
 };
 
 // 16 bytes of the workspace at byte offset `off`, read past the L1 (sc1):
@@ -329,8 +375,11 @@ __device__ __forceinline__ u32x4 load16_l2(__amdgpu_buffer_rsrc_t rsrc, int64_t 
 // requested together.  The mapping uses shifts only: the item's set-up is
 // on the decode path's critical chain, and every instruction a wave issues
 // there costs about 4 cycles at four waves a SIMD.
-template <class T, int WN>
-__device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeLds<T, WN>& lds) {
+// NORM: wave 3 also adds each row's sums of x^2 (sumsq, chunk order) and
+// keeps rsqrt(ss / in_dim + eps) in lds.rstd.
+template <class T, int WN, bool NORM = false>
+__device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeLds<T, WN>& lds,
+                            const float* sumsq = nullptr, float eps = 0.f) {
   static_assert(kGroups == 4 && kGroupMaxRank / 4 <= 16, "one chunk group per wave, at most 16 quads a row");
   const int quads = (en.rank + 3) >> 2;
   const int per = (a.kc + kGroups - 1) / kGroups;  // chunks per group
@@ -357,6 +406,22 @@ __device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeL
     }
     lds.part[grp][row][q] = sum;
   }
+  if constexpr (NORM) {
+    const int l = threadIdx.x & 63;
+    if (grp == kGroups - 1 && l < en.nr) {
+      const float* sq = sumsq + static_cast<int64_t>(en.pos + l) * a.kc;
+      float t = 0.f;
+      for (int cb = 0; cb < a.kc; cb += 4) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = sq[min(cb + k, a.kc - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (cb + k < a.kc) t += v[k];
+      }
+      lds.rstd[l] = rsqrtf(t / static_cast<float>(a.in_dim) + eps);
+    }
+  }
   lds_barrier();
 }
 
@@ -372,10 +437,13 @@ struct ExpandRows {
 // Expand item (entry e, column tile nt_g).  LINKED: the sums come as tagged
 // words from this launch's shrink items (or are computed here), else as
 // fp32 from the previous launch.
-template <class T, int NBT, int SP, int WN, int RS, bool LINKED>
+// NORM (expand half of the fused RMSNorm launch): y = round(rstd * sum),
+// with each row's rstd from the shrink's sums of x^2.
+template <class T, int NBT, int SP, int WN, int RS, bool LINKED, bool NORM = false>
 __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, const Entry& en, int nt_g,
                              const int (&orow_raw)[ExpandRows<T, WN>::RPT], DecodeLds<T, WN>& lds,
-                             f32x4 (*red)[kWave]) {
+                             f32x4 (*red)[kWave], const float* sumsq = nullptr, float eps = 0.f) {
+  static_assert(!(NORM && LINKED), "the fused RMSNorm path runs as two launches");
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   constexpr int KSTEP = T::KSTEP;
@@ -491,7 +559,7 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
       load_out();
     }
   }
-  gather_sums<T, WN>(a, en, s, lds);
+  gather_sums<T, WN, NORM>(a, en, s, lds, sumsq, eps);
   MLORA_STAMP(4);
   fence_regs(bf);
 
@@ -506,6 +574,11 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
       if (row < en.nr && c4 < rank) {
 #pragma unroll
         for (int grp = 0; grp < kGroups; ++grp) sum += lds.part[grp][row][c4 / 4];
+        if constexpr (NORM) {
+          const float r = lds.rstd[row];
+#pragma unroll
+          for (int q2 = 0; q2 < 4; ++q2) sum[q2] *= r;
+        }
       }
       raw* y = lds.ytile + row * YS + c4;
 #pragma unroll
@@ -563,9 +636,10 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
 // Shrink items of entries j, j + e_grid, ... (item: K chunk, and slice group
 // when the slices' A blocks are split over items).  en / xrow_raw: entry j
 // and this thread's row word, already requested.
-template <class T, int NBT, int SCHED>
+template <class T, int NBT, int SCHED, bool NORM = false>
 __device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, int item, int n_ent, Entry en,
-                             int xrow_raw, f32x4 (*red)[kWave]) {
+                             int xrow_raw, f32x4 (*red)[kWave], const typename T::raw_t* nw = nullptr,
+                             float* sumsq = nullptr, float* ssl = nullptr) {
   constexpr int SP = kGroupStepsLinked;
   int sg = 0, c = item;
   if (a.s_groups != 1) {
@@ -577,14 +651,14 @@ __device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, in
   // grid smaller than the plan), so nothing the loop hoists runs before it.
   MLORA_STAMP(1);
   if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
-    shrink_chunk<T, NBT, SP>(a, j, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag);
+    shrink_chunk<T, NBT, SP, false, NORM>(a, j, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag, nw, sumsq, ssl);
   else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0)
     atomicAdd(a.header + kWsPlanErrors, 1);
   for (int e = j + a.e_grid; e < n_ent; e += a.e_grid) {
     xrow_raw = load_entry_row(plan, e, threadIdx.x & 15);
     en = load_entry(plan, e, a.r_max, a.num_slots);
     if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
-      shrink_chunk<T, NBT, SP>(a, e, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag);
+      shrink_chunk<T, NBT, SP, false, NORM>(a, e, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag, nw, sumsq, ssl);
     else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0)
       atomicAdd(a.header + kWsPlanErrors, 1);
   }
@@ -593,16 +667,17 @@ __device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, in
 // Expand items (column tile `tile`) of entries j, j + e_grid, ...;
 // count_errors: this launch has no shrink items, so tile 0 reports entries
 // it cannot take.
-template <class T, int NBT, int WN, int RS, int SCHED>
+template <class T, int NBT, int WN, int RS, int SCHED, bool NORM = false>
 __device__ void expand_items(const int32_t* plan, const DecodeArgs& a, int j, int tile, int n_ent, Entry en,
                              int (&rows_raw)[ExpandRows<T, WN>::RPT], DecodeLds<T, WN>& lds, f32x4 (*red)[kWave],
-                             bool count_errors) {
+                             bool count_errors, const float* sumsq = nullptr, float eps = 0.f) {
   constexpr int SP = kGroupStepsLinked;
   constexpr int RPT = ExpandRows<T, WN>::RPT;
   for (int e = j;;) {
     MLORA_STAMP(1);
     if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
-      expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked>(a, plan, e, en, tile, rows_raw, lds, red);
+      expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked, NORM>(a, plan, e, en, tile, rows_raw, lds, red, sumsq,
+                                                                      eps);
     else if (count_errors && en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && tile == 0)
       atomicAdd(a.header + kWsPlanErrors, 1);
     e += a.e_grid;
@@ -717,6 +792,97 @@ template <class T>
 hipError_t launch_dtype(const int32_t* plan, const DecodeArgs& a, int nbt, int mode, int phases, hipStream_t stream) {
   if (a.r_max <= T::KSTEP) return launch_nbt<T, 1, 1>(plan, a, nbt, mode, phases, stream);
   return launch_nbt<T, 1, 2>(plan, a, nbt, mode, phases, stream);
+}
+
+// ------------------------------------------- fused RMSNorm + decode shrink
+// Shrink launch: grid (e_grid, n_shrink + norm rows).  Items [0, n_shrink)
+// are the shrink items of the two-launch schedule, with x * w on the MFMA
+// and the rows' sums of x^2 stored; workgroup (j, n_shrink + i) is RMSNorm
+// row block i * e_grid + j (256 / tpr rows), written as the RMSNorm kernel
+// writes it.  Nothing in the launch waits on another workgroup.
+template <class T, int NBT>
+__global__ __launch_bounds__(256, NBT >= 8 ? 2 : 4) void planned_norm_shrink_kernel(const int32_t* __restrict__ plan,
+                                                                                     int plan_cap, int n_shrink,
+                                                                                     DecodeArgs a, NormShrinkArgs na) {
+  __shared__ f32x4 red[3 * NBT][kWave];
+  __shared__ float ssl[3 * 16];
+  const int j = blockIdx.x;
+  const int item = blockIdx.y;
+  if (item >= n_shrink) {
+    const int64_t blk = static_cast<int64_t>(item - n_shrink) * gridDim.x + j;
+    // At most two chunks a thread held (the rest streamed twice): the same
+    // chunks in the same order as the RMSNorm kernel's, so the same bits.
+    if (blk * (256 / na.rms.tpr) < na.rms.rows)
+      rmsnorm_block<T, 2, true, true, false>(na.rms, blk, ssl, min(na.rms.nc, 2));
+    return;
+  }
+  const int ef = min(j, plan_cap - 1);
+  const int row_raw = load_entry_row(plan, ef, threadIdx.x & 15);
+  const Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
+  const int p0 = plan[0];
+  const int n_ent = min(p0, min(plan_cap, a.e_cap));
+  if (j == 0 && item == 0 && threadIdx.x == 0 && p0 > min(plan_cap, a.e_cap)) atomicAdd(a.header + kWsPlanErrors, 1);
+  if (j < n_ent)
+    shrink_items<T, NBT, kGroupShrinkOnly, true>(plan, a, j, item, n_ent, en, row_raw, red,
+                                                 static_cast<const typename T::raw_t*>(na.rms.w), na.sumsq, ssl);
+}
+
+// Expand launch: the expand items of the two-launch schedule, y scaled by
+// each row's rstd before its rounding.
+template <class T, int WN, int RS>
+__global__ __launch_bounds__(256, 4) void planned_norm_expand_kernel(const int32_t* __restrict__ plan, int plan_cap,
+                                                                     DecodeArgs a, const float* __restrict__ sumsq,
+                                                                     float eps) {
+  __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
+  constexpr int RPT = ExpandRows<T, WN>::RPT;
+  const int j = blockIdx.x;
+  const int ef = min(j, plan_cap - 1);
+  int rows_raw[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) rows_raw[i] = load_entry_row(plan, ef, ExpandRows<T, WN>::row_of(threadIdx.x, i));
+  const Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
+  const int n_ent = min(plan[0], min(plan_cap, a.e_cap));
+  if (j < n_ent)
+    expand_items<T, 1, WN, RS, kGroupExpandOnly, true>(plan, a, j, blockIdx.y, n_ent, en, rows_raw, lds, nullptr,
+                                                       true, sumsq, eps);
+}
+
+template <class T, int NBT>
+hipError_t launch_norm_shrink(const int32_t* plan, const DecodeArgs& a, const NormShrinkArgs& na, hipStream_t stream) {
+  const int n_shrink = a.s_groups * a.kc;
+  const int64_t blocks = (na.rms.rows + (256 / na.rms.tpr) - 1) / (256 / na.rms.tpr);
+  const int64_t items = n_shrink + (blocks + a.e_grid - 1) / a.e_grid;
+  if (a.e_grid <= 0 || blocks <= 0) return hipSuccess;
+  if (items > 65535 || !grid_fits(items * a.e_grid)) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((planned_norm_shrink_kernel<T, NBT>), dim3(static_cast<unsigned>(a.e_grid), static_cast<unsigned>(items)),
+                     dim3(256), 0, stream, plan, a.plan_cap, n_shrink, a, na);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_norm_t(const int32_t* plan, const DecodeArgs& a, const NormShrinkArgs& na, int nbt, int phases,
+                         hipStream_t stream) {
+  if (phases & 1) {
+    hipError_t e;
+    switch (nbt) {
+      case 1: e = launch_norm_shrink<T, 1>(plan, a, na, stream); break;
+      case 2: e = launch_norm_shrink<T, 2>(plan, a, na, stream); break;
+      default: e = launch_norm_shrink<T, 4>(plan, a, na, stream); break;
+    }
+    if (e != hipSuccess) return e;
+  }
+  if ((phases & 2) && a.e_grid > 0 && a.n_tiles > 0) {
+    if (a.n_tiles > 65535 || !grid_fits(static_cast<int64_t>(a.n_tiles) * a.e_grid)) return hipErrorInvalidConfiguration;
+    const dim3 grid(static_cast<unsigned>(a.e_grid), static_cast<unsigned>(a.n_tiles));
+    if (a.r_max <= T::KSTEP)
+      hipLaunchKernelGGL((planned_norm_expand_kernel<T, 1, 1>), grid, dim3(256), 0, stream, plan, a.plan_cap, a,
+                         na.sumsq, na.rms.eps);
+    else
+      hipLaunchKernelGGL((planned_norm_expand_kernel<T, 1, 2>), grid, dim3(256), 0, stream, plan, a.plan_cap, a,
+                         na.sumsq, na.rms.eps);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
 // Plan of a segment table, built on the device by one workgroup of 1024
@@ -900,7 +1066,9 @@ bool plan_decode(int in_dim, int r_max, int n_slices, int rows, int dtype, Decod
   sh->flags_off = kWsHeaderBytes;
   sh->partials_off = sh->flags_off + round256(static_cast<size_t>(sh->e_cap) * sh->s_groups * sh->kc * sizeof(uint64_t));
   sh->plan_off = sh->partials_off + round256(n_sums * sizeof(float));
-  sh->bytes = sh->plan_off + sizeof(int32_t) * (kPlanHeaderWords + static_cast<size_t>(sh->e_cap) * kPlanEntryWords);
+  sh->sumsq_off =
+      sh->plan_off + round256(sizeof(int32_t) * (kPlanHeaderWords + static_cast<size_t>(sh->e_cap) * kPlanEntryWords));
+  sh->bytes = sh->sumsq_off + sizeof(float) * static_cast<size_t>(rows) * sh->kc;
   return true;
 }
 
@@ -913,6 +1081,12 @@ hipError_t launch_planned(const int32_t* plan, const DecodeArgs& args, int dtype
                           hipStream_t stream) {
   if (dtype == MLORA_BF16) return launch_dtype<BF16>(plan, args, nbt, mode, phases, stream);
   return launch_dtype<F16>(plan, args, nbt, mode, phases, stream);
+}
+
+hipError_t launch_planned_norm(const int32_t* plan, const DecodeArgs& args, const NormShrinkArgs& na, int dtype,
+                               int nbt, int phases, hipStream_t stream) {
+  if (dtype == MLORA_BF16) return launch_norm_t<BF16>(plan, args, na, nbt, phases, stream);
+  return launch_norm_t<F16>(plan, args, na, nbt, phases, stream);
 }
 
 }  // namespace mlora

@@ -209,7 +209,7 @@ struct DecodeArgs {
 // shrink items per chunk, and the workspace regions.
 struct DecodeShape {
   int kc, k_chunk, nbt, s_groups;
-  size_t flags_off, partials_off, plan_off, bytes;
+  size_t flags_off, partials_off, plan_off, sumsq_off, bytes;
   int e_cap;
 };
 bool plan_decode(int in_dim, int r_max, int n_slices, int rows, int dtype, DecodeShape* sh);
@@ -261,6 +261,27 @@ struct RmsArgs {
 };
 
 hipError_t launch_rmsnorm(RmsArgs args, int dtype, hipStream_t stream);
+
+// Threads per row and registered chunks per thread of the RMSNorm kernel for
+// rows of `hidden` elements (the fused RMSNorm + decode shrink takes the same,
+// so both write the same bits).
+void rmsnorm_shape(int hidden, int dtype, int* tpr, int* nc);
+
+// ------------------------------------------- fused RMSNorm + decode shrink
+// The two-launch planned decode with the RMSNorm of its input rows folded
+// into the shrink launch.  That launch holds the shrink items and, past them
+// in the grid, norm workgroups that write y = RMSNorm(x) for every row (the
+// RMSNorm kernel's rows, same bits).  A shrink item reads the raw x rows and
+// the weight, multiplies on MFMA round(x * w) instead of y, and stores with
+// its chunk sums the chunk's fp32 sum of x^2 for each row; the expand items
+// add a row's sums of squares in chunk order, take rstd = rsqrt(ss / in_dim
+// + eps), and round rstd * sum to the storage type as y . A^T.
+struct NormShrinkArgs {
+  RmsArgs rms;   // the call's rows: x, weight (data dtype, 16-byte aligned), y, eps
+  float* sumsq;  // [ws_rows][kc]: per planned row and K chunk, the sum of x^2
+};
+hipError_t launch_planned_norm(const int32_t* plan, const DecodeArgs& args, const NormShrinkArgs& na, int dtype,
+                               int nbt, int phases, hipStream_t stream);
 
 // -------------------------------------------------------------- pool upload
 constexpr int64_t kScatterElems = 8192;  // elements per workgroup and block

@@ -367,6 +367,74 @@ def apply_grouped(x: torch.Tensor, a_stacks: Sequence[torch.Tensor], b_stacks: S
     return True
 
 
+def rmsnorm_apply_grouped(x: torch.Tensor, weight: torch.Tensor, eps: float, y: torch.Tensor,
+                          a_stacks: Sequence[torch.Tensor], b_stacks: Sequence[torch.Tensor],
+                          meta: KernelInputMetaData, out: torch.Tensor, out_cols: Sequence[int],
+                          workspace: Optional[LinkedWorkspace] = None, phases: int = 3) -> bool:
+    """RMSNorm of ``x`` into ``y`` folded into the slot-grouped apply of LoRA on ``y`` into ``out``.
+
+    Two launches.  The first (``phases`` 1) writes ``y`` (the same bits as
+    ``rmsnorm_fwd``) and the LoRA shrink, which reads ``x`` itself:
+    ``round(x * weight)`` on MFMA, each row's ``rsqrt(mean(x^2) + eps)``
+    applied to its sums.  The second (``phases`` 2) runs the expand into
+    ``out``; a layer runs its base GEMM on ``y`` in between.  Returns False
+    (nothing launched) when the call is not eligible (then run ``rmsnorm_fwd``
+    and ``apply_grouped``): the grouped path's shapes, bf16/fp16, a weight of
+    x's dtype, 16-byte aligned rows.  ``y`` must not overlap ``x``.  In fp16,
+    ``x * weight`` must be finite in fp16 for every element.
+    """
+    _require_gpu(x, "x")
+    dev = x.device
+    n = len(a_stacks)
+    if len(b_stacks) != n or not 1 <= n <= _ffi.MAX_SLICES:
+        raise ValueError("need matching A and B stacks (1..4 slices)")
+    if phases not in (1, 2, 3):
+        raise ValueError(f"phases {phases} not in 1..3")
+    if x.dim() != 2 or x.stride(1) != 1 or out.dim() != 2 or out.stride(1) != 1:
+        return False
+    if x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype or weight.dim() != 1:
+        return False
+    if y.dim() != 2 or y.stride(1) != 1 or y.shape != x.shape or y.dtype != x.dtype or y.device != dev:
+        raise ValueError("y must be a row-contiguous tensor of x's shape, dtype and device")
+    in_dim, r_max = x.shape[1], a_stacks[0].shape[1]
+    if weight.shape[0] != in_dim or weight.stride(0) != 1 or weight.device != dev:
+        raise ValueError(f"weight must be a contiguous [{in_dim}] tensor on x's device")
+    for i, (a, b) in enumerate(zip(a_stacks, b_stacks)):
+        _check_stack(a, f"A[{i}]", x.dtype, dev)
+        _check_stack(b, f"B[{i}]", x.dtype, dev)
+        if a.shape[1] != r_max or a.shape[2] != in_dim or b.shape[2] != r_max:
+            raise ValueError(f"slice {i}: A {tuple(a.shape)} / B {tuple(b.shape)} do not match r_max={r_max}, in={in_dim}")
+        if out_cols[i] < 0 or out_cols[i] + b.shape[1] > out.shape[1]:
+            raise ValueError(f"slice {i}: columns outside the output")
+    if out.shape[0] < x.shape[0] or out.dtype != x.dtype or out.device != dev:
+        raise ValueError("output must cover x's rows with x's dtype and device")
+    lib = _ffi.lib()
+    dt = _ffi.dtype_code(x.dtype)
+    m, keep = seg_meta(meta, dev, min(min(a.shape[0] for a in a_stacks), min(b.shape[0] for b in b_stacks)))
+    if m.plan is None:
+        _device_plan(meta, m, x.shape[0], dev)
+    key = (in_dim, r_max, n, x.shape[0], m.num_slots, dt, 2)
+    need = _GROUPED_WS_BYTES.get(key)
+    if need is None:
+        if len(_GROUPED_WS_BYTES) >= 4096:
+            _GROUPED_WS_BYTES.clear()
+        need = _GROUPED_WS_BYTES[key] = lib.mlora_grouped_workspace_bytes(*key)
+    if need == 0:
+        return False
+    stream = _ffi.stream_ptr(dev)
+    ws_ptr, ws_bytes = (workspace or _default_workspace(dev, linked=True)).get(need, dev, stream or 0)
+    sl = _slices(a_stacks, b_stacks, out_cols)
+    rc = lib.mlora_rmsnorm_apply_grouped(
+        x.data_ptr(), x.stride(0), x.shape[0], in_dim, weight.data_ptr(), float(eps), y.data_ptr(), y.stride(0), sl,
+        n, r_max, out.data_ptr(), out.stride(0), ctypes.byref(m), dt, ws_ptr, ws_bytes, int(phases), stream,
+    )
+    del keep
+    if rc == -2:
+        return False
+    _ffi.check(rc, "mlora_rmsnorm_apply_grouped")
+    return True
+
+
 def build_plan_device(meta: KernelInputMetaData, num_rows: int, num_slots: int, cap: Optional[int] = None) -> torch.Tensor:
     """The table's plan built on the device (``mlora_build_plan``) into a new int32 tensor."""
     dev = meta.seg_indptr.device

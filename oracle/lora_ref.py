@@ -148,13 +148,16 @@ def apply_kernel_numerics(
     meta: KernelInputMetaData,
     base: torch.Tensor,
     col_offsets: Optional[Sequence[int]] = None,
+    shrink_input: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """The GPU kernels' rounding sequence on the CPU; returns ``(mid, out)`` in the storage dtype.
 
     fp32 accumulation in float64 here (the kernels' fp32 sums differ from it
     only in summation order), ``mid`` rounded to the storage dtype, delta
     scaled in fp32 and rounded, then added to the residual in fp32 and
-    rounded again.
+    rounded again.  ``shrink_input``: float64 rows the shrink multiplies
+    with A in place of x (the fused RMSNorm form's
+    ``rmsnorm_ref.rmsnorm_shrink_input``); the storage dtype stays x's.
     """
     dt = x.dtype
     r_max = a_stacks[0].shape[1]
@@ -162,7 +165,7 @@ def apply_kernel_numerics(
         col_offsets = _consecutive(b_stacks)
     mid = torch.zeros(x.shape[0], len(a_stacks) * r_max, dtype=torch.float32)
     out = base.detach().cpu().float().clone()
-    x64 = x.detach().cpu().double()
+    x64 = x.detach().cpu().double() if shrink_input is None else shrink_input.detach().cpu().double()
     for start, end, slot, r, sc in segments(meta, r_max=r_max):
         scale = float(torch.tensor(sc, dtype=torch.float32))
         for s, (a, b, c0) in enumerate(zip(a_stacks, b_stacks, col_offsets)):

@@ -527,7 +527,7 @@ def test_slices_not_multiples_of_the_expand_tile(dev, mode):
 
 
 def test_abi_version(dev):
-    assert _ffi.lib().mlora_abi_version() == _ffi.ABI_VERSION == 5
+    assert _ffi.lib().mlora_abi_version() == _ffi.ABI_VERSION == 6
 
 
 def test_largest_supported_shape(dev):

@@ -246,3 +246,67 @@ def test_add_rmsnorm_closed_forms():
     ints = torch.randint(-64, 64, (5, 64), generator=g).bfloat16()
     h, _ = add_rmsnorm_ref(ints, ints, w, 1e-5)
     assert torch.equal(h, (2 * ints.float()).bfloat16())
+
+
+# ------------------------------------------- RMSNorm folded into the shrink
+def _rows_at_scales(n, k, seed, lo=-2.0, hi=2.0):
+    """n rows of k N(0,1) values, row i scaled by 10**u with u uniform in [lo, hi]."""
+    g = torch.Generator().manual_seed(seed)
+    scale = 10.0 ** (torch.rand(n, 1, generator=g) * (hi - lo) + lo)
+    return (torch.randn(n, k, generator=g) * scale).bfloat16(), g
+
+
+def test_rmsnorm_shrink_input_closed_form_constant_rows():
+    """Row of constant c and w = 1: round(c * 1) = c, so the input is c / sqrt(c^2 + eps)."""
+    from oracle.rmsnorm_ref import rmsnorm_shrink_input
+
+    for c in (0.5, -3.0, 1e-3, 96.0):
+        x = torch.full((3, 32), c).bfloat16()
+        want = float(x[0, 0]) / math.sqrt(float(x[0, 0]) ** 2 + 1e-5)
+        got = rmsnorm_shrink_input(x, torch.ones(32).bfloat16(), 1e-5)
+        assert torch.allclose(got, torch.full((3, 32), want, dtype=torch.float64), rtol=0, atol=1e-12)
+
+
+def test_rmsnorm_shrink_input_is_rmsnorm_up_to_one_rounding():
+    """Against the float64 RMSNorm, the fused shrink input differs only by the
+    rounding of x * w to bf16: relative error at most 2^-8 per element, over
+    rows whose scales span four decades (so a missing or misplaced rstd shows)."""
+    from oracle.rmsnorm_ref import rmsnorm_f64, rmsnorm_shrink_input
+
+    x, g = _rows_at_scales(48, 512, 7)
+    w = (torch.randn(512, generator=g) * 0.3 + 2.0).bfloat16()
+    got = rmsnorm_shrink_input(x, w, 1e-5)
+    want = rmsnorm_f64(x, w, 1e-5)
+    rel = ((got - want).abs() / want.abs().clamp_min(1e-30)).max().item()
+    assert rel <= 2.0 ** -8, rel
+
+    # Planted mistakes fail the same bound: no rstd at all, rstd taken from
+    # x * w instead of x, and the mean over a wrong count (a dropped column).
+    xw = (x.float() * w.float()).bfloat16().double()
+    x64 = x.double()
+    mutants = {
+        "no rstd": xw,
+        "rstd of x*w": xw / torch.sqrt((xw * xw).mean(-1, keepdim=True) + 1e-5),
+        "mean over k-1": xw / torch.sqrt((x64 * x64).sum(-1, keepdim=True) / 511 + 1e-5),
+    }
+    for name, m in mutants.items():
+        r = ((m - want).abs() / want.abs().clamp_min(1e-30)).max().item()
+        assert r > 2.0 ** -8, name
+
+
+def test_fused_rmsnorm_lora_numerics_match_closed_form():
+    """The fused form's rounding sequence (the shrink on rmsnorm_shrink_input)
+    stays within the bf16 tolerance of float64 RMSNorm followed by the LoRA
+    closed form, on rows at scales over four decades."""
+    from oracle.rmsnorm_ref import rmsnorm_f64, rmsnorm_shrink_input
+
+    wl = cpu_small(dtype=torch.bfloat16)
+    x, g = _rows_at_scales(wl.x.shape[0], wl.x.shape[1], 11)
+    w = (torch.randn(wl.x.shape[1], generator=g) * 0.1 + 1.0).bfloat16()
+    _, out = apply_kernel_numerics(x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base,
+                                   shrink_input=rmsnorm_shrink_input(x, w, 1e-5))
+    ref = apply_f64(rmsnorm_f64(x, w, 1e-5), wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
+    torch.testing.assert_close(out.double(), ref, atol=2e-2, rtol=1e-2)
+    # fed x itself instead, the sequence misses the closed form
+    _, bad = apply_kernel_numerics(x, wl.a_stacks, wl.b_stacks, wl.meta, wl.base)
+    assert not torch.allclose(bad.double(), ref, atol=2e-2, rtol=1e-2)

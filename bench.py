@@ -496,7 +496,8 @@ def bench_other(args) -> int:
     import torch
 
     from multi_lora_amd import HipLoRABackend, synthetic
-    from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, Workspace, apply_grouped, expand, shrink
+    from multi_lora_amd.kernels.lora_ops import (LinkedWorkspace, Workspace, apply_grouped, expand,
+                                                 rmsnorm_apply_grouped, shrink)
     from multi_lora_amd.kernels.rmsnorm import rmsnorm_fwd
 
     dev = torch.device("cuda", 0)
@@ -573,7 +574,12 @@ def bench_other(args) -> int:
             _, a, b, out = reps[i % n_rep]
             assert apply_grouped(xn[i % n_rep], a, b, meta, out, cols, be.linked_workspace, mode=1)
 
+        def fused_norm(i):
+            x, a, b, out = reps[i % n_rep]
+            assert rmsnorm_apply_grouped(x, w, eps, xn[i % n_rep], a, b, meta, out, cols, be.linked_workspace)
+
         parts = {"rmsnorm": (norm, norm_bytes),
+                 "rmsnorm folded into the planned decode's shrink launch (two launches)": (fused_norm, total_bytes),
                  "planned decode (3 slices, the library's choice of schedule)": (lora, lora_bytes),
                  "planned decode, one launch (schedule comparison)": (lora_one, lora_bytes),
                  "planned decode, two launches (schedule comparison)": (lora_two, lora_bytes),
@@ -1300,6 +1306,8 @@ OTHER_CONFIGS = {
     "c3_prefill_gate_up": ("prefill_gate_up", "HipLoRABackend.apply_lora_multi, gate|up (two slices)"),
     "c3_prefill_down": ("prefill_down", "HipLoRABackend.apply_lora_multi"),
     "c4_rmsnorm_qkv": ("decode_qkv", "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi over q|k|v"),
+    "c4_rmsnorm_qkv_fused": ("decode_qkv", "HipLoRABackend.rmsnorm_apply_lora_multi over q|k|v (the RMSNorm in the "
+                                           "LoRA shrink's launch)"),
     "c5_qkv": ("c5_qkv", "HipLoRABackend.apply_lora_multi over q|k|v, one layer's call"),
     "c5_o": ("c5_o", "HipLoRABackend.apply_lora_multi, one layer's call"),
     "c5_gate_up": ("c5_gate_up", "HipLoRABackend.apply_lora_multi over gate|up, one layer's call"),
@@ -1336,8 +1344,11 @@ def other_configs(regions: int = 7) -> dict:
             eps = host.extra["eps"]
             nbytes += 2 * host.x.numel() * host.x.element_size() + w.numel() * w.element_size()
 
-        def step(i, reps=reps, be=be, cols=cols, w=w):
+        def step(i, reps=reps, be=be, cols=cols, w=w, fused=key.endswith("_fused")):
             x, a, b, out = reps[i % len(reps)]
+            if fused:
+                be.rmsnorm_apply_lora_multi(x, w, eps, a, b, out, cols)
+                return
             if w is not None:
                 x = rmsnorm_fwd(x, w, eps)
             be.apply_lora_multi(x, a, b, out, cols)

@@ -251,12 +251,12 @@ int mlora_apply_grouped_static(const void* x, int64_t x_row_stride, int32_t num_
  *   out[t, out_col_s + n] += round(scaling * round(rstd_t * (round(x[t] * w) . A_s[slot,:rank]))
  *                                  . B_s[slot, n, :rank])
  * The first launch (phases & 1) writes y, the same bits mlora_rmsnorm writes,
- * and the shrink's K-chunk sums: the shrink reads x once and multiplies
- * round(x * w) with A on MFMA, keeping each row's sum of x^2 per chunk, so it
- * needs no y and no pass before it.  The second launch (phases & 2) adds a
- * row's sums, rstd_t = rsqrt(sum of x^2 / in_dim + eps) scales them before the
- * reference's `mid` rounding, and the expand follows as in
- * mlora_apply_grouped.  In a layer the base GEMM on y runs between the two
+ * with each row's rstd_t = rsqrt(mean(x[t]^2) + eps) kept in the workspace,
+ * and the shrink's K-chunk sums: the shrink reads x and multiplies
+ * round(x * w) with A on MFMA, so it needs no y and no pass before it.  The
+ * second launch (phases & 2) adds a row's chunk sums, scales them by rstd_t
+ * before the reference's `mid` rounding, and runs the expand as
+ * mlora_apply_grouped does.  In a layer the base GEMM on y runs between the two
  * halves (phases 1, GEMM, phases 2), since the expand adds into its output.
  * Against the unfused path (mlora_rmsnorm, then mlora_apply_grouped on y)
  * only the rounding of the MFMA inputs differs (round(x * w) scaled after

@@ -5,16 +5,20 @@ with the same methods and the same int32 coercion of the segment table, but
 with no fallback: a CPU tensor or a missing library raises.  Besides the
 reference's ``run_lora_a_sgemm`` / ``run_lora_b_sgemm`` / ``apply_lora`` it
 offers ``apply_lora_multi`` for fused projections (q|k|v, gate|up): one
-shrink that reads x once and one expand over all slices.
+shrink that reads x once and one expand over all slices, and
+``rmsnorm_apply_lora_multi``, which folds the RMSNorm in front of such a
+projection into the LoRA shrink's launch.
 """
 
 from __future__ import annotations
 
-from typing import List, Optional, Sequence
+from typing import Callable, List, Optional, Sequence
 
 import torch
 
-from ..kernels.lora_ops import GROUPED_MAX_LEN, LinkedWorkspace, Workspace, apply_grouped, apply_segments, expand, shrink
+from ..kernels.lora_ops import (GROUPED_MAX_LEN, LinkedWorkspace, Workspace, apply_grouped, apply_segments, expand,
+                                 rmsnorm_apply_grouped, shrink)
+from ..kernels.rmsnorm import rmsnorm_fwd
 from .base import LoRABackend
 
 
@@ -89,3 +93,48 @@ class HipLoRABackend(LoRABackend):
         ):
             return base_output
         return apply_segments(x, a_stacks, b_stacks, meta, base_output, col_offsets, workspace=self.workspace)
+
+    def rmsnorm_apply_lora_multi(
+        self,
+        x: torch.Tensor,
+        weight: torch.Tensor,
+        eps: float,
+        a_stacks: Sequence[torch.Tensor],
+        b_stacks: Sequence[torch.Tensor],
+        base_output: torch.Tensor,
+        col_offsets: Optional[List[int]] = None,
+        base_fn: Optional[Callable[[torch.Tensor, torch.Tensor], None]] = None,
+    ) -> torch.Tensor:
+        """``y = RMSNorm(x)``, then ``base_fn(y, base_output)`` if given (the
+        base projection writing ``base_output``), then every slice's LoRA
+        delta of ``y`` added into ``base_output``; returns ``y``.
+
+        Decode-shaped batches run the RMSNorm inside the LoRA shrink's launch
+        (``mlora_rmsnorm_apply_grouped``: x read once, no RMSNorm launch of
+        its own, y the same bits as ``rmsnorm_fwd``); the delta then differs
+        from LoRA on y only in the rounding of the shrink's inputs.  Other
+        batches run ``rmsnorm_fwd`` and ``apply_lora_multi``.
+        """
+        meta = self._meta()
+        if x.dim() != 2:
+            raise ValueError("HipLoRABackend expects x [S, in]")
+        if col_offsets is None:
+            col_offsets, c = [], 0
+            for b in b_stacks:
+                col_offsets.append(c)
+                c += b.shape[1]
+        x = x.contiguous()
+        a_stacks = [a.contiguous() for a in a_stacks]
+        b_stacks = [b.contiguous() for b in b_stacks]
+        y = torch.empty_like(x)
+        args = (x, weight, eps, y, a_stacks, b_stacks, meta, base_output, col_offsets, self.linked_workspace)
+        if meta.max_len <= GROUPED_MAX_LEN and rmsnorm_apply_grouped(*args, phases=1):
+            if base_fn is not None:
+                base_fn(y, base_output)
+            rmsnorm_apply_grouped(*args, phases=2)
+            return y
+        y = rmsnorm_fwd(x, weight, eps)
+        if base_fn is not None:
+            base_fn(y, base_output)
+        self.apply_lora_multi(y, a_stacks, b_stacks, base_output, col_offsets)
+        return y

@@ -472,7 +472,7 @@ static int apply_grouped_impl(const void* x, int64_t x_row_stride, int32_t num_r
   if (norm != nullptr) {
     mlora::NormShrinkArgs na{};
     na.rms = norm_rms_args(*norm, x, x_row_stride, num_rows, in_dim, dtype);
-    na.sumsq = reinterpret_cast<float*>(ws + sh.sumsq_off);
+    na.rstd = reinterpret_cast<float*>(ws + sh.rstd_off);
     const hipError_t e = mlora::launch_planned_norm(plan, args, na, dtype, sh.nbt, phases, st);
     if (e != hipSuccess) return hip_fail(e, "fused RMSNorm grouped launch");
     return 0;

@@ -50,10 +50,10 @@
 // the same sums (bit-identical results); the kernel boundary orders them.
 //
 // Fused RMSNorm (two launches): the shrink launch also holds the RMSNorm of
-// the call's rows (the RMSNorm kernel's row body, so the same y), and its
-// shrink items multiply round(x * w) instead of y, storing each row's sum of
-// x^2 per K chunk; the expand items scale a row's summed chunks by its
-// rsqrt(mean(x^2) + eps) before the mid rounding.
+// the call's rows (the RMSNorm kernel's row body, so the same y, and each
+// row's rsqrt(mean(x^2) + eps) stored), and its shrink items multiply
+// round(x * w) instead of y; the expand items scale a row's summed chunks by
+// that rstd before the mid rounding.
 #include "kernels.h"
 #include "loads.h"
 #include "rmsnorm_row.h"
@@ -190,12 +190,10 @@ __device__ __forceinline__ int64_t sum_index(const DecodeArgs& a, int pos, int c
 // the single launch keeps four workgroups a CU without spilling (q|k|v at
 // rank 16: 12.6 vs 14.0 us at 64 tokens, 19.2 vs 20.9 at 256).
 // NORM (the fused RMSNorm launch): the MFMA takes round(x * w) with the
-// RMSNorm weight nw, and the chunk's fp32 sum of x^2 of each row goes to
-// sumsq[pos + row][c] (slice group 0; ssl: 48 floats of LDS).
+// RMSNorm weight nw.
 template <class T, int NBT, int SP, bool LEAN = false, bool NORM = false>
 __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xrow, int sg, int c,
-                             f32x4 (*red)[kWave], uint64_t flag, const typename T::raw_t* nw = nullptr,
-                             float* sumsq = nullptr, float* ssl = nullptr) {
+                             f32x4 (*red)[kWave], uint64_t flag, const typename T::raw_t* nw = nullptr) {
   static_assert(!(NORM && LEAN), "the fused RMSNorm shrink has no recompute path");
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -232,7 +230,6 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
   f32x4 acc[NBT];
 #pragma unroll
   for (int j = 0; j < NBT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float ss = 0.f;  // NORM: this lane's sum of x^2
   if constexpr (!LEAN) {
     u32x4 af[SP][NBT];
 #pragma unroll
@@ -269,11 +266,7 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
       for (int sp = 0; sp < SP; ++sp) {
         float f[VEC];
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          const float v = chunk_elem<T>(xv[sp], q);
-          ss += v * v;
-          f[q] = v * chunk_elem<T>(wv[sp], q);
-        }
+        for (int q = 0; q < VEC; ++q) f[q] = chunk_elem<T>(xv[sp], q) * chunk_elem<T>(wv[sp], q);
         xv[sp] = pack_chunk<T>(f);
       }
     }
@@ -305,12 +298,6 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
     }
   }
   MLORA_STAMP_AFTER_LOADS(2);
-  if constexpr (NORM) {
-    // Lanes r16 + 16 g hold row r16's elements of the chunk.
-    ss += __shfl_xor(ss, 16, kWave);
-    ss += __shfl_xor(ss, 32, kWave);
-    if (wave > 0 && g == 0) ssl[(wave - 1) * 16 + r16] = ss;
-  }
   if (wave > 0) {
 #pragma unroll
     for (int j = 0; j < NBT; ++j)
@@ -336,10 +323,6 @@ __device__ void shrink_chunk(const DecodeArgs& a, int e, const Entry& en, int xr
         *reinterpret_cast<f32x4*>(a.partials + sum_index(a, en.pos + r16, c, (s_first + sl) * a.r_max + n)) = acc[j];
       }
     }
-    if constexpr (NORM) {
-      const float tot = ((ss + ssl[r16]) + ssl[16 + r16]) + ssl[32 + r16];
-      if (sg == 0 && g == 0 && r16 < en.nr) sumsq[static_cast<int64_t>(en.pos + r16) * a.kc + c] = tot;
-    }
     if (flag != 0) {
       // The flag goes out only once every sum of the chunk has reached the L2.
       asm volatile("" ::: "memory");
@@ -360,7 +343,6 @@ struct DecodeLds {
   raw ytile[16 * (kGroupMaxRank + T::VEC)];
   f32x4 part[kGroups][16][kGroupMaxRank / 4];  // per chunk group: sums of each (row, 4 columns)
   uint64_t missing;                             // chunks not received
-  float rstd[16];                               // fused RMSNorm: each row's rsqrt(mean(x^2) + eps)
 };
 
 // 16 bytes of the workspace at byte offset `off`, read past the L1 (sc1):
@@ -375,11 +357,8 @@ __device__ __forceinline__ u32x4 load16_l2(__amdgpu_buffer_rsrc_t rsrc, int64_t 
 // requested together.  The mapping uses shifts only: the item's set-up is
 // on the decode path's critical chain, and every instruction a wave issues
 // there costs about 4 cycles at four waves a SIMD.
-// NORM: wave 3 also adds each row's sums of x^2 (sumsq, chunk order) and
-// keeps rsqrt(ss / in_dim + eps) in lds.rstd.
-template <class T, int WN, bool NORM = false>
-__device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeLds<T, WN>& lds,
-                            const float* sumsq = nullptr, float eps = 0.f) {
+template <class T, int WN>
+__device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeLds<T, WN>& lds) {
   static_assert(kGroups == 4 && kGroupMaxRank / 4 <= 16, "one chunk group per wave, at most 16 quads a row");
   const int quads = (en.rank + 3) >> 2;
   const int per = (a.kc + kGroups - 1) / kGroups;  // chunks per group
@@ -406,22 +385,6 @@ __device__ void gather_sums(const DecodeArgs& a, const Entry& en, int s, DecodeL
     }
     lds.part[grp][row][q] = sum;
   }
-  if constexpr (NORM) {
-    const int l = threadIdx.x & 63;
-    if (grp == kGroups - 1 && l < en.nr) {
-      const float* sq = sumsq + static_cast<int64_t>(en.pos + l) * a.kc;
-      float t = 0.f;
-      for (int cb = 0; cb < a.kc; cb += 4) {
-        float v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = sq[min(cb + k, a.kc - 1)];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (cb + k < a.kc) t += v[k];
-      }
-      lds.rstd[l] = rsqrtf(t / static_cast<float>(a.in_dim) + eps);
-    }
-  }
   lds_barrier();
 }
 
@@ -438,11 +401,12 @@ struct ExpandRows {
 // words from this launch's shrink items (or are computed here), else as
 // fp32 from the previous launch.
 // NORM (expand half of the fused RMSNorm launch): y = round(rstd * sum),
-// with each row's rstd from the shrink's sums of x^2.
+// with the rstd of the thread's row t / 16 (table row yrow_raw) requested
+// with B and the output rows.
 template <class T, int NBT, int SP, int WN, int RS, bool LINKED, bool NORM = false>
 __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, const Entry& en, int nt_g,
                              const int (&orow_raw)[ExpandRows<T, WN>::RPT], DecodeLds<T, WN>& lds,
-                             f32x4 (*red)[kWave], const float* sumsq = nullptr, float eps = 0.f) {
+                             f32x4 (*red)[kWave], const float* rstd = nullptr, int yrow_raw = 0) {
   static_assert(!(NORM && LINKED), "the fused RMSNorm path runs as two launches");
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
@@ -509,6 +473,10 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
   // item by as much (measured: +0.5 us per 0.5 us of delay).
   load_b();
   load_out();
+  // The rstd of the row whose y this thread forms below: one load, issued
+  // before the sums, so the gather's wait covers it.
+  float rs = 1.f;
+  if constexpr (NORM) rs = rstd[clamp_row(yrow_raw, a.rows)];
   MLORA_STAMP(2);
 
   if constexpr (LINKED) {
@@ -559,7 +527,7 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
       load_out();
     }
   }
-  gather_sums<T, WN, NORM>(a, en, s, lds, sumsq, eps);
+  gather_sums<T, WN>(a, en, s, lds);
   MLORA_STAMP(4);
   fence_regs(bf);
 
@@ -575,9 +543,8 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
 #pragma unroll
         for (int grp = 0; grp < kGroups; ++grp) sum += lds.part[grp][row][c4 / 4];
         if constexpr (NORM) {
-          const float r = lds.rstd[row];
 #pragma unroll
-          for (int q2 = 0; q2 < 4; ++q2) sum[q2] *= r;
+          for (int q2 = 0; q2 < 4; ++q2) sum[q2] *= rs;
         }
       }
       raw* y = lds.ytile + row * YS + c4;
@@ -638,8 +605,7 @@ __device__ void expand_entry(const DecodeArgs& a, const int32_t* plan, int e, co
 // and this thread's row word, already requested.
 template <class T, int NBT, int SCHED, bool NORM = false>
 __device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, int item, int n_ent, Entry en,
-                             int xrow_raw, f32x4 (*red)[kWave], const typename T::raw_t* nw = nullptr,
-                             float* sumsq = nullptr, float* ssl = nullptr) {
+                             int xrow_raw, f32x4 (*red)[kWave], const typename T::raw_t* nw = nullptr) {
   constexpr int SP = kGroupStepsLinked;
   int sg = 0, c = item;
   if (a.s_groups != 1) {
@@ -651,14 +617,14 @@ __device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, in
   // grid smaller than the plan), so nothing the loop hoists runs before it.
   MLORA_STAMP(1);
   if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
-    shrink_chunk<T, NBT, SP, false, NORM>(a, j, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag, nw, sumsq, ssl);
+    shrink_chunk<T, NBT, SP, false, NORM>(a, j, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag, nw);
   else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0)
     atomicAdd(a.header + kWsPlanErrors, 1);
   for (int e = j + a.e_grid; e < n_ent; e += a.e_grid) {
     xrow_raw = load_entry_row(plan, e, threadIdx.x & 15);
     en = load_entry(plan, e, a.r_max, a.num_slots);
     if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
-      shrink_chunk<T, NBT, SP, false, NORM>(a, e, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag, nw, sumsq, ssl);
+      shrink_chunk<T, NBT, SP, false, NORM>(a, e, en, clamp_row(xrow_raw, a.rows), sg, c, red, flag, nw);
     else if (en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && item == 0)
       atomicAdd(a.header + kWsPlanErrors, 1);
   }
@@ -667,23 +633,26 @@ __device__ void shrink_items(const int32_t* plan, const DecodeArgs& a, int j, in
 // Expand items (column tile `tile`) of entries j, j + e_grid, ...;
 // count_errors: this launch has no shrink items, so tile 0 reports entries
 // it cannot take.
+// NORM: rstd holds each table row's rstd; yrow_raw is the row word of entry
+// j's row threadIdx.x / 16.
 template <class T, int NBT, int WN, int RS, int SCHED, bool NORM = false>
 __device__ void expand_items(const int32_t* plan, const DecodeArgs& a, int j, int tile, int n_ent, Entry en,
                              int (&rows_raw)[ExpandRows<T, WN>::RPT], DecodeLds<T, WN>& lds, f32x4 (*red)[kWave],
-                             bool count_errors, const float* sumsq = nullptr, float eps = 0.f) {
+                             bool count_errors, const float* rstd = nullptr, int yrow_raw = 0) {
   constexpr int SP = kGroupStepsLinked;
   constexpr int RPT = ExpandRows<T, WN>::RPT;
   for (int e = j;;) {
     MLORA_STAMP(1);
     if (en.rank > 0 && en.nr > 0 && en.pos >= 0 && en.pos + en.nr <= a.ws_rows)
-      expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked, NORM>(a, plan, e, en, tile, rows_raw, lds, red, sumsq,
-                                                                      eps);
+      expand_entry<T, NBT, SP, WN, RS, SCHED == kGroupLinked, NORM>(a, plan, e, en, tile, rows_raw, lds, red, rstd,
+                                                                      yrow_raw);
     else if (count_errors && en.rank > 0 && en.nr > 0 && threadIdx.x == 0 && tile == 0)
       atomicAdd(a.header + kWsPlanErrors, 1);
     e += a.e_grid;
     if (e >= n_ent) break;
 #pragma unroll
     for (int i = 0; i < RPT; ++i) rows_raw[i] = load_entry_row(plan, e, ExpandRows<T, WN>::row_of(threadIdx.x, i));
+    if constexpr (NORM) yrow_raw = load_entry_row(plan, e, threadIdx.x >> 4);
     en = load_entry(plan, e, a.r_max, a.num_slots);
   }
 }
@@ -795,44 +764,55 @@ hipError_t launch_dtype(const int32_t* plan, const DecodeArgs& a, int nbt, int m
 }
 
 // ------------------------------------------- fused RMSNorm + decode shrink
-// Shrink launch: grid (e_grid, n_shrink + norm rows).  Items [0, n_shrink)
-// are the shrink items of the two-launch schedule, with x * w on the MFMA
-// and the rows' sums of x^2 stored; workgroup (j, n_shrink + i) is RMSNorm
-// row block i * e_grid + j (256 / tpr rows), written as the RMSNorm kernel
-// writes it.  Nothing in the launch waits on another workgroup.
+// Shrink launch: grid (e_grid, norm rows + n_shrink).  Workgroup (j, i)
+// for i < n_norm is RMSNorm row block i * e_grid + j (256 / tpr rows),
+// written as the RMSNorm kernel writes it, with each row's rstd stored; the
+// items after them are the shrink items of the two-launch schedule, with
+// round(x * w) on the MFMA.  The norm rows come first in the grid, so they
+// run beside the first shrink items instead of after the last.  Nothing in
+// the launch waits on another workgroup.
 template <class T, int NBT>
 __global__ __launch_bounds__(256, NBT >= 8 ? 2 : 4) void planned_norm_shrink_kernel(const int32_t* __restrict__ plan,
-                                                                                     int plan_cap, int n_shrink,
+                                                                                     int plan_cap, int n_norm,
                                                                                      DecodeArgs a, NormShrinkArgs na) {
   __shared__ f32x4 red[3 * NBT][kWave];
-  __shared__ float ssl[3 * 16];
+  __shared__ float nred[4];
   const int j = blockIdx.x;
-  const int item = blockIdx.y;
-  if (item >= n_shrink) {
-    const int64_t blk = static_cast<int64_t>(item - n_shrink) * gridDim.x + j;
+  const int item = static_cast<int>(blockIdx.y) - n_norm;
+  if (item < 0) {
+    const int64_t blk = static_cast<int64_t>(blockIdx.y) * gridDim.x + j;
     // At most two chunks a thread held (the rest streamed twice): the same
     // chunks in the same order as the RMSNorm kernel's, so the same bits.
     if (blk * (256 / na.rms.tpr) < na.rms.rows)
-      rmsnorm_block<T, 2, true, true, false>(na.rms, blk, ssl, min(na.rms.nc, 2));
+      rmsnorm_block<T, 2, true, true, false, true>(na.rms, blk, nred, min(na.rms.nc, 2), na.rstd);
     return;
   }
   const int ef = min(j, plan_cap - 1);
   const int row_raw = load_entry_row(plan, ef, threadIdx.x & 15);
   const Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
   const int p0 = plan[0];
+  {
+    // As in planned_kernel: every line of the kernel arguments is touched in
+    // the round trip that brings the entry.
+    const char* ks = (const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int kLines = static_cast<int>((sizeof(DecodeArgs) + sizeof(NormShrinkArgs) + 16 + 63) / 64);
+    int acc = 0;
+#pragma unroll
+    for (int i = 0; i < kLines; ++i) acc |= *reinterpret_cast<const int*>(ks + i * 64);
+    asm volatile("" ::"s"(acc), "s"(p0), "s"(en.slot), "s"(en.rank), "s"(en.nr), "s"(en.pos));
+  }
   const int n_ent = min(p0, min(plan_cap, a.e_cap));
   if (j == 0 && item == 0 && threadIdx.x == 0 && p0 > min(plan_cap, a.e_cap)) atomicAdd(a.header + kWsPlanErrors, 1);
   if (j < n_ent)
     shrink_items<T, NBT, kGroupShrinkOnly, true>(plan, a, j, item, n_ent, en, row_raw, red,
-                                                 static_cast<const typename T::raw_t*>(na.rms.w), na.sumsq, ssl);
+                                                 static_cast<const typename T::raw_t*>(na.rms.w));
 }
 
 // Expand launch: the expand items of the two-launch schedule, y scaled by
 // each row's rstd before its rounding.
 template <class T, int WN, int RS>
 __global__ __launch_bounds__(256, 4) void planned_norm_expand_kernel(const int32_t* __restrict__ plan, int plan_cap,
-                                                                     DecodeArgs a, const float* __restrict__ sumsq,
-                                                                     float eps) {
+                                                                     DecodeArgs a, const float* __restrict__ rstd) {
   __shared__ __attribute__((aligned(16))) DecodeLds<T, WN> lds;
   constexpr int RPT = ExpandRows<T, WN>::RPT;
   const int j = blockIdx.x;
@@ -840,22 +820,37 @@ __global__ __launch_bounds__(256, 4) void planned_norm_expand_kernel(const int32
   int rows_raw[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) rows_raw[i] = load_entry_row(plan, ef, ExpandRows<T, WN>::row_of(threadIdx.x, i));
+  const int yrow_raw = load_entry_row(plan, ef, threadIdx.x >> 4);
   const Entry en = load_entry(plan, ef, a.r_max, a.num_slots);
-  const int n_ent = min(plan[0], min(plan_cap, a.e_cap));
+  const int p0 = plan[0];
+  {
+    // As in planned_kernel: every line of the kernel arguments is touched in
+    // the round trip that brings the entry.
+    const char* ks = (const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int kLines = static_cast<int>((sizeof(DecodeArgs) + 32 + 63) / 64);
+    int acc = 0;
+#pragma unroll
+    for (int i = 0; i < kLines; ++i) acc |= *reinterpret_cast<const int*>(ks + i * 64);
+    asm volatile("" ::"s"(acc), "s"(p0), "s"(en.slot), "s"(en.rank), "s"(en.nr), "s"(en.pos));
+  }
+  const int n_ent = min(p0, min(plan_cap, a.e_cap));
+  if (j == 0 && blockIdx.y == 0 && threadIdx.x == 0 && p0 > min(plan_cap, a.e_cap))
+    atomicAdd(a.header + kWsPlanErrors, 1);
   if (j < n_ent)
     expand_items<T, 1, WN, RS, kGroupExpandOnly, true>(plan, a, j, blockIdx.y, n_ent, en, rows_raw, lds, nullptr,
-                                                       true, sumsq, eps);
+                                                       true, rstd, yrow_raw);
 }
 
 template <class T, int NBT>
 hipError_t launch_norm_shrink(const int32_t* plan, const DecodeArgs& a, const NormShrinkArgs& na, hipStream_t stream) {
   const int n_shrink = a.s_groups * a.kc;
+  if (a.e_grid <= 0 || na.rms.rows <= 0) return hipSuccess;
   const int64_t blocks = (na.rms.rows + (256 / na.rms.tpr) - 1) / (256 / na.rms.tpr);
-  const int64_t items = n_shrink + (blocks + a.e_grid - 1) / a.e_grid;
-  if (a.e_grid <= 0 || blocks <= 0) return hipSuccess;
+  const int64_t n_norm = (blocks + a.e_grid - 1) / a.e_grid;
+  const int64_t items = n_norm + n_shrink;
   if (items > 65535 || !grid_fits(items * a.e_grid)) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((planned_norm_shrink_kernel<T, NBT>), dim3(static_cast<unsigned>(a.e_grid), static_cast<unsigned>(items)),
-                     dim3(256), 0, stream, plan, a.plan_cap, n_shrink, a, na);
+                     dim3(256), 0, stream, plan, a.plan_cap, static_cast<int>(n_norm), a, na);
   return hipGetLastError();
 }
 
@@ -876,10 +871,10 @@ hipError_t launch_norm_t(const int32_t* plan, const DecodeArgs& a, const NormShr
     const dim3 grid(static_cast<unsigned>(a.e_grid), static_cast<unsigned>(a.n_tiles));
     if (a.r_max <= T::KSTEP)
       hipLaunchKernelGGL((planned_norm_expand_kernel<T, 1, 1>), grid, dim3(256), 0, stream, plan, a.plan_cap, a,
-                         na.sumsq, na.rms.eps);
+                         na.rstd);
     else
       hipLaunchKernelGGL((planned_norm_expand_kernel<T, 1, 2>), grid, dim3(256), 0, stream, plan, a.plan_cap, a,
-                         na.sumsq, na.rms.eps);
+                         na.rstd);
     return hipGetLastError();
   }
   return hipSuccess;
@@ -1066,9 +1061,9 @@ bool plan_decode(int in_dim, int r_max, int n_slices, int rows, int dtype, Decod
   sh->flags_off = kWsHeaderBytes;
   sh->partials_off = sh->flags_off + round256(static_cast<size_t>(sh->e_cap) * sh->s_groups * sh->kc * sizeof(uint64_t));
   sh->plan_off = sh->partials_off + round256(n_sums * sizeof(float));
-  sh->sumsq_off =
+  sh->rstd_off =
       sh->plan_off + round256(sizeof(int32_t) * (kPlanHeaderWords + static_cast<size_t>(sh->e_cap) * kPlanEntryWords));
-  sh->bytes = sh->sumsq_off + sizeof(float) * static_cast<size_t>(rows) * sh->kc;
+  sh->bytes = sh->rstd_off + sizeof(float) * static_cast<size_t>(rows);
   return true;
 }
 

@@ -209,7 +209,7 @@ struct DecodeArgs {
 // shrink items per chunk, and the workspace regions.
 struct DecodeShape {
   int kc, k_chunk, nbt, s_groups;
-  size_t flags_off, partials_off, plan_off, sumsq_off, bytes;
+  size_t flags_off, partials_off, plan_off, rstd_off, bytes;
   int e_cap;
 };
 bool plan_decode(int in_dim, int r_max, int n_slices, int rows, int dtype, DecodeShape* sh);
@@ -269,16 +269,15 @@ void rmsnorm_shape(int hidden, int dtype, int* tpr, int* nc);
 
 // ------------------------------------------- fused RMSNorm + decode shrink
 // The two-launch planned decode with the RMSNorm of its input rows folded
-// into the shrink launch.  That launch holds the shrink items and, past them
-// in the grid, norm workgroups that write y = RMSNorm(x) for every row (the
-// RMSNorm kernel's rows, same bits).  A shrink item reads the raw x rows and
-// the weight, multiplies on MFMA round(x * w) instead of y, and stores with
-// its chunk sums the chunk's fp32 sum of x^2 for each row; the expand items
-// add a row's sums of squares in chunk order, take rstd = rsqrt(ss / in_dim
-// + eps), and round rstd * sum to the storage type as y . A^T.
+// into the shrink launch.  That launch holds norm workgroups that write
+// y = RMSNorm(x) for every row (the RMSNorm kernel's rows, same bits) and
+// each row's rstd = rsqrt(mean(x^2) + eps), and the shrink items, which read
+// the raw x rows and the weight and multiply round(x * w) with A on MFMA
+// instead of y.  The expand items scale a row's summed chunks by its rstd
+// before rounding them to the storage type as y . A^T.
 struct NormShrinkArgs {
-  RmsArgs rms;   // the call's rows: x, weight (data dtype, 16-byte aligned), y, eps
-  float* sumsq;  // [ws_rows][kc]: per planned row and K chunk, the sum of x^2
+  RmsArgs rms;  // the call's rows: x, weight (data dtype, 16-byte aligned), y, eps
+  float* rstd;  // [rows]: each row's rstd, as the norm rows computed it
 };
 hipError_t launch_planned_norm(const int32_t* plan, const DecodeArgs& args, const NormShrinkArgs& na, int dtype,
                                int nbt, int phases, hipStream_t stream);

@@ -52,9 +52,11 @@ __device__ __forceinline__ u32x4 add_chunk(const u32x4& x, const u32x4& r) {
 // The 256 / tpr rows of row block `block` (256 threads; every thread calls
 // it).  `red`: 4 floats of LDS.  nc <= NC chunks a thread are held in
 // registers (the RMSNorm kernel passes NC itself); rows wider than tpr * nc
-// chunks stream the rest a second time.
-template <class T, int NC, bool AL, bool WV, bool ADD>
-__device__ __forceinline__ void rmsnorm_block(const RmsArgs& a, int64_t block, float* red, int nc = NC) {
+// chunks stream the rest a second time.  RSTD: each row's
+// rsqrt(mean(x^2) + eps) also goes to rstd_out[row].
+template <class T, int NC, bool AL, bool WV, bool ADD, bool RSTD = false>
+__device__ __forceinline__ void rmsnorm_block(const RmsArgs& a, int64_t block, float* red, int nc = NC,
+                                              float* rstd_out = nullptr) {
   using raw = typename T::raw_t;
   constexpr int VEC = T::VEC;
   const int tid = threadIdx.x;
@@ -144,6 +146,9 @@ __device__ __forceinline__ void rmsnorm_block(const RmsArgs& a, int64_t block, f
   }
   if (!row_ok) return;
   const float rstd = rsqrtf(ss / static_cast<float>(hidden) + a.eps);
+  if constexpr (RSTD) {
+    if (li == 0) rstd_out[row] = rstd;
+  }
   raw* yrow = static_cast<raw*>(a.y) + row * a.y_stride;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {

@@ -76,6 +76,8 @@ OTHER_WORKLOADS = {
     "prefill_down": "prefill MLP down 14336->4096, 8 segments of U[64,1024] tokens, ranks {16,32,64}, r_max 64",
     "decode_qkv": "RMSNorm then q|k|v 4096->[4096,1024,1024], 256 one-token segments, 256-slot pool, "
                   "128 rank-32 adapters",
+    "decode_qkv_fused": "RMSNorm folded into the q|k|v LoRA call (mlora_rmsnorm_apply_grouped, two launches): "
+                        "4096->[4096,1024,1024], 256 one-token segments, 256-slot pool, 128 rank-32 adapters",
     "decode_q_resident": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool holding 64 resident "
                          "rank-16 adapters, tokens drawn over 32 of them",
     "decode_q_device_plan": "decode q_proj 4096->4096, 128 one-token segments, 64-slot pool, 32 rank-16 adapters; "
@@ -522,7 +524,7 @@ def bench_other(args) -> int:
     kernels = {}
     calls = max(args.kernel_steps // 8, 128)
 
-    if name == "decode_qkv":
+    if name in ("decode_qkv", "decode_qkv_fused"):
         w = host.extra["norm_weight"].to(dev)
         eps = host.extra["eps"]
         xn = [torch.empty_like(r[0]) for r in reps]
@@ -544,6 +546,9 @@ def bench_other(args) -> int:
 
         def step(i):
             x, a, b, out = reps[i % n_rep]
+            if name == "decode_qkv_fused":
+                be.rmsnorm_apply_lora_multi(x, w, eps, a, b, out, cols)
+                return
             y = rmsnorm_fwd(x, w, eps)
             be.apply_lora_multi(y, a, b, out, cols)
 
@@ -568,7 +573,10 @@ def bench_other(args) -> int:
                                          _ffi.dtype_code(w.dtype), ys[i % n_rep].data_ptr(), in_dim, S, in_dim, eps,
                                          _ffi.dtype_code(x.dtype), _ffi.stream_ptr(dev)), "mlora_rmsnorm")
 
-        total_bytes = lora_bytes + norm_bytes
+        # Fused, x is one input of both the norm rows and the shrink: y written and the weight on top of
+        # the LoRA bytes.  Unfused, the RMSNorm reads x and the LoRA path reads y.
+        fused_bytes = lora_bytes + S * in_dim * e + in_dim * e
+        total_bytes = fused_bytes if name == "decode_qkv_fused" else lora_bytes + norm_bytes
         add_bytes = 4 * S * in_dim * e + in_dim * e
         def lora_one(i):
             _, a, b, out = reps[i % n_rep]
@@ -579,13 +587,15 @@ def bench_other(args) -> int:
             assert rmsnorm_apply_grouped(x, w, eps, xn[i % n_rep], a, b, meta, out, cols, be.linked_workspace)
 
         parts = {"rmsnorm": (norm, norm_bytes),
-                 "rmsnorm folded into the planned decode's shrink launch (two launches)": (fused_norm, total_bytes),
+                 "rmsnorm folded into the planned decode's shrink launch (two launches)": (fused_norm, fused_bytes),
                  "planned decode (3 slices, the library's choice of schedule)": (lora, lora_bytes),
                  "planned decode, one launch (schedule comparison)": (lora_one, lora_bytes),
                  "planned decode, two launches (schedule comparison)": (lora_two, lora_bytes),
                  "add_rmsnorm fused (schedule comparison)": (add_norm, add_bytes),
                  "add then rmsnorm, unfused (schedule comparison)": (add_then_norm, add_bytes)}
-        path = "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-planned decode, the library's schedule)"
+        path = ("HipLoRABackend.rmsnorm_apply_lora_multi (the RMSNorm in the planned decode's shrink launch)"
+                if name == "decode_qkv_fused" else
+                "rmsnorm_fwd, then HipLoRABackend.apply_lora_multi (slot-planned decode, the library's schedule)")
     elif name in GROUPED_WORKLOADS:
         def lora(i):
             x, a, b, out = reps[i % n_rep]
@@ -772,7 +782,7 @@ def cpu_baseline_other(name: str, host, total_bytes: int, budget_s: float) -> di
 # COPY_ELEMS bf16 values (read once, written once).
 COPY_ELEMS = 32 << 20
 PROFILE_CALLS = 64
-GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_q_device_plan", "decode_qkv")
+GROUPED_WORKLOADS = ("decode_q", "decode_q_resident", "decode_q_device_plan", "decode_qkv", "decode_qkv_fused")
 PREFILL_WORKLOADS = ("prefill_gate_up", "prefill_down", "c5_gate_up", "c5_qkv", "c5_o", "c5_down")
 MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
@@ -818,7 +828,8 @@ def traffic_bytes(name: str, prefix: str = ""):
 def profile_traffic(name: str) -> int:
     """PROFILE_CALLS calls of a workload's LoRA path as the backend runs it
     (HipLoRABackend.apply_lora_multi; decode_qkv's input normalised
-    beforehand), over rotating replicas, then a plain copy kernel of known
+    beforehand; decode_qkv_fused: HipLoRABackend.rmsnorm_apply_lora_multi on
+    the raw rows), over rotating replicas, then a plain copy kernel of known
     size.  Meant to run under rocprofv3 --pmc."""
     import torch
 
@@ -834,15 +845,20 @@ def profile_traffic(name: str) -> int:
     n_rep = replicas_for(touched_bytes(host))
     reps = [(host.x.to(dev), [a.to(dev) for a in host.a_stacks], [b.to(dev) for b in host.b_stacks],
              host.base.to(dev)) for _ in range(n_rep)]
+    fused = name == "decode_qkv_fused"
     if "norm_weight" in host.extra:
         w = host.extra["norm_weight"].to(dev)
-        reps = [(rmsnorm_fwd(x, w, host.extra["eps"]), a, b, out) for x, a, b, out in reps]
+        if not fused:
+            reps = [(rmsnorm_fwd(x, w, host.extra["eps"]), a, b, out) for x, a, b, out in reps]
     be = HipLoRABackend()
     be.set_kernel_input_metadata(meta)
     torch.cuda.synchronize()
     for i in range(PROFILE_CALLS):
         x, a, b, out = reps[i % n_rep]
-        be.apply_lora_multi(x, a, b, out, host.col_offsets)
+        if fused:
+            be.rmsnorm_apply_lora_multi(x, w, host.extra["eps"], a, b, out, host.col_offsets)
+        else:
+            be.apply_lora_multi(x, a, b, out, host.col_offsets)
     torch.cuda.synchronize()
     src = torch.randn(COPY_ELEMS, device=dev).bfloat16()
     dst = torch.empty_like(src)
@@ -909,6 +925,13 @@ def summarize_pmc(name: str, dirs) -> int:
     f_scale, w_scale = copy_kib / fetch["copy"], copy_kib / write["copy"]
     host = workload_host(name)
     algo = synthetic.algorithmic_bytes(host)
+    reads = algo - host.base.numel() * host.x.element_size()
+    if name == "decode_qkv_fused":
+        # the RMSNorm's y written and its weight read; x, which the norm rows and the shrink items both
+        # read, is counted once, with the LoRA bytes
+        e = host.x.element_size()
+        algo += host.x.numel() * e + host.extra["norm_weight"].numel() * e
+        reads += host.extra["norm_weight"].numel() * e
     kernels = {}
     for k in sorted(set(fetch["kernels"]) | set(write["kernels"])):
         fb = fetch["kernels"].get(k, 0.0) / PROFILE_CALLS * f_scale * 1024
@@ -942,14 +965,15 @@ def summarize_pmc(name: str, dirs) -> int:
                     + (" <MFMA_DIR>" if len(dirs) > 2 else ""))
     out = {
         "workload": OTHER_WORKLOADS.get(name, HEADLINE_WORKLOAD),
-        "path": "HipLoRABackend.apply_lora_multi, the library's choice of kernels",
+        "path": ("HipLoRABackend.rmsnorm_apply_lora_multi (the RMSNorm in the shrink launch)"
+                 if name == "decode_qkv_fused" else "HipLoRABackend.apply_lora_multi, the library's choice of kernels"),
         "calls": PROFILE_CALLS,
         "algorithmic_bytes_per_call": algo,
         "hbm_bytes_per_call": total_f + total_w,
         "fetch_bytes_per_call": total_f,
         "write_bytes_per_call": total_w,
         "traffic_over_algorithmic": round((total_f + total_w) / algo, 4),
-        "fetch_over_algorithmic_reads": round(total_f / (algo - host.base.numel() * host.x.element_size()), 4),
+        "fetch_over_algorithmic_reads": round(total_f / reads, 4),
         "kernels": kernels,
         "mfma": mfma,
         "copy_calibration": {"bytes_each_way": COPY_ELEMS * 2, "FETCH_SIZE_kib": fetch["copy"],
@@ -1342,7 +1366,9 @@ def other_configs(regions: int = 7) -> dict:
         if w is not None:
             w = w.to(dev)
             eps = host.extra["eps"]
-            nbytes += 2 * host.x.numel() * host.x.element_size() + w.numel() * w.element_size()
+            # unfused: x read by the RMSNorm, y written; fused: y written (x counted once, with the LoRA bytes)
+            n_x = 1 if key.endswith("_fused") else 2
+            nbytes += n_x * host.x.numel() * host.x.element_size() + w.numel() * w.element_size()
 
         def step(i, reps=reps, be=be, cols=cols, w=w, fused=key.endswith("_fused")):
             x, a, b, out = reps[i % len(reps)]

@@ -178,3 +178,52 @@ def test_weight_of_another_dtype_is_not_taken(dev):
     w = torch.ones(1024, device=dev, dtype=torch.float32)
     assert not rmsnorm_apply_grouped(wl.x, w, 1e-5, torch.empty_like(wl.x), wl.a_stacks, wl.b_stacks, wl.meta,
                                      wl.clone_base(), wl.col_offsets)
+
+
+def test_backend_rmsnorm_apply_with_base_projection(dev):
+    """HipLoRABackend.rmsnorm_apply_lora_multi on a decode table: y is the
+    RMSNorm's bits, base_fn writes the base projection of y between the two
+    launches, and the LoRA delta of y is added on top (float64 closed form)."""
+    from multi_lora_amd import HipLoRABackend
+
+    wl = synthetic.decode_qkv(device=dev, tokens=64, seed=14)
+    x, w = scaled(wl.x, 14), wl.extra["norm_weight"]
+    g = torch.Generator().manual_seed(14)
+    wq = (torch.randn(sum(b.shape[1] for b in wl.b_stacks), x.shape[1], generator=g) * 0.02).to(x.dtype).to(dev)
+    out = torch.empty(x.shape[0], wq.shape[0], dtype=x.dtype, device=dev)
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(wl.meta)
+    calls = []
+
+    def base_fn(y, o):
+        calls.append(1)
+        torch.mm(y, wq.t(), out=o)
+
+    y = be.rmsnorm_apply_lora_multi(x, w, 1e-5, wl.a_stacks, wl.b_stacks, out, wl.col_offsets, base_fn=base_fn)
+    torch.cuda.synchronize()
+    assert calls == [1]
+    assert torch.equal(y.cpu(), rmsnorm_fwd(x, w, 1e-5).cpu())
+    base = (y.float() @ wq.float().t()).to(x.dtype).cpu()
+    cm = cpu_meta(wl.meta)
+    want = apply_f64(rmsnorm_f64(x.cpu(), w.cpu(), 1e-5), [a.cpu() for a in wl.a_stacks],
+                     [b.cpu() for b in wl.b_stacks], cm, base, wl.col_offsets)
+    # the base GEMM's own rounding differs from the fp32 product above by a unit of bf16
+    assert_tol_f64(out.cpu(), want, "backend fused call vs float64")
+
+
+def test_backend_rmsnorm_apply_prefill_table_takes_the_unfused_path(dev):
+    """Segments longer than the decode path takes: RMSNorm, then the segment
+    apply on y, bit for bit."""
+    from multi_lora_amd import HipLoRABackend
+
+    wl = workload("prefill", dev, [40, 3, 70], [1, 0, 2], [16, 16, 16], [1.0, 2.0, 0.5], 1024, [512, 128], 16, 15)
+    x, w = scaled(wl.x, 15), norm_weight(1024, wl.x.dtype, dev, 15)
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(wl.meta)
+    got = wl.clone_base()
+    y = be.rmsnorm_apply_lora_multi(x, w, 1e-5, wl.a_stacks, wl.b_stacks, got, wl.col_offsets)
+    ref = wl.clone_base()
+    be.apply_lora_multi(rmsnorm_fwd(x, w, 1e-5), wl.a_stacks, wl.b_stacks, ref, wl.col_offsets)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), rmsnorm_fwd(x, w, 1e-5).cpu())
+    assert torch.equal(got.cpu(), ref.cpu())

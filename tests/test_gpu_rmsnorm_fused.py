@@ -227,3 +227,18 @@ def test_backend_rmsnorm_apply_prefill_table_takes_the_unfused_path(dev):
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), rmsnorm_fwd(x, w, 1e-5).cpu())
     assert torch.equal(got.cpu(), ref.cpu())
+
+
+def test_table_without_plan(dev):
+    """A table with no host plan: each half builds the plan on the device;
+    the same bits as with the table's own plan."""
+    lens = [1] * 48 + [5, 3]
+    g = torch.Generator().manual_seed(16)
+    slots = torch.randint(0, 20, (len(lens),), generator=g).tolist()
+    ranks = [16] * 18 + [0, 0]
+    planned = workload("planned", dev, lens, slots, ranks, [1.0] * 20, 2048, [1024, 256, 256], 16, 16)
+    bare = workload("bare", dev, lens, slots, ranks, [1.0] * 20, 2048, [1024, 256, 256], 16, 16, with_plan=False)
+    x, w = scaled(planned.x, 16), norm_weight(2048, planned.x.dtype, dev, 16)
+    y1, o1 = fused(planned, x, w, 1e-5)
+    y2, o2 = fused(bare, x, w, 1e-5, split=True)
+    assert torch.equal(y1, y2) and torch.equal(o1, o2)

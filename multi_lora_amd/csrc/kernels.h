@@ -47,7 +47,7 @@ struct ShrinkArgs {
 };
 
 struct ShrinkPlan {
-  int bm;         // 16 or 64 token rows per tile
+  int bm;         // token rows per tile: 16, 64, or 128 (streamed kernel only)
   int m_tiles;
   int ks;
   int k_per_split;
@@ -98,6 +98,9 @@ struct ExpandArgs {
 // their output tiles with the non-temporal hint (the tile is read and written
 // once; the hint keeps B and mid, which other tiles read again, in the L2).
 constexpr int kStreamNtTilesPerCu = 6;
+// Reductions of at least this many elements over long segments take the
+// streamed shrink's 128-row tiles.
+constexpr int kLongKRows128 = 8192;
 // Largest r_max, and widest output in 256-column tiles, for which the
 // expand takes split sums.
 constexpr int kFuseMaxRank = 64;

@@ -808,6 +808,8 @@ template <class T, int NBT>
 hipError_t launch_dma(const ShrinkPlan& p, const ShrinkArgs& args, hipStream_t stream) {
   if (p.bm == 64 && p.kt == 64 && p.stages == 3)
     return launch_with<T>(shrink_dma_kernel<T, NBT, 64, 64, 3>, p, args, stream, 256);
+  if (p.bm == 128 && p.kt == 64 && p.stages == 3)
+    return launch_with<T>(shrink_dma_kernel<T, NBT, 64, 128, 3>, p, args, stream, 512);
   return hipErrorInvalidValue;
 }
 
@@ -907,6 +909,17 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
       p.kt = kDmaKt;
       p.stages = kDmaStages;
     }
+    // Long reductions over long segments: 128-row tiles (eight waves), so a
+    // stage carries twice the x rows for the same A rows.  Prefill down
+    // (K 14336, 8 segments of 64..1024 rows): shrink + reduce 33.8 -> 31.0 us
+    // at the same six splits (12 splits, what the tile count below would
+    // give for 128-row tiles, 32.4 us; 256-row tiles 31.2 us at 12 splits, a
+    // fourth stage 31.5 us).  At K 4096 (prefill gate|up) they do not pay
+    // (22.5 vs 22.0 us), and batches of short segments keep 64 rows.
+    if (streamed && in_dim >= kLongKRows128 && rows >= 256LL * bs) {
+      p.bm = 128;
+      p.m_tiles = cdiv(max_len > 0 ? max_len : 1, p.bm);
+    }
     const int unit = streamed ? kDmaKt : kstep;
     const int units = cdiv(in_dim, unit);
     const int ncols = n_slices * r_max;
@@ -931,14 +944,22 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
 }
 
 hipError_t launch_shrink(const ShrinkPlan& plan, ShrinkArgs args, int dtype, bool aligned, hipStream_t stream) {
-  args.m_tiles = plan.m_tiles;
-  args.ks = plan.ks;
-  args.k_per_split = plan.k_per_split;
+  ShrinkPlan p = plan;
+  if (p.bm > 64 && !aligned) {
+    // 128-row tiles are the streamed kernel's, which needs aligned rows; the
+    // register-staged kernels take 64-row tiles, at most twice as many a
+    // segment.
+    p.bm = 64;
+    p.m_tiles *= 2;
+  }
+  args.m_tiles = p.m_tiles;
+  args.ks = p.ks;
+  args.k_per_split = p.k_per_split;
   args.part_cols = args.n_slices * args.r_max;
   switch (dtype) {
-    case MLORA_BF16: return launch_dtype<BF16>(plan, args, aligned, stream);
-    case MLORA_F16: return launch_dtype<F16>(plan, args, aligned, stream);
-    default: return launch_dtype<F32>(plan, args, aligned, stream);
+    case MLORA_BF16: return launch_dtype<BF16>(p, args, aligned, stream);
+    case MLORA_F16: return launch_dtype<F16>(p, args, aligned, stream);
+    default: return launch_dtype<F32>(p, args, aligned, stream);
   }
 }
 

@@ -56,6 +56,9 @@ def case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, seed):
     ("qkv_r64_decode", [1] * 24 + [5], [i % 6 for i in range(25)], [64, 17, 64, 0, 40, 64], 4096, [512, 128, 128],
      64, torch.bfloat16),
     ("qkv_r64_long", [150, 200, 130], [0, 1, 0], [64, 40], 4096, [512, 128, 128], 64, torch.float16),
+    # long reductions over long segments: the streamed shrink's 128-row tiles
+    ("long_k8192", [300, 520, 280], [0, 1, 2], [64, 16, 40], 8192, [1024, 256], 64, torch.bfloat16),
+    ("long_k14336_f16", [260, 1, 400], [1, 2, 0], [32, 64, 0], 14336, [512], 64, torch.float16),
 ])
 def test_one_call_equals_two_calls(dev, name, lens, slots, ranks, in_dim, outs, r_max, dtype):
     x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, len(name))
@@ -68,6 +71,28 @@ def test_one_call_equals_two_calls(dev, name, lens, slots, ranks, in_dim, outs, 
     assert torch.equal(one.cpu(), two), f"{name}: one-call result differs from shrink + expand"
     assert not torch.isnan(one).any().item(), name
     assert_tol_f64(one.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), name)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_k_rows_not_16_byte_aligned(dev, dtype):
+    """A batch that plans the streamed shrink's 128-row tiles, with x rows
+    4 elements apart from 16-byte alignment: the register-staged kernels run
+    it on 64-row tiles instead, with the same results as aligned rows."""
+    lens, slots, ranks, in_dim, outs, r_max = [300, 1, 420], [0, 1, 2], [64, 16, 48], 8192, [768], 64
+    x, As, Bs, base, cols, meta_cpu, scal = case(dev, lens, slots, ranks, in_dim, outs, r_max, dtype, 77)
+    meta = make_meta(lens, slots, ranks, scal, dev, dtype)
+    Ad, Bd = [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    padded = torch.zeros(x.shape[0], in_dim + 4, dtype=dtype, device=dev)
+    padded[:, :in_dim] = x.to(dev)
+    xs = padded[:, :in_dim]
+    assert xs.stride(0) % 8 != 0
+    got = base.to(dev).clone()
+    apply_segments(xs, Ad, Bd, meta, got, cols, workspace=Workspace())
+    aligned = base.to(dev).clone()
+    apply_segments(x.to(dev), Ad, Bd, meta, aligned, cols, workspace=Workspace())
+    torch.cuda.synchronize()
+    assert_tol_f64(got.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), f"unaligned {dtype}")
+    assert_tol_f64(aligned.cpu(), apply_f64(x, As, Bs, meta_cpu, base, cols), f"aligned {dtype}")
 
 
 @pytest.mark.parametrize("name,lens,slots,ranks,in_dim,outs,r_max,dtype", [

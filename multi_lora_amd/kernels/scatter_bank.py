@@ -24,7 +24,7 @@ def scatter_stage(stage: torch.Tensor, slots: torch.Tensor, tables: dict, total:
     elements) into pool slots ``slots[:h]`` (int32 or int64, on the device).
 
     ``BLOCK`` is accepted for the reference's signature; the HIP kernel's
-    block is fixed at 8192 elements, and any positive value gives the same
+    block is fixed at 2048 elements, and any positive value gives the same
     result."""
     _require_gpu(stage, "stage")
     dev = stage.device

@@ -915,8 +915,10 @@ bool plan_shrink(int in_dim, int r_max, int n_slices, int rows, int bs, int max_
     // at the same six splits (12 splits, what the tile count below would
     // give for 128-row tiles, 32.4 us; 256-row tiles 31.2 us at 12 splits, a
     // fourth stage 31.5 us).  At K 4096 (prefill gate|up) they do not pay
-    // (22.5 vs 22.0 us), and batches of short segments keep 64 rows.
-    if (streamed && in_dim >= kLongKRows128 && rows >= 256LL * bs) {
+    // (22.5 vs 22.0 us), and batches of short segments keep 64 rows.  At
+    // most four A blocks a launch: with eight, three 128-row stages need
+    // 96 KB of LDS, one workgroup a CU.
+    if (streamed && in_dim >= kLongKRows128 && rows >= 256LL * bs && p.nbt <= 4) {
       p.bm = 128;
       p.m_tiles = cdiv(max_len > 0 ? max_len : 1, p.bm);
     }

@@ -94,6 +94,30 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert rc == 0
 
 
+def test_fused_rmsnorm_grouped_rejects_bad_arguments():
+    """mlora_rmsnorm_apply_grouped checks its own arguments before anything
+    is read or launched: placeholder addresses are never dereferenced."""
+    lib = _ffi.lib()
+    fake = _ffi.SegMeta(256, 512, 768, 1024, 1, 1, 4, _ffi.MLORA_BF16)
+    sl = _ffi.SliceArray()
+    bf = _ffi.MLORA_BF16
+    x, w, y, out, ws = 1 << 20, 2 << 20, 4 << 20, 8 << 20, 16 << 20
+
+    def call(x=x, xs=64, rows=4, k=64, w=w, y=y, ys=64, dt=bf):
+        return lib.mlora_rmsnorm_apply_grouped(x, xs, rows, k, w, 1e-5, y, ys, sl, 1, 16, out, 64,
+                                               ctypes.byref(fake), dt, ws, 1 << 20, 3, None)
+
+    assert call(dt=_ffi.MLORA_F32) == -2 and b"bf16 or fp16" in lib.mlora_last_error()
+    assert call(w=None) == -1 and b"null" in lib.mlora_last_error()
+    assert call(ys=32) == -1 and b"below in_dim" in lib.mlora_last_error()
+    assert call(x=x + 2) == -2 and b"aligned" in lib.mlora_last_error()       # x not 16-byte aligned
+    assert call(xs=68) == -2 and b"aligned" in lib.mlora_last_error()         # row stride not 8 elements
+    assert call(y=x + 256) == -1 and b"overlaps" in lib.mlora_last_error()    # y's rows run into x's
+    # y right after x's rows: no overlap, so the checks move on to the (empty) slices
+    assert call(y=x + 4 * 64 * 2) == -1 and b"slice 0: A or B is null" in lib.mlora_last_error()
+    assert call(rows=0) == 0                                                   # nothing to do
+
+
 def test_errors_map_to_reference_exception_types():
     with pytest.raises(ValueError):
         _ffi.lib()  # loads

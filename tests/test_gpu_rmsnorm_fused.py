@@ -242,3 +242,28 @@ def test_table_without_plan(dev):
     y1, o1 = fused(planned, x, w, 1e-5)
     y2, o2 = fused(bare, x, w, 1e-5, split=True)
     assert torch.equal(y1, y2) and torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes(dev, seed):
+    """Seeded random decode shapes through the fused call: dtype, pool size,
+    ranks (zero, partial, full), r_max, 1-4 slices of widths that are not tile
+    multiples, K, and a table of short segments; y bit-identical to the
+    RMSNorm kernel's, out held to float64 and to the fused rounding sequence."""
+    import random
+
+    rng = random.Random(1000 + seed)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    r_max = rng.choice([8, 16, 24, 32, 48, 64])
+    n_slices = rng.randint(1, 4 if r_max <= 32 else 3)
+    in_dim = 8 * rng.randint(16, 700)
+    outs = [8 * rng.randint(4, 200) for _ in range(n_slices)]
+    n_slots = rng.choice([3, 7, 16, 64, 300])
+    ranks = [rng.choice([0, r_max, max(1, r_max // 2), rng.randint(1, r_max)]) for _ in range(n_slots)]
+    ranks[rng.randrange(n_slots)] = r_max
+    lens = [rng.choice([1, 1, 1, 2, 5, 16]) for _ in range(rng.randint(1, 60))]
+    slots = [rng.randrange(n_slots) for _ in lens]
+    scal = [0.5 + (i % 4) * 0.25 for i in range(n_slots)]
+    wl = workload(f"random{seed}", dev, lens, slots, ranks, scal, in_dim, outs, r_max, 2000 + seed, dtype=dtype)
+    check(wl, scaled(wl.x, 3000 + seed), norm_weight(in_dim, dtype, dev, seed), 1e-5,
+          f"random {seed}: {dtype}, r_max {r_max}, {n_slices} slices, in {in_dim}, {len(lens)} segments")

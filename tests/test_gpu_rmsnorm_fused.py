@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from multi_lora_amd import synthetic
+from multi_lora_amd.synthetic import make_meta
 from multi_lora_amd.kernels.lora_ops import LinkedWorkspace, apply_grouped, rmsnorm_apply_grouped
 from multi_lora_amd.kernels.rmsnorm import rmsnorm_fwd
 from oracle.lora_ref import apply_f64, apply_kernel_numerics
@@ -267,3 +268,62 @@ def test_random_shapes(dev, seed):
     wl = workload(f"random{seed}", dev, lens, slots, ranks, scal, in_dim, outs, r_max, 2000 + seed, dtype=dtype)
     check(wl, scaled(wl.x, 3000 + seed), norm_weight(in_dim, dtype, dev, seed), 1e-5,
           f"random {seed}: {dtype}, r_max {r_max}, {n_slices} slices, in {in_dim}, {len(lens)} segments")
+
+
+@pytest.mark.parametrize("plan", ["packed", "device"])
+def test_graph_replays_follow_table_rewrites(dev, plan):
+    """The fused call captured once follows a segment table rewritten in
+    place between replays: through write_kernel_input_metadata (which
+    rebuilds the packed plan), or, for a table without a plan, through the
+    device plan build captured with the call."""
+    from multi_lora_amd import HipLoRABackend
+    from multi_lora_amd.batch_info import BatchLoRAInfo, fill_column, write_kernel_input_metadata
+    from tests.test_gpu_grouped import _packed_meta
+
+    wl = synthetic.decode_q(device=dev, tokens=64, in_dim=2048, out=2048, n_slots=16, n_adapters=8, rank=16, seed=17)
+    a, b = wl.a_stacks[0], wl.b_stacks[0]
+    x, w = scaled(wl.x, 17), norm_weight(2048, wl.x.dtype, dev, 17)
+    if plan == "packed":
+        meta = _packed_meta(dev, wl.seg_slots, wl.slot_ranks, wl.scalings)
+    else:
+        meta = make_meta(wl.seg_lens, wl.seg_slots, wl.slot_ranks, wl.scalings, dev, torch.bfloat16,
+                         with_plan=False)
+    be = HipLoRABackend()
+    be.set_kernel_input_metadata(meta)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    out = wl.clone_base()
+    with torch.cuda.stream(stream):  # the capture stream's workspace exists before capture
+        y0 = be.rmsnorm_apply_lora_multi(x, w, 1e-5, [a], [b], out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        y = be.rmsnorm_apply_lora_multi(x, w, 1e-5, [a], [b], out)
+    for _ in range(3):
+        out.copy_(wl.base)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager) and torch.equal(y, y0)
+
+    new_slots = [(s + 3) % 8 for s in wl.seg_slots]
+    if plan == "packed":
+        assert write_kernel_input_metadata(meta, BatchLoRAInfo(new_slots, wl.slot_ranks, wl.scalings), device=dev,
+                                           dtype=torch.bfloat16, seq_lens=[]) is meta
+    else:
+        fill_column(meta.weight_indices, new_slots, 0)
+    ref_meta = make_meta(wl.seg_lens, new_slots, wl.slot_ranks, wl.scalings, dev, torch.bfloat16)
+    be2 = HipLoRABackend()
+    be2.set_kernel_input_metadata(ref_meta)
+    eager2 = wl.clone_base()
+    be2.rmsnorm_apply_lora_multi(x, w, 1e-5, [a], [b], eager2)
+    torch.cuda.synchronize()
+    assert not torch.equal(eager2, eager)
+    for _ in range(3):
+        out.copy_(wl.base)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager2)
+    assert be.linked_workspace.counters()[1] == 0

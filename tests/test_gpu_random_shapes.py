@@ -6,7 +6,8 @@ limits of the path under test.  The decode path (segments of at most 16
 rows) must match float64 to the bf16/fp16 tolerance and the kernels'
 rounding sequence to one unit, with its two schedules bit-identical; the
 segment path (prefill and mixed batches) the same, with the one-call path
-bit-identical to shrink then expand.
+bit-identical to shrink then expand; long reductions over long segments
+(the streamed shrink's 128-row tiles) are drawn separately.
 """
 
 import random
@@ -92,3 +93,35 @@ def test_segment_path_random_shapes(dev, seed):
     torch.cuda.synchronize()
     assert torch.equal(one.cpu(), two), f"case {seed}: one call differs from shrink + expand"
     oracle_check(two, x, As, Bs, base, cols, meta, f"segment case {seed} {case[:5]}")
+
+
+def draw_long_k(rng: random.Random):
+    """Long reductions over long segments (K 8192..16384, at least 256 rows a
+    segment on average, at most four A blocks a launch): the streamed
+    shrink's 128-row tiles."""
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    r_max = rng.choice([16, 32, 64])
+    n_slices = 1 if r_max == 64 else rng.randint(1, 2)
+    in_dim = 8 * rng.randint(1024, 2048)
+    outs = [8 * rng.randint(16, 160) for _ in range(n_slices)]
+    n_slots = rng.choice([3, 7, 16])
+    ranks = [rng.choice([0, r_max, max(1, r_max // 2), rng.randint(1, r_max)]) for _ in range(n_slots)]
+    ranks[rng.randrange(n_slots)] = r_max
+    lens = [rng.choice([256, 300, 520, 700, 1, 3]) for _ in range(rng.randint(1, 4))]
+    if sum(lens) < 256 * len(lens):
+        lens[0] = 256 * len(lens)
+    slots = [rng.randrange(n_slots) for _ in lens]
+    return dtype, r_max, in_dim, outs, n_slots, ranks, lens, slots
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_segment_path_long_k_random_shapes(dev, seed):
+    case = draw_long_k(random.Random(5000 + seed))
+    x, As, Bs, base, cols, meta = build(dev, seed, *case)
+    xd, Ad, Bd = x.to(dev), [a.to(dev) for a in As], [b.to(dev) for b in Bs]
+    _, two = run_hip(xd, Ad, Bd, meta, base.to(dev), cols)
+    one = base.to(dev).clone()
+    apply_segments(xd, Ad, Bd, meta, one, cols, workspace=Workspace())
+    torch.cuda.synchronize()
+    assert torch.equal(one.cpu(), two), f"long-K case {seed}: one call differs from shrink + expand"
+    oracle_check(two, x, As, Bs, base, cols, meta, f"long-K case {seed} {case[:4]} lens {case[6]}")

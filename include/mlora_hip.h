@@ -261,7 +261,9 @@ int mlora_apply_grouped_static(const void* x, int64_t x_row_stride, int32_t num_
  * Against the unfused path (mlora_rmsnorm, then mlora_apply_grouped on y)
  * only the rounding of the MFMA inputs differs (round(x * w) scaled after
  * the sum instead of round(x * rstd * w)), within the tolerance of an fp32
- * reference.  The weight has the data dtype; y must not overlap x.
+ * reference.  The weight has the data dtype; y must not overlap x.  In
+ * fp16, every x * w must be finite in fp16 (the unfused path rounds
+ * x * rstd * w instead, which is smaller where mean(x^2) > 1).
  * Workspace: mlora_grouped_workspace_bytes (any mode), the same conditions
  * as mlora_apply_grouped (zero-filled before its first use, one stream);
  * a table without LoRA work still writes y.

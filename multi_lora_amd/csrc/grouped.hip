@@ -399,7 +399,10 @@ void set_short_tiles(const ExpandArgs& ea, int wn, GroupedArgs* ga) {
 template <class T, bool FUSED, int LBM, bool NT = false>
 hipError_t launch_mixed_t(const ExpandArgs& ea, GroupedArgs ga, int64_t long_rows, int long_segs,
                           int short_units, int cus, hipStream_t stream) {
-  // One K-step (r_max <= 32): short items of kMixedShortWn tiles (c5 gate|up
+  // Measurements below are on a mixed batch of 2 x 512 prompt rows and 64
+  // one-row segments over 35 rank-16 adapters (gate|up: 4096 -> 2 x 14336;
+  // q|k|v: 4096 -> [4096, 1024, 1024]).
+  // One K-step (r_max <= 32): short items of kMixedShortWn tiles (gate|up
   // 38.3 vs 39.3 us for the expand); two: one tile, as the registers allow.
   set_short_tiles(ea, ga.r_max <= T::KSTEP ? kMixedShortWn : 1, &ga);
   const int64_t lu = mixed_long_units<LBM>(long_rows, long_segs);
@@ -407,10 +410,10 @@ hipError_t launch_mixed_t(const ExpandArgs& ea, GroupedArgs ga, int64_t long_row
   const int long_units = static_cast<int>(lu);
   // Short items are latency-bound, long tiles bandwidth-bound.  Short items
   // that fit in one round of workgroup slots (four a CU) go first, and the
-  // long tiles fill the other slots (c5 q|k|v: 672 short items, 24.6 vs 25.0
+  // long tiles fill the other slots (q|k|v: 672 short items, 24.6 vs 25.0
   // us interleaved); more than that, and short-first would run rounds of
   // short items alone before the first long tile, so the kinds alternate
-  // (c5 gate|up: 3136 short items, 49.7 vs 51.3 us), and each short unit
+  // (gate|up: 3136 short items, 49.7 vs 51.3 us), and each short unit
   // takes two slots one after the other, which halves the workgroups that
   // wait on their table scans (48.2 vs 49.4 us; three slots a unit: 48.5).
   const int interleave = static_cast<int64_t>(short_units) * ga.n_tiles > 4 * static_cast<int64_t>(cus) ? 1 : 0;
@@ -432,10 +435,10 @@ hipError_t launch_mixed_dt(const ExpandArgs& ea, const GroupedArgs& ga, bool fus
                            int short_units, int cus, hipStream_t stream) {
   if (fused) return launch_mixed_t<T, true, kExpandLongBM>(ea, ga, long_rows, long_segs, short_units, cus, stream);
   // Streamed 64-row tiles when they give every CU at least its four
-  // workgroups (c5 gate|up: 1792 of them, 39.4 vs 40.7 us); fewer, larger
-  // tiles leave CUs idle (c5 q|k|v: 384, 13.0 vs 12.1 us).
+  // workgroups (the mixed batch's gate|up: 1792 of them, 39.4 vs 40.7 us);
+  // fewer, larger tiles leave CUs idle (its q|k|v: 384, 13.0 vs 12.1 us).
   // With at least kStreamNtTilesPerCu streamed tiles a CU, their output
-  // tiles are read and written with the non-temporal hint (c5 gate|up, 1792
+  // tiles are read and written with the non-temporal hint (gate|up, 1792
   // tiles: expand 38.4 -> 33.1 us).
   const int64_t streamed = mixed_long_units<kExpandStreamBM>(long_rows, long_segs) * ea.n_tiles;
   if (cus > 0 && streamed >= static_cast<int64_t>(kStreamNtTilesPerCu) * cus)
